@@ -1,0 +1,207 @@
+/*
+ * rnsmx: MI355X (gfx950) native RNS linear / fused-QKV backend, C ABI.
+ *
+ * The boundary replaces the pybind11 module `rns_llm._C` of Nek1tt/rns-llm
+ * (csrc/bindings.cpp:45-75) and the host-side constant cache of
+ * `CudaRNSBackend` (src/rns_llm/backends/cuda_backend.py:48-66, 137-166).
+ *
+ * Conventions
+ *   - Every pointer named *_dev is a device pointer on the current HIP device;
+ *     everything else is host memory.
+ *   - Every call that launches work is asynchronous on `stream` and never
+ *     synchronises, allocates, or frees memory.  Scratch memory is always
+ *     caller-owned (`workspace`, sized by the *_workspace_bytes queries).
+ *   - Return value: RNSMX_OK (0) on success, otherwise an RNSMX_E* code and a
+ *     thread-local message readable through rnsmx_last_error().
+ *   - Integer results are exact: bit-identical to A.astype(int64) @ B for any
+ *     input whose product fits the moduli's centered range.
+ */
+#ifndef RNSMX_H
+#define RNSMX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RNSMX_MAX_CHANNELS 10
+#define RNSMX_K_ALIGN 64 /* K padding of residue planes, bytes */
+
+enum rnsmx_status {
+  RNSMX_OK = 0,
+  RNSMX_EINVAL = 1,  /* bad argument: shape, dtype, pointer, moduli */
+  RNSMX_ERANGE = 2,  /* arithmetic range: product or accumulator bound */
+  RNSMX_ELAUNCH = 3, /* HIP runtime reported an error */
+  RNSMX_ESPACE = 4   /* caller-provided workspace too small */
+};
+
+enum rnsmx_dtype {
+  RNSMX_INT8 = 0,
+  RNSMX_INT16 = 1,
+  RNSMX_INT32 = 2,
+  RNSMX_INT64 = 3,
+  RNSMX_FLOAT32 = 4,
+  RNSMX_FLOAT16 = 5,
+  RNSMX_BFLOAT16 = 6
+};
+
+/*
+ * Moduli set plus every constant the kernels need, built on the host and
+ * passed to kernels by value (kernel-argument memory, read through scalar
+ * loads).  Replaces `_host_constants` / `_DeviceConstants`
+ * (cuda_backend.py:48-66): Barrett reciprocals, Garner inverses and the
+ * modulus product.
+ */
+typedef struct rnsmx_moduli {
+  int32_t channels;
+  int32_t moduli[RNSMX_MAX_CHANNELS];
+  uint32_t magic[RNSMX_MAX_CHANNELS];  /* floor(2^32 / m_i)                   */
+  uint32_t c31[RNSMX_MAX_CHANNELS];    /* 2^31 mod m_i                        */
+  uint32_t qinv[RNSMX_MAX_CHANNELS];   /* (prod_{j<i} m_j)^-1 mod m_i         */
+  uint32_t ucoef[RNSMX_MAX_CHANNELS][RNSMX_MAX_CHANNELS];
+                                       /* [j][i], j<i: -(prod_{l<j} m_l)*qinv_i mod m_i */
+  int64_t prefix[RNSMX_MAX_CHANNELS + 1]; /* prod_{j<i} m_j, i = 0..channels  */
+} rnsmx_moduli_t;
+
+/* Thread-local text of the last error (empty string when none). */
+const char *rnsmx_last_error(void);
+
+/* ABI version; bumped on any signature or struct change. */
+int32_t rnsmx_abi_version(void);
+
+/*
+ * Host only.  Validates the set (each m in [2,255], pairwise coprime,
+ * product < 2^63) and fills `out`.
+ * Replaces reference.py:11-23 (validate_moduli), reference.py:43-67
+ * (crt_constants, garner_pairwise_inverses) and cuda_backend.py:48-55.
+ */
+int32_t rnsmx_moduli_init(const int32_t *moduli, int32_t channels,
+                          rnsmx_moduli_t *out);
+
+/*
+ * Host only.  Fills `lut` (int16 [channels][4][256]) with b*256^p mod m_c:
+ * the compact byte-decomposition table of reference.py:70-88.
+ */
+int32_t rnsmx_compact_lut(const rnsmx_moduli_t *mods, int16_t *lut);
+
+/*
+ * Centered residue encode: values [rows][cols] (RNSMX_INT8/16/32,
+ * contiguous) -> out_dev [channels][rows][out_ld] int8 with
+ * r = v mod m in [-floor(m/2), floor(m/2)], and zero bytes in columns
+ * [cols, out_ld).  out_ld >= cols.  When row_l1_dev is non-null it receives
+ * int64 sum_k |v[row][k]| per row; when absmax_dev is non-null the maximum
+ * |v| is folded into it with an atomic max (the caller zeroes it first).
+ * Replaces _C.encode_centered (csrc/rns_cuda.cu:584-626, kernel 98-124);
+ * the plain reference form is rows=1, cols=numel, out_ld=numel.
+ */
+int32_t rnsmx_encode_centered(const void *values_dev, int32_t dtype,
+                              int64_t rows, int64_t cols, int64_t out_ld,
+                              const rnsmx_moduli_t *mods, int8_t *out_dev,
+                              int64_t *row_l1_dev, int32_t *absmax_dev,
+                              void *stream);
+
+/* Bytes of workspace rnsmx_matmul_centered_fused_out needs. */
+int64_t rnsmx_fused_workspace_bytes(int64_t m, int64_t k, int64_t n,
+                                    int32_t channels);
+
+/*
+ * Drop-in fused op: a_dev [R][M][K] and b_dev [R][K][N] centered int8
+ * residue planes (contiguous, the reference layout) -> out_dev [M][N] int64.
+ * Per-channel int8 GEMM on MFMA, modular reduction (Barrett, or the byte
+ * LUT `lut_dev` [R][4][256] for channels < lut_channels), Garner mixed
+ * radix and signed correction, all in one GEMM epilogue.  No K%4 / N%4
+ * restriction.  `workspace_dev` holds the repacked operands.
+ * Replaces _C.matmul_centered_fused_out (csrc/rns_cuda.cu:887-980: cuBLAS
+ * site 478-523 + fused_reduce_garner_kernel 442-476).
+ */
+int32_t rnsmx_matmul_centered_fused_out(
+    const int8_t *a_dev, const int8_t *b_dev, int32_t m, int32_t k, int32_t n,
+    const rnsmx_moduli_t *mods, const int16_t *lut_dev, int32_t lut_channels,
+    void *workspace_dev, int64_t workspace_bytes, int64_t *out_dev,
+    void *stream);
+
+/*
+ * Weight preparation: b_nk_dev [N][K] (int8/16/32, i.e. the quantized
+ * nn.Linear weight, or B transposed) -> packed_dev [R][N][kp] centered
+ * residues, kp = round_up(K, RNSMX_K_ALIGN), zero padded.  absmax_dev
+ * (nullable, zeroed by the caller) receives max |b| for the adaptive bound.
+ * Replaces CudaRNSBackend.prepare_weight (cuda_backend.py:464-487), whose
+ * storage is [R][K][N]; the K-contiguous layout feeds both MFMA operands
+ * with 16-byte loads.
+ */
+int32_t rnsmx_prepare_weight(const void *b_nk_dev, int32_t dtype, int32_t n,
+                             int32_t k, const rnsmx_moduli_t *mods,
+                             int8_t *packed_dev, int32_t *absmax_dev,
+                             void *stream);
+
+/* Bytes of workspace rnsmx_matmul_prepared_fused needs for M rows. */
+int64_t rnsmx_prepared_workspace_bytes(int64_t m, int64_t k,
+                                       int32_t channels);
+
+/* Epilogue selector of rnsmx_matmul_prepared_fused. */
+typedef struct rnsmx_epilogue {
+  int32_t out_dtype;            /* RNSMX_INT64 (exact) or FLOAT32/16/BFLOAT16 */
+  const float *a_scale_dev;     /* [1] activation scale (float outputs)      */
+  const float *w_scale_dev;     /* [N] per-output-channel scale              */
+  const float *bias_dev;        /* [N] or null                               */
+} rnsmx_epilogue_t;
+
+/* Adaptive channel prefix, decided on the device. */
+typedef struct rnsmx_adaptive {
+  int32_t min_channels;         /* 0 = off (all channels)                    */
+  const int32_t *w_absmax_dev;  /* [1] max |B| from rnsmx_prepare_weight     */
+  int64_t *meta_dev;            /* [4] out: channels, bound, capacity, overflow */
+} rnsmx_adaptive_t;
+
+/*
+ * Hot path: a_dev [M][K] (int8/16/32 activations) x prepared weight
+ * (packed_dev from rnsmx_prepare_weight, n x k) -> out_dev [M][N].
+ * Encodes activations (fused row-L1 bound), runs the per-channel MFMA GEMM
+ * with the reduction + Garner (+ optional dequant) epilogue.  With
+ * adaptive.min_channels > 0 the GEMM picks, on the device and without any
+ * host synchronisation, the shortest moduli prefix c >= min_channels with
+ * 2 * max_i(sum_k |a_ik|) * max|B| < prod(prefix); if none fits it uses the
+ * full set and sets meta[3] = 1.
+ * Replaces matmul_prepared_fused (cuda_backend.py:514-539) and
+ * matmul_prepared_adaptive_fused (cuda_backend.py:577-622, whose selector
+ * synchronises at :591).
+ */
+int32_t rnsmx_matmul_prepared_fused(
+    const void *a_dev, int32_t a_dtype, int32_t m, int32_t k, int32_t n,
+    const int8_t *packed_dev, const rnsmx_moduli_t *mods,
+    const int16_t *lut_dev, int32_t lut_channels,
+    const rnsmx_adaptive_t *adaptive, const rnsmx_epilogue_t *epilogue,
+    void *workspace_dev, int64_t workspace_bytes, void *out_dev,
+    void *stream);
+
+/*
+ * GEMM stage of rnsmx_matmul_prepared_fused on activations already encoded
+ * by rnsmx_encode_centered into a_res_dev [R][M][a_ld] (a_ld a multiple of
+ * RNSMX_K_ALIGN, zero bytes in [K, a_ld)), against a prepared weight.  Same
+ * epilogue options, no adaptive prefix (all channels).  Lets a caller
+ * encode once and reuse the residues (e.g. one activation against several
+ * weights) and times the GEMM kernel on its own.
+ * Replaces the cuBLAS + fused_reduce_garner half of _C.matmul_centered_fused_out
+ * (csrc/rns_cuda.cu:949-976) for a prepared weight.
+ */
+int32_t rnsmx_matmul_residues_prepared(
+    const int8_t *a_res_dev, int64_t a_ld, int32_t m, int32_t k, int32_t n,
+    const int8_t *packed_dev, const rnsmx_moduli_t *mods,
+    const int16_t *lut_dev, int32_t lut_channels,
+    const rnsmx_epilogue_t *epilogue, void *out_dev, void *stream);
+
+/*
+ * Garner reconstruction of centered residues [R][count] int8 -> int64.
+ * Replaces _C.decode_garner (csrc/rns_cuda.cu:818-885, kernel 416-440).
+ */
+int32_t rnsmx_decode_garner(const int8_t *residues_dev, int64_t count,
+                            const rnsmx_moduli_t *mods, int64_t *out_dev,
+                            void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RNSMX_H */

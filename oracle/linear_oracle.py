@@ -1,0 +1,69 @@
+"""CPU oracle for the float chain around the integer core of ``RNSLinear``.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/rns_oracle.py``).
+
+Restates ``src/rns_llm/layers/rns_linear.py`` of the reference op by op on the
+CPU with torch float32 tensors, so the same IEEE operations run as on the GPU:
+
+  * ``_symmetric_scale`` (``rns_linear.py:154-159``): amax(|v|) / 127,
+    clamped below at float32 eps; per tensor for activations, per output
+    channel (dim=1) for weights;
+  * ``_quantize`` (``:161-166``): round-half-to-even(v / s) clamped to
+    +-quant_max, cast to int8 (int16 for 12/16-bit);
+  * weight preparation (``:183-185``): B = quantized(W).T, contiguous;
+  * forward (``:238-275``): int64 result -> float32, then ``* s_a``, then
+    ``* s_w[None, :]``, then ``+ bias``, then cast to the input dtype.
+
+The integer product is the exact int64 matmul, which every RNS backend must
+reproduce bit for bit.  Pinned by tests/test_oracle.py against hand-computed
+float32 values and against ``torch.nn.functional.linear`` within quantization
+error bounds.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+
+def quant_max(bits: int) -> int:
+    return (1 << (bits - 1)) - 1
+
+
+def symmetric_scale(values: torch.Tensor, bits: int = 8, dim=None) -> torch.Tensor:
+    amax = values.detach().abs().amax(dim=dim, keepdim=True)
+    return torch.clamp(amax / float(quant_max(bits)), min=torch.finfo(torch.float32).eps)
+
+
+def quantize(values: torch.Tensor, scale: torch.Tensor, bits: int = 8) -> torch.Tensor:
+    q = quant_max(bits)
+    dtype = torch.int8 if bits == 8 else torch.int16
+    return torch.clamp(torch.round(values / scale), -q, q).to(dtype)
+
+
+def prepare_weight(weight: torch.Tensor, bits: int = 8):
+    """(B [K, N] int, per-output-channel scale [N] f32)."""
+    w = weight.detach().float().cpu()
+    scale = symmetric_scale(w, bits, dim=1)
+    b = quantize(w, scale, bits).transpose(0, 1).contiguous()
+    return b, scale.squeeze(1)
+
+
+def quantize_activations(inputs: torch.Tensor, in_features: int, bits: int = 8):
+    """(A [M, K] int, per-tensor scale [1, 1] f32)."""
+    flat = inputs.detach().cpu().reshape(-1, in_features).float().contiguous()
+    scale = symmetric_scale(flat, bits)
+    return quantize(flat, scale, bits).contiguous(), scale
+
+
+def linear_forward(inputs: torch.Tensor, weight: torch.Tensor, bias, bits: int = 8):
+    """Full rns-mode ``RNSLinear.forward`` on the CPU; returns (output, int64
+    integer product)."""
+    out_features, in_features = weight.shape
+    b, w_scale = prepare_weight(weight, bits)
+    a, a_scale = quantize_activations(inputs, in_features, bits)
+    integer = torch.from_numpy(a.numpy().astype(np.int64) @ b.numpy().astype(np.int64))
+    out = integer.float() * a_scale * w_scale.unsqueeze(0)
+    if bias is not None:
+        out = out + bias.detach().cpu().float()
+    shape = tuple(inputs.shape[:-1]) + (out_features,)
+    return out.reshape(shape).to(inputs.dtype), integer

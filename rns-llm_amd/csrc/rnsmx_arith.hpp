@@ -1,0 +1,82 @@
+// Device-side modular arithmetic for the rnsmx kernels.
+//
+// Reduction follows Barrett (1986): for a 32-bit x and magic = floor(2^32/m),
+// q = mulhi(x, magic) is floor(x/m) or floor(x/m) - 1, so x - q*m lies in
+// [0, 2m) and one conditional subtraction finishes.  Signed 32-bit values are
+// biased by 2^31 (an exact XOR of the sign bit) so every int32, including
+// INT32_MIN, reduces without a magnitude/negate step; the bias is removed
+// with the precomputed 2^31 mod m.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <type_traits>
+#include <utility>
+
+#include "rnsmx.h"
+
+namespace rnsmx {
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [0, N).
+template <int N, typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F &&f,
+                                                std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl<N>(static_cast<F &&>(f), std::make_integer_sequence<int, N>{});
+}
+
+// x mod m for any 32-bit x.
+__device__ __forceinline__ uint32_t mod_u32(uint32_t x, uint32_t m, uint32_t magic) {
+  const uint32_t q = __umulhi(x, magic);
+  const uint32_t r = x - q * m;
+  return r >= m ? r - m : r;
+}
+
+// Canonical residue in [0, m) of a signed 32-bit value.
+__device__ __forceinline__ uint32_t canon_i32(int32_t v, uint32_t m, uint32_t magic,
+                                              uint32_t c31) {
+  const uint32_t r = mod_u32(static_cast<uint32_t>(v) ^ 0x80000000u, m, magic);
+  return r >= c31 ? r - c31 : r + m - c31;
+}
+
+// Same residue through the compact byte table of one channel (int16 [4][256],
+// entry [p][b] = b * 256^p mod m), applied to the biased value.
+__device__ __forceinline__ uint32_t canon_i32_lut(int32_t v, const int16_t *__restrict__ t,
+                                                  uint32_t m, uint32_t c31) {
+  const uint32_t u = static_cast<uint32_t>(v) ^ 0x80000000u;
+  uint32_t s = static_cast<uint32_t>(t[u & 255u]) +
+               static_cast<uint32_t>(t[256 + ((u >> 8) & 255u)]) +
+               static_cast<uint32_t>(t[512 + ((u >> 16) & 255u)]) +
+               static_cast<uint32_t>(t[768 + (u >> 24)]);
+  // s < 4m
+  if (s >= 2 * m) s -= 2 * m;
+  if (s >= m) s -= m;
+  return s >= c31 ? s - c31 : s + m - c31;
+}
+
+// Centered residue in [-floor(m/2), floor(m/2)] of a signed 32-bit value.
+__device__ __forceinline__ int32_t centered_i32(int32_t v, uint32_t m, uint32_t magic,
+                                                uint32_t c31) {
+  const uint32_t r = canon_i32(v, m, magic, c31);
+  return r > (m >> 1) ? static_cast<int32_t>(r) - static_cast<int32_t>(m)
+                      : static_cast<int32_t>(r);
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int t) {
+  return (w >> (8 * t)) & 0xFFu;
+}
+
+// Round-to-nearest-even float -> bfloat16 bits (finite inputs; NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu))
+    return static_cast<uint16_t>((u >> 16) | 0x40u);
+  const uint32_t lsb = (u >> 16) & 1u;
+  return static_cast<uint16_t>((u + 0x7FFFu + lsb) >> 16);
+}
+
+}  // namespace rnsmx

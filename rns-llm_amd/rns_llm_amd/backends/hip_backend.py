@@ -1,0 +1,752 @@
+"""HIP / gfx950 implementation of the reference's RNS backend contract.
+
+``HipRNSBackend`` implements the method contract of the reference's
+``CudaRNSBackend`` (``src/rns_llm/backends/cuda_backend.py:110-799``) under its
+own name: same method names, keyword arguments, return values, aliasing of
+workspace outputs, stats counters and exception types.  Every device
+computation goes through ``librnsmx.so`` (``include/rnsmx.h``); there is no
+host or torch fallback for the integer path.
+
+Deliberate deviations (each keeps results bit-identical):
+  * prepared weights are stored K-contiguous ``[R, N, kp]`` (``packed``); the
+    public ``residues`` field is the reference-shaped ``[R, K, N]`` view of it;
+  * ``kernel`` names are ``"mfma"``; ``RNSLinear`` asks ``supports_fused`` instead
+    of comparing the kernel string with ``"cublas"``;
+  * the workspace's ``accumulators`` tensor is byte scratch sized by the
+    library (the fused kernel has no int32 round trip);
+  * ``matmul_prepared_adaptive_fused`` selects the channel prefix on the
+    device; its metadata is a lazy mapping that synchronises (and raises
+    ``OverflowError`` when no prefix fits) only when read.
+"""
+from __future__ import annotations
+
+import ctypes
+from collections import Counter
+from collections.abc import Mapping
+from dataclasses import dataclass, field
+from math import prod
+from typing import Iterable, Sequence
+
+import torch
+
+from .. import _native
+from ..moduli import (
+    centered_accumulator_bound,
+    minimal_prefix_channels,
+    safe_l1_dot_bound,
+    validate_moduli,
+)
+
+KERNEL_NAME = "mfma"
+
+
+@dataclass
+class _DeviceConstants:
+    moduli: torch.Tensor          # int32 [R] on the device
+    compact_lut: torch.Tensor     # int16 [R, 4, 256] on the device
+    modulus_product: int
+    native: _native.Moduli        # rnsmx_moduli_t (kernel-argument constants)
+    native_ref: object            # ctypes.byref(native), built once
+
+
+@dataclass(frozen=True)
+class PreparedRNSWeight:
+    """Weight encoded once into centered residue planes.
+
+    ``residues`` has the reference shape ``[R, K, N]`` (a view); ``packed`` is
+    the K-contiguous ``[R, N, kp]`` storage the kernels read.
+    """
+
+    residues: torch.Tensor
+    moduli: tuple[int, ...]
+    k: int
+    n: int
+    kernel: str
+    packed: torch.Tensor | None = None
+    absmax: torch.Tensor | None = None  # int32 [1], max |B| on the device
+
+
+@dataclass
+class RNSWorkspace:
+    """Reusable memory for one (rows, channels, stream) of one layer."""
+
+    accumulators: torch.Tensor  # uint8 scratch for the library
+    output: torch.Tensor        # [M, N] int64
+    channels: int
+    m: int
+    n: int
+
+
+class PreparedAdaptiveRNSWeight:
+    """One encoded weight with every safe prefix variant (views, no copies)."""
+
+    def __init__(self, variants: dict, full_moduli: tuple[int, ...],
+                 absmax: torch.Tensor, min_channels: int):
+        self.variants = variants
+        self.full_moduli = full_moduli
+        self.absmax = absmax
+        self.min_channels = min_channels
+        self._max_abs_weight: int | None = None
+
+    @property
+    def max_abs_weight(self) -> int:
+        """max |B| as a Python int (synchronises once, on first read)."""
+        if self._max_abs_weight is None:
+            self._max_abs_weight = int(self.absmax.item())
+        return self._max_abs_weight
+
+
+@dataclass
+class RNSRequestBatchWorkspace:
+    """Preallocated activation buffer plus fused GEMM workspace."""
+
+    activations: torch.Tensor
+    fused: RNSWorkspace
+    rows_per_request: tuple[int, ...]
+    k: int
+
+
+class AdaptiveMetadata(Mapping):
+    """``{"channels", "bound", "capacity"}`` of one adaptive call, read lazily
+    from the device.  Reading it synchronises with the stream; when the
+    device found that even the full moduli set cannot hold the bound it
+    raises ``OverflowError`` like ``minimal_prefix_channels``."""
+
+    _KEYS = ("channels", "bound", "capacity")
+
+    def __init__(self, meta: torch.Tensor, full_moduli: tuple[int, ...]):
+        self.device_tensor = meta
+        self._full = full_moduli
+        self._host: dict | None = None
+
+    def _load(self) -> dict:
+        if self._host is None:
+            channels, bound, capacity, overflow = (int(v) for v in self.device_tensor.tolist())
+            if overflow:
+                raise OverflowError(
+                    f"full moduli set cannot represent bound {bound}; capacity={capacity}")
+            self._host = {"channels": channels, "bound": bound, "capacity": capacity}
+        return self._host
+
+    @property
+    def overflow(self) -> bool:
+        return bool(int(self.device_tensor[3].item()))
+
+    def __getitem__(self, key):
+        return self._load()[key]
+
+    def __iter__(self):
+        return iter(self._KEYS)
+
+    def __len__(self):
+        return len(self._KEYS)
+
+    def __repr__(self):
+        return f"AdaptiveMetadata({self._host if self._host is not None else '<on device>'})"
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+class HipRNSBackend:
+    """RNS backend on MI355X: one MFMA GEMM launch for all residue channels
+    with the modular reduction, Garner reconstruction and signed correction
+    in its epilogue."""
+
+    name = "hip-rns-mfma"
+
+    def __init__(self) -> None:
+        if not torch.cuda.is_available():
+            raise RuntimeError("no GPU is visible to this PyTorch (ROCm) installation")
+        self._lib = _native.lib()
+        self._device_cache: dict[tuple[int, tuple[int, ...]], _DeviceConstants] = {}
+        self._stats: Counter[str] = Counter()
+
+    # ------------------------------------------------------------------
+    # Stats (cuda_backend.py:129-135)
+    # ------------------------------------------------------------------
+    def reset_stats(self) -> None:
+        self._stats.clear()
+
+    def stats_snapshot(self) -> dict[str, int]:
+        return dict(self._stats)
+
+    # ------------------------------------------------------------------
+    # Constants (cuda_backend.py:137-166)
+    # ------------------------------------------------------------------
+    def _constants(self, device: torch.device, moduli: Iterable[int]) -> _DeviceConstants:
+        mods = tuple(moduli)
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        key = (index, mods)
+        cached = self._device_cache.get(key)
+        if cached is not None:
+            return cached
+        mods = validate_moduli(mods)
+        if prod(mods) > 2**63 - 1:
+            raise OverflowError("moduli product must fit signed int64")
+        native = _native.make_moduli(mods)
+        lut_host = torch.empty((len(mods), 4, 256), dtype=torch.int16)
+        _native.check(self._lib.rnsmx_compact_lut(ctypes.byref(native), lut_host.data_ptr()))
+        dev = torch.device("cuda", index)
+        cached = _DeviceConstants(
+            moduli=torch.tensor(mods, dtype=torch.int32, device=dev),
+            compact_lut=lut_host.to(dev),
+            modulus_product=prod(mods),
+            native=native,
+            native_ref=ctypes.byref(native),
+        )
+        self._device_cache[key] = cached
+        return cached
+
+    @staticmethod
+    def _validate_matrix(matrix: torch.Tensor, name: str, ndim: int) -> None:
+        if not matrix.is_cuda:
+            raise ValueError(f"{name} must be a GPU tensor")
+        if matrix.ndim != ndim:
+            raise ValueError(f"{name} must have rank {ndim}")
+        if not matrix.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+
+    # ------------------------------------------------------------------
+    # Encoding (cuda_backend.py:188-200)
+    # ------------------------------------------------------------------
+    def encode_centered(self, values: torch.Tensor, moduli: Iterable[int]) -> torch.Tensor:
+        """Encode int8/int16/int32 values as signed-int8 centered residues
+        ``[R, *values.shape]``."""
+        self._validate_matrix(values, "values", values.ndim)
+        if values.dtype not in (torch.int8, torch.int16, torch.int32):
+            raise ValueError("centered encoder supports int8, int16 and int32")
+        consts = self._constants(values.device, moduli)
+        self._stats["encode_centered_calls"] += 1
+        self._stats["encode_centered_values"] += int(values.numel())
+        r = len(consts.moduli)
+        out = torch.empty((r,) + tuple(values.shape), dtype=torch.int8, device=values.device)
+        n = int(values.numel())
+        if n == 0:
+            return out
+        src = _aligned(values)
+        _native.check(self._lib.rnsmx_encode_centered(
+            src.data_ptr(), _native.dtype_code(values.dtype), 1, n, n, consts.native_ref,
+            out.data_ptr(), None, None, _stream_handle(values.device)))
+        return out
+
+    # ------------------------------------------------------------------
+    # Bounds and selection (cuda_backend.py:205-261)
+    # ------------------------------------------------------------------
+    @staticmethod
+    def accumulator_bound(k: int, moduli: Iterable[int]) -> int:
+        mods = validate_moduli(moduli)
+        return int(k) * (max(mods) - 1) ** 2
+
+    @staticmethod
+    def centered_accumulator_bound(k: int, moduli: Iterable[int]) -> int:
+        return centered_accumulator_bound(k, moduli)
+
+    def mfma_compatible(self, *, k: int, n: int, moduli: Iterable[int],
+                        device: torch.device) -> bool:
+        """The MFMA path takes any K and N (no multiple-of-4 rule) for 2..10
+        channels whose int32 accumulators cannot overflow."""
+        del n, device
+        mods = validate_moduli(moduli)
+        return (2 <= len(mods) <= _native.MAX_CHANNELS
+                and self.centered_accumulator_bound(k, mods) <= 0x7FFFFFFF)
+
+    def select_centered_kernel(self, *, k: int, n: int, moduli: Iterable[int],
+                               requested: str = "auto", device: torch.device) -> str:
+        if requested not in ("auto", KERNEL_NAME):
+            raise ValueError(f"unknown kernel {requested!r}; this backend provides 'mfma'")
+        if not self.mfma_compatible(k=k, n=n, moduli=moduli, device=device):
+            raise ValueError("MFMA path constraints are not satisfied "
+                             "(2..10 channels, K * max(floor(m/2))^2 < 2^31)")
+        return KERNEL_NAME
+
+    @staticmethod
+    def supports_fused(prepared) -> bool:
+        return getattr(prepared, "packed", None) is not None
+
+    # ------------------------------------------------------------------
+    # Workspaces (cuda_backend.py:366-396)
+    # ------------------------------------------------------------------
+    def create_workspace(self, *, device: torch.device, channels: int, m: int, n: int,
+                         k: int | None = None) -> RNSWorkspace:
+        scratch_bytes = 0
+        if k is not None:
+            scratch_bytes = int(self._lib.rnsmx_prepared_workspace_bytes(m, k, channels))
+        return RNSWorkspace(
+            accumulators=torch.empty((max(scratch_bytes, 0),), dtype=torch.uint8, device=device),
+            output=torch.empty((m, n), dtype=torch.int64, device=device),
+            channels=channels,
+            m=m,
+            n=n,
+        )
+
+    @staticmethod
+    def _check_workspace(workspace: RNSWorkspace, *, channels: int, m: int, n: int,
+                         device: torch.device) -> None:
+        if (workspace.channels, workspace.m, workspace.n) != (channels, m, n):
+            raise ValueError("workspace shape does not match operation")
+        if workspace.accumulators.device != device or workspace.output.device != device:
+            raise ValueError("workspace device does not match operation")
+
+    @staticmethod
+    def _scratch(workspace: RNSWorkspace, nbytes: int) -> torch.Tensor:
+        if nbytes < 0:
+            raise ValueError("bad workspace size")
+        if workspace.accumulators.numel() < nbytes:
+            workspace.accumulators = torch.empty(
+                (nbytes,), dtype=torch.uint8, device=workspace.output.device)
+        return workspace.accumulators
+
+    # ------------------------------------------------------------------
+    # Fused ops
+    # ------------------------------------------------------------------
+    def matmul_centered_fused(self, a_residues: torch.Tensor, b_residues: torch.Tensor,
+                              moduli: Iterable[int], *, lut_channels: int = 0,
+                              workspace: RNSWorkspace | None = None) -> torch.Tensor:
+        """Residue planes a [R, M, K] and b [R, K, N] -> exact int64 [M, N]
+        (``cuda_backend.py:398-459``).  Returns ``workspace.output``."""
+        self._validate_matrix(a_residues, "a_residues", 3)
+        self._validate_matrix(b_residues, "b_residues", 3)
+        if a_residues.dtype != torch.int8 or b_residues.dtype != torch.int8:
+            raise ValueError("fused path expects centered int8 residue planes")
+        if a_residues.device != b_residues.device:
+            raise ValueError("inputs must share device")
+        if (a_residues.shape[0] != b_residues.shape[0]
+                or a_residues.shape[2] != b_residues.shape[1]):
+            raise ValueError("R/K dimensions do not match")
+        if lut_channels not in (0, 1, 2):
+            raise ValueError("lut_channels must be 0, 1 or 2")
+        mods = validate_moduli(moduli)
+        channels, m, k = map(int, a_residues.shape)
+        n = int(b_residues.shape[2])
+        if channels != len(mods):
+            raise ValueError("moduli count does not match channels")
+        if not self.mfma_compatible(k=k, n=n, moduli=mods, device=a_residues.device):
+            raise ValueError("fused path requires an MFMA-compatible shape (2..10 channels, "
+                             "int32-safe K)")
+        device = a_residues.device
+        if workspace is None:
+            workspace = self.create_workspace(device=device, channels=channels, m=m, n=n)
+        self._check_workspace(workspace, channels=channels, m=m, n=n, device=device)
+        consts = self._constants(device, mods)
+        scratch = self._scratch(
+            workspace, int(self._lib.rnsmx_fused_workspace_bytes(m, k, n, channels)))
+        self._stats["fused_gemm_calls"] += 1
+        self._stats[f"fused_gemm_channels_{channels}"] += 1
+        _native.check(self._lib.rnsmx_matmul_centered_fused_out(
+            _aligned(a_residues).data_ptr(), b_residues.data_ptr(), m, k, n, consts.native_ref,
+            consts.compact_lut.data_ptr(), lut_channels, scratch.data_ptr(), scratch.numel(),
+            workspace.output.data_ptr(), _stream_handle(device)))
+        return workspace.output
+
+    def matmul_centered_residues(self, a_residues: torch.Tensor, b_residues: torch.Tensor,
+                                 moduli: Iterable[int], *, kernel: str = "auto") -> torch.Tensor:
+        """Residue-domain product [R, M, N] int8 (centered), as
+        ``cuda_backend.py:300-344`` returns.  The exact integer product has
+        the same residue in every channel as the per-channel modular GEMM
+        (CRT reconstruction preserves residues), so this is the fused product
+        re-encoded."""
+        self._validate_matrix(a_residues, "a_residues", 3)
+        self._validate_matrix(b_residues, "b_residues", 3)
+        if a_residues.dtype != torch.int8 or b_residues.dtype != torch.int8:
+            raise ValueError("centered residue matrices must use torch.int8")
+        if a_residues.device != b_residues.device:
+            raise ValueError("a_residues and b_residues must share a device")
+        if a_residues.shape[0] != b_residues.shape[0]:
+            raise ValueError("channel counts do not match")
+        if a_residues.shape[2] != b_residues.shape[1]:
+            raise ValueError("K dimensions do not match")
+        mods = validate_moduli(moduli)
+        if len(mods) != a_residues.shape[0]:
+            raise ValueError("moduli count does not match residue channels")
+        self.select_centered_kernel(k=int(a_residues.shape[2]), n=int(b_residues.shape[2]),
+                                    moduli=mods, requested=kernel, device=a_residues.device)
+        exact = self.matmul_centered_fused(a_residues, b_residues, mods).clone()
+        return self._encode_int64_centered(exact, mods)
+
+    def _encode_int64_centered(self, values: torch.Tensor, mods: tuple[int, ...]) -> torch.Tensor:
+        # int64 values are residue-reduced with torch integer ops (exact).
+        mt = self._constants(values.device, mods).moduli.to(torch.int64).view(
+            (-1,) + (1,) * values.ndim)
+        r = torch.remainder(values.unsqueeze(0), mt)
+        return torch.where(r > mt // 2, r - mt, r).to(torch.int8)
+
+    def decode_garner(self, residues: torch.Tensor, moduli: Iterable[int]) -> torch.Tensor:
+        """Centered int8 residues [R, *] -> int64 [*] (``cuda_backend.py:349-364``)."""
+        self._validate_matrix(residues, "residues", residues.ndim)
+        if residues.dtype != torch.int8:
+            raise ValueError("Garner decoder expects centered int8 residues")
+        consts = self._constants(residues.device, moduli)
+        if residues.shape[0] != len(consts.moduli):
+            raise ValueError("residue channel count does not match moduli")
+        out = torch.empty(tuple(residues.shape[1:]), dtype=torch.int64, device=residues.device)
+        count = int(out.numel())
+        if count:
+            _native.check(self._lib.rnsmx_decode_garner(
+                residues.data_ptr(), count, consts.native_ref, out.data_ptr(),
+                _stream_handle(residues.device)))
+        return out
+
+    def decode(self, residues: torch.Tensor, moduli: Iterable[int], *,
+               signed: bool = True) -> torch.Tensor:
+        """CRT decode with torch integer ops (the reference's legacy decoder,
+        ``cuda_backend.py:706-731``)."""
+        self._validate_matrix(residues, "residues", residues.ndim)
+        if residues.dtype not in (torch.uint8, torch.int8):
+            raise ValueError("decoder expects uint8 canonical or int8 centered residues")
+        mods = validate_moduli(moduli)
+        big_p = prod(mods)
+        if big_p > (2**63 - 1) // 256:
+            raise OverflowError("CRT product is too large for the int64 torch decoder")
+        result = torch.zeros(residues.shape[1:], dtype=torch.int64, device=residues.device)
+        for c, m in enumerate(mods):
+            cof = big_p // m
+            basis = (cof * pow(cof % m, -1, m)) % big_p
+            canon = torch.remainder(residues[c].to(torch.int64), m)
+            # canon * basis < 256 * P fits int64 by the check above
+            result = torch.remainder(result + canon * basis, big_p)
+        if signed:
+            result = torch.where(result > big_p // 2, result - big_p, result)
+        return result
+
+    # ------------------------------------------------------------------
+    # Prepared weights (cuda_backend.py:464-622)
+    # ------------------------------------------------------------------
+    def _prepare_nk(self, b_nk: torch.Tensor, mods: tuple[int, ...], k: int, n: int,
+                    kernel: str) -> PreparedRNSWeight:
+        consts = self._constants(b_nk.device, mods)
+        r = len(mods)
+        kp = (k + _native.K_ALIGN - 1) // _native.K_ALIGN * _native.K_ALIGN
+        packed = torch.empty((r, n, kp), dtype=torch.int8, device=b_nk.device)
+        absmax = torch.zeros((1,), dtype=torch.int32, device=b_nk.device)
+        self._stats["encode_centered_calls"] += 1
+        self._stats["encode_centered_values"] += int(b_nk.numel())
+        _native.check(self._lib.rnsmx_prepare_weight(
+            _aligned(b_nk).data_ptr(), _native.dtype_code(b_nk.dtype), n, k, consts.native_ref,
+            packed.data_ptr(), absmax.data_ptr(), _stream_handle(b_nk.device)))
+        residues = packed[:, :, :k].transpose(1, 2)
+        return PreparedRNSWeight(residues=residues, moduli=mods, k=k, n=n, kernel=kernel,
+                                 packed=packed, absmax=absmax)
+
+    def prepare_weight(self, b: torch.Tensor, moduli: Iterable[int]) -> PreparedRNSWeight:
+        """B [K, N] int8/int16/int32 -> prepared centered residues."""
+        self._validate_matrix(b, "b", 2)
+        if b.dtype not in (torch.int8, torch.int16, torch.int32):
+            raise ValueError("prepared weights support int8/int16/int32")
+        mods = validate_moduli(moduli)
+        k, n = int(b.shape[0]), int(b.shape[1])
+        kernel = self.select_centered_kernel(k=k, n=n, moduli=mods, requested="auto",
+                                             device=b.device)
+        return self._prepare_nk(b.t().contiguous(), mods, k, n, kernel)
+
+    def prepare_weight_nk(self, w: torch.Tensor, moduli: Iterable[int]) -> PreparedRNSWeight:
+        """Same as ``prepare_weight(w.T)`` for a quantized nn.Linear weight
+        W [N, K], without the transpose."""
+        self._validate_matrix(w, "w", 2)
+        if w.dtype not in (torch.int8, torch.int16, torch.int32):
+            raise ValueError("prepared weights support int8/int16/int32")
+        mods = validate_moduli(moduli)
+        n, k = int(w.shape[0]), int(w.shape[1])
+        kernel = self.select_centered_kernel(k=k, n=n, moduli=mods, requested="auto",
+                                             device=w.device)
+        return self._prepare_nk(w, mods, k, n, kernel)
+
+    def _check_activation(self, a: torch.Tensor, prepared: PreparedRNSWeight) -> None:
+        self._validate_matrix(a, "a", 2)
+        if a.dtype not in (torch.int8, torch.int16, torch.int32):
+            raise ValueError("a must be int8/int16/int32")
+        if int(a.shape[1]) != prepared.k:
+            raise ValueError("K dimension does not match prepared weight")
+        if a.device != prepared.residues.device:
+            raise ValueError("activation and prepared weight must share device")
+        if not self.supports_fused(prepared):
+            raise ValueError("prepared weight was not built by this backend")
+
+    def matmul_prepared_fused(self, a: torch.Tensor, prepared_weight: PreparedRNSWeight, *,
+                              lut_channels: int = 0, workspace: RNSWorkspace | None = None,
+                              out: torch.Tensor | None = None, a_scale: torch.Tensor | None = None,
+                              w_scale: torch.Tensor | None = None,
+                              bias: torch.Tensor | None = None) -> torch.Tensor:
+        """a [M, K] int8/16/32 x prepared B -> exact int64 [M, N]
+        (``cuda_backend.py:514-539``), returned as ``workspace.output``.
+
+        With ``out`` (float32/float16/bfloat16 [M, N]) plus ``a_scale`` [1]
+        and ``w_scale`` [N] (and optional ``bias`` [N], all float32), the
+        epilogue instead writes ``((float)x * a_scale) * w_scale + bias`` in
+        ``out``'s dtype, the float chain of ``RNSLinear.forward``."""
+        return self._prepared_call(a, prepared_weight, lut_channels, workspace, None,
+                                   out, a_scale, w_scale, bias)
+
+    def _prepared_call(self, a, prepared, lut_channels, workspace, adaptive, out,
+                       a_scale, w_scale, bias):
+        self._check_activation(a, prepared)
+        if lut_channels not in (0, 1, 2):
+            raise ValueError("lut_channels must be 0, 1 or 2")
+        device = a.device
+        m, k, n = int(a.shape[0]), prepared.k, prepared.n
+        channels = len(prepared.moduli)
+        consts = self._constants(device, prepared.moduli)
+        if workspace is None:
+            workspace = self.create_workspace(device=device, channels=channels, m=m, n=n, k=k)
+        self._check_workspace(workspace, channels=channels, m=m, n=n, device=device)
+        scratch = self._scratch(
+            workspace, int(self._lib.rnsmx_prepared_workspace_bytes(m, k, channels)))
+        epi = None
+        target = workspace.output
+        if out is not None:
+            if out.shape != (m, n) or not out.is_contiguous() or out.device != device:
+                raise ValueError("out must be a contiguous [M, N] tensor on the same device")
+            if a_scale is None or w_scale is None:
+                raise ValueError("float output needs a_scale and w_scale")
+            for name, t, size in (("a_scale", a_scale, 1), ("w_scale", w_scale, n),
+                                  ("bias", bias, n)):
+                if t is None:
+                    continue
+                if t.dtype != torch.float32 or t.numel() != size or not t.is_contiguous():
+                    raise ValueError(f"{name} must be a contiguous float32 tensor of {size} values")
+            epi = _native.Epilogue(
+                _native.dtype_code(out.dtype), a_scale.data_ptr(), w_scale.data_ptr(),
+                bias.data_ptr() if bias is not None else None)
+            epi = ctypes.byref(epi)
+            target = out
+        self._stats["encode_centered_calls"] += 1
+        self._stats["encode_centered_values"] += int(a.numel())
+        self._stats["fused_gemm_calls"] += 1
+        self._stats[f"fused_gemm_channels_{channels}"] += 1
+        _native.check(self._lib.rnsmx_matmul_prepared_fused(
+            _aligned(a).data_ptr(), _native.dtype_code(a.dtype), m, k, n,
+            prepared.packed.data_ptr(), consts.native_ref, consts.compact_lut.data_ptr(),
+            lut_channels, adaptive, epi, scratch.data_ptr(), scratch.numel(),
+            target.data_ptr(), _stream_handle(device)))
+        return target
+
+    def encode_activations(self, a: torch.Tensor, prepared_weight: PreparedRNSWeight,
+                           out: torch.Tensor | None = None) -> torch.Tensor:
+        """a [M, K] -> centered residues [R, M, kp], zero padded to the
+        prepared weight's K alignment (the layout the GEMM reads)."""
+        self._check_activation(a, prepared_weight)
+        m, k = int(a.shape[0]), prepared_weight.k
+        kp = int(prepared_weight.packed.shape[2])
+        r = len(prepared_weight.moduli)
+        if out is None:
+            out = torch.empty((r, m, kp), dtype=torch.int8, device=a.device)
+        elif out.shape != (r, m, kp) or out.dtype != torch.int8 or not out.is_contiguous():
+            raise ValueError("out must be a contiguous int8 [R, M, kp] tensor")
+        consts = self._constants(a.device, prepared_weight.moduli)
+        self._stats["encode_centered_calls"] += 1
+        self._stats["encode_centered_values"] += int(a.numel())
+        _native.check(self._lib.rnsmx_encode_centered(
+            _aligned(a).data_ptr(), _native.dtype_code(a.dtype), m, k, kp, consts.native_ref,
+            out.data_ptr(), None, None, _stream_handle(a.device)))
+        return out
+
+    def matmul_residues_prepared(self, a_residues: torch.Tensor, prepared_weight: PreparedRNSWeight,
+                                 *, lut_channels: int = 0, out: torch.Tensor | None = None,
+                                 a_scale=None, w_scale=None, bias=None) -> torch.Tensor:
+        """GEMM stage alone: residues from ``encode_activations`` x prepared
+        weight -> int64 [M, N] (or the float epilogue into ``out``)."""
+        if a_residues.ndim != 3 or a_residues.dtype != torch.int8 or not a_residues.is_contiguous():
+            raise ValueError("a_residues must be a contiguous int8 [R, M, kp] tensor")
+        r, m, kp = map(int, a_residues.shape)
+        if r != len(prepared_weight.moduli) or kp != int(prepared_weight.packed.shape[2]):
+            raise ValueError("a_residues do not match the prepared weight")
+        if lut_channels not in (0, 1, 2):
+            raise ValueError("lut_channels must be 0, 1 or 2")
+        n = prepared_weight.n
+        consts = self._constants(a_residues.device, prepared_weight.moduli)
+        epi = None
+        if out is None:
+            out = torch.empty((m, n), dtype=torch.int64, device=a_residues.device)
+        elif out.dtype != torch.int64:
+            if a_scale is None or w_scale is None:
+                raise ValueError("float output needs a_scale and w_scale")
+            epi = ctypes.byref(_native.Epilogue(
+                _native.dtype_code(out.dtype), a_scale.data_ptr(), w_scale.data_ptr(),
+                bias.data_ptr() if bias is not None else None))
+        if out.shape != (m, n) or not out.is_contiguous():
+            raise ValueError("out must be a contiguous [M, N] tensor")
+        self._stats["fused_gemm_calls"] += 1
+        self._stats[f"fused_gemm_channels_{r}"] += 1
+        _native.check(self._lib.rnsmx_matmul_residues_prepared(
+            a_residues.data_ptr(), kp, m, prepared_weight.k, n, prepared_weight.packed.data_ptr(),
+            consts.native_ref, consts.compact_lut.data_ptr(), lut_channels, epi, out.data_ptr(),
+            _stream_handle(a_residues.device)))
+        return out
+
+    def matmul_prepared(self, a: torch.Tensor, prepared_weight: PreparedRNSWeight, *,
+                        decode: bool = True, kernel: str = "auto") -> torch.Tensor:
+        """Non-workspace entry (``cuda_backend.py:489-512``): the exact int64
+        product, or its centered residues with ``decode=False``."""
+        self._check_activation(a, prepared_weight)
+        self.select_centered_kernel(k=prepared_weight.k, n=prepared_weight.n,
+                                    moduli=prepared_weight.moduli, requested=kernel,
+                                    device=a.device)
+        exact = self.matmul_prepared_fused(a, prepared_weight).clone()
+        return exact if decode else self._encode_int64_centered(exact, prepared_weight.moduli)
+
+    def prepare_weight_adaptive(self, b: torch.Tensor, moduli: Iterable[int], *,
+                                min_channels: int = 3) -> PreparedAdaptiveRNSWeight:
+        """Encode once; every prefix variant shares the storage."""
+        full = self.prepare_weight(b, moduli)
+        return self._adaptive_from(full, min_channels)
+
+    def prepare_weight_adaptive_nk(self, w: torch.Tensor, moduli: Iterable[int], *,
+                                   min_channels: int = 3) -> PreparedAdaptiveRNSWeight:
+        full = self.prepare_weight_nk(w, moduli)
+        return self._adaptive_from(full, min_channels)
+
+    def _adaptive_from(self, full: PreparedRNSWeight, min_channels: int) -> PreparedAdaptiveRNSWeight:
+        if not 2 <= min_channels <= len(full.moduli):
+            raise ValueError("min_channels must be between 2 and full channel count")
+        variants = {}
+        for c in range(min_channels, len(full.moduli) + 1):
+            prefix = full.moduli[:c]
+            kernel = self.select_centered_kernel(k=full.k, n=full.n, moduli=prefix,
+                                                 requested="auto", device=full.residues.device)
+            variants[c] = PreparedRNSWeight(
+                residues=full.residues[:c], moduli=prefix, k=full.k, n=full.n, kernel=kernel,
+                packed=full.packed[:c], absmax=full.absmax)
+        return PreparedAdaptiveRNSWeight(variants, full.moduli, full.absmax, min_channels)
+
+    def select_adaptive_variant(self, a: torch.Tensor, prepared: PreparedAdaptiveRNSWeight):
+        """Host-side selection with the reference's synchronising bound
+        (``cuda_backend.py:577-600``); the fused adaptive call does not use
+        it."""
+        self._validate_matrix(a, "a", 2)
+        if a.dtype not in (torch.int8, torch.int16, torch.int32):
+            raise ValueError("a must be int8/int16/int32")
+        max_row_l1 = int(a.to(torch.int64).abs().sum(dim=1).max().item()) if a.numel() else 0
+        bound = safe_l1_dot_bound(max_row_l1, prepared.max_abs_weight)
+        channels = minimal_prefix_channels(prepared.full_moduli, bound,
+                                           min_channels=prepared.min_channels)
+        self._stats["adaptive_selections"] += 1
+        self._stats[f"adaptive_channels_{channels}"] += 1
+        return prepared.variants[channels], bound
+
+    def matmul_prepared_adaptive_fused(self, a: torch.Tensor, prepared: PreparedAdaptiveRNSWeight,
+                                       *, lut_channels: int = 2,
+                                       workspace_by_channels: dict | None = None,
+                                       return_metadata: bool = False, out=None, a_scale=None,
+                                       w_scale=None, bias=None):
+        """Adaptive prefix chosen on the device (no host synchronisation).
+        The full-set workspace is used for every prefix; the output is exact
+        whenever the bound fits the full set, and the metadata reports the
+        prefix that was used."""
+        full = prepared.variants[len(prepared.full_moduli)]
+        workspace = None
+        if workspace_by_channels is not None:
+            workspace = workspace_by_channels.get(len(prepared.full_moduli))
+        meta = torch.empty((4,), dtype=torch.int64, device=a.device)
+        adaptive = _native.Adaptive(prepared.min_channels, prepared.absmax.data_ptr(),
+                                    meta.data_ptr())
+        self._stats["adaptive_selections"] += 1
+        result = self._prepared_call(a, full, lut_channels, workspace, ctypes.byref(adaptive),
+                                     out, a_scale, w_scale, bias)
+        if return_metadata:
+            return result, AdaptiveMetadata(meta, prepared.full_moduli)
+        return result
+
+    # ------------------------------------------------------------------
+    # Continuous batching (cuda_backend.py:624-703)
+    # ------------------------------------------------------------------
+    def create_request_batch_workspace(self, *, device: torch.device, dtype: torch.dtype,
+                                       rows_per_request: Sequence[int], k: int, channels: int,
+                                       n: int) -> RNSRequestBatchWorkspace:
+        rows = tuple(int(x) for x in rows_per_request)
+        if not rows or any(x <= 0 for x in rows):
+            raise ValueError("rows_per_request must contain positive sizes")
+        total = sum(rows)
+        return RNSRequestBatchWorkspace(
+            activations=torch.empty((total, k), dtype=dtype, device=device),
+            fused=self.create_workspace(device=device, channels=channels, m=total, n=n, k=k),
+            rows_per_request=rows,
+            k=int(k),
+        )
+
+    def matmul_prepared_fused_requests(self, requests: Sequence[torch.Tensor],
+                                       prepared_weight: PreparedRNSWeight, *,
+                                       lut_channels: int = 2,
+                                       workspace: RNSRequestBatchWorkspace | None = None,
+                                       clone_outputs: bool = False) -> tuple[torch.Tensor, ...]:
+        """Concatenate requests along M, run one fused GEMM, split the rows."""
+        if not requests:
+            raise ValueError("requests must not be empty")
+        first = requests[0]
+        rows = tuple(int(x.shape[0]) for x in requests)
+        for index, t in enumerate(requests):
+            self._validate_matrix(t, f"requests[{index}]", 2)
+            if t.dtype != first.dtype or t.device != first.device:
+                raise ValueError("all requests must share dtype/device")
+            if int(t.shape[1]) != prepared_weight.k:
+                raise ValueError("request K does not match prepared weight")
+        if workspace is None:
+            workspace = self.create_request_batch_workspace(
+                device=first.device, dtype=first.dtype, rows_per_request=rows,
+                k=prepared_weight.k, channels=len(prepared_weight.moduli), n=prepared_weight.n)
+        if workspace.rows_per_request != rows or workspace.k != prepared_weight.k:
+            raise ValueError("request batch workspace does not match request shapes")
+        offset = 0
+        for t in requests:
+            workspace.activations[offset:offset + t.shape[0]].copy_(t)
+            offset += int(t.shape[0])
+        merged = self.matmul_prepared_fused(workspace.activations, prepared_weight,
+                                            lut_channels=lut_channels, workspace=workspace.fused)
+        outputs = []
+        offset = 0
+        for r in rows:
+            view = merged[offset:offset + r]
+            outputs.append(view.clone() if clone_outputs else view)
+            offset += r
+        self._stats["continuous_batch_calls"] += 1
+        self._stats["continuous_batch_requests"] += len(requests)
+        return tuple(outputs)
+
+    # ------------------------------------------------------------------
+    # Convenience wrappers (cuda_backend.py:733-799)
+    # ------------------------------------------------------------------
+    def matmul_wide(self, a: torch.Tensor, b: torch.Tensor, moduli: Iterable[int], *,
+                    decode: bool = True, kernel: str = "auto") -> torch.Tensor:
+        self._validate_matrix(a, "a", 2)
+        self._validate_matrix(b, "b", 2)
+        if a.dtype not in (torch.int8, torch.int16, torch.int32):
+            raise ValueError("a must be int8/int16/int32")
+        if b.dtype != a.dtype:
+            raise ValueError("a and b must use the same integer dtype")
+        if a.shape[1] != b.shape[0]:
+            raise ValueError("K dimensions do not match")
+        mods = validate_moduli(moduli)
+        a_res = self.encode_centered(a, mods)
+        b_res = self.encode_centered(b, mods)
+        if decode:
+            return self.matmul_centered_fused(a_res, b_res, mods).clone()
+        return self.matmul_centered_residues(a_res, b_res, mods, kernel=kernel)
+
+    def matmul_wide_fused(self, a: torch.Tensor, b: torch.Tensor, moduli: Iterable[int], *,
+                          lut_channels: int = 0,
+                          workspace: RNSWorkspace | None = None) -> torch.Tensor:
+        self._validate_matrix(a, "a", 2)
+        self._validate_matrix(b, "b", 2)
+        if a.dtype not in (torch.int8, torch.int16, torch.int32):
+            raise ValueError("a must be int8/int16/int32")
+        if b.dtype != a.dtype or a.shape[1] != b.shape[0]:
+            raise ValueError("dtype/K mismatch")
+        mods = validate_moduli(moduli)
+        a_res = self.encode_centered(a, mods)
+        b_res = self.encode_centered(b, mods)
+        return self.matmul_centered_fused(a_res, b_res, mods, lut_channels=lut_channels,
+                                          workspace=workspace)
+
+    def matmul_int8(self, a: torch.Tensor, b: torch.Tensor, moduli: Iterable[int], *,
+                    decode: bool = True, kernel: str = "auto") -> torch.Tensor:
+        if a.dtype != torch.int8 or b.dtype != torch.int8:
+            raise ValueError("matmul_int8 expects int8 inputs")
+        return self.matmul_wide(a, b, moduli, decode=decode, kernel=kernel)
+
+
+def hip_extension_available() -> bool:
+    return _native.available()

@@ -1,0 +1,383 @@
+"""GPU parity: every result of the HIP path equals the CPU oracle / exact
+int64 product bit for bit (integer outputs) or the op-by-op float chain bit
+for bit (dequantized outputs).  Mirrors tests/test_cuda_backend.py of the
+reference plus the BASELINE configs and their edge cases."""
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from oracle import c_oracle, linear_oracle
+from oracle import rns_oracle as ro
+from rns_llm_amd import RNSLinear, RNSQKVProjection, choose_moduli_for_dot
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+DENSE4 = (255, 253, 251, 247)
+DEV = "cuda"
+
+
+def rand_i8(gen, shape, lo=-127, hi=127):
+    return torch.randint(lo, hi + 1, shape, dtype=torch.int8, generator=gen)
+
+
+def exact(a, b):
+    return ro.exact_matmul(np.asarray(a), np.asarray(b))
+
+
+# --------------------------------------------------------------------------
+# encode
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("moduli", [DENSE4, (251, 241, 239, 233), (3, 5, 7, 11, 13, 17, 19, 23, 29, 31),
+                                    (254, 253, 251), (2, 3)])
+def test_encode_int8_exhaustive(backend, moduli):
+    v = torch.arange(-128, 128, dtype=torch.int16).to(torch.int8).repeat(3)[:700]  # ragged numel
+    got = backend.encode_centered(v.to(DEV), moduli).cpu().numpy()
+    np.testing.assert_array_equal(got, ro.encode_centered(v.numpy(), moduli))
+
+
+@pytest.mark.parametrize("dtype", [torch.int16, torch.int32])
+def test_encode_wide_dtypes(backend, dtype):
+    gen = torch.Generator().manual_seed(3)
+    info = torch.iinfo(dtype)
+    v = torch.randint(info.min, info.max, (33, 47), dtype=torch.int64, generator=gen).to(dtype)
+    v[0, :4] = torch.tensor([info.min, info.max, 0, -1], dtype=dtype)
+    got = backend.encode_centered(v.to(DEV), DENSE4).cpu().numpy()
+    assert got.shape == (4, 33, 47)
+    np.testing.assert_array_equal(got, ro.encode_centered(v.numpy(), DENSE4))
+
+
+def test_encode_empty(backend):
+    out = backend.encode_centered(torch.empty((0, 5), dtype=torch.int8, device=DEV), DENSE4)
+    assert out.shape == (4, 0, 5)
+
+
+# --------------------------------------------------------------------------
+# golden vectors through both fused entry points
+# --------------------------------------------------------------------------
+GOLDEN_CASES = [p for p in sorted(glob.glob(os.path.join(GOLDEN, "*.npz")))
+                if "expected" in np.load(p)]
+
+
+@pytest.mark.parametrize("path", GOLDEN_CASES, ids=lambda p: os.path.basename(p)[:-4])
+@pytest.mark.parametrize("lut", [0, 2])
+def test_golden_prepared_fused(backend, path, lut):
+    g = np.load(path)
+    mods = tuple(int(m) for m in g["moduli"])
+    a = torch.from_numpy(g["a"]).to(DEV)
+    b = torch.from_numpy(g["b"]).to(DEV)
+    prepared = backend.prepare_weight(b, mods)
+    out = backend.matmul_prepared_fused(a, prepared, lut_channels=min(lut, len(mods)))
+    np.testing.assert_array_equal(out.cpu().numpy(), g["expected"])
+
+
+@pytest.mark.parametrize("path", GOLDEN_CASES, ids=lambda p: os.path.basename(p)[:-4])
+def test_golden_centered_fused_dropin(backend, path):
+    g = np.load(path)
+    mods = tuple(int(m) for m in g["moduli"])
+    a = torch.from_numpy(g["a"]).to(DEV)
+    b = torch.from_numpy(g["b"]).to(DEV)
+    out = backend.matmul_wide_fused(a, b, mods, lut_channels=1)
+    np.testing.assert_array_equal(out.cpu().numpy(), g["expected"])
+
+
+# --------------------------------------------------------------------------
+# shapes: skinny and tiled kernels, ragged edges, every channel capacity
+# --------------------------------------------------------------------------
+SHAPES = [(1, 768, 2304), (4, 768, 768), (16, 768, 2304), (17, 64, 20), (33, 100, 37),
+          (64, 768, 96), (65, 768, 130), (128, 768, 2304), (256, 768, 2304), (300, 200, 333),
+          (1024, 768, 256)]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+def test_prepared_fused_shapes(backend, m, k, n):
+    gen = torch.Generator().manual_seed(m * 7 + k + n)
+    a = rand_i8(gen, (m, k))
+    b = rand_i8(gen, (k, n))
+    mods = choose_moduli_for_dot(k, 127, 127, strategy="dense_coprime")
+    prepared = backend.prepare_weight(b.to(DEV), mods)
+    out = backend.matmul_prepared_fused(a.to(DEV), prepared, lut_channels=2)
+    np.testing.assert_array_equal(out.cpu().numpy(), exact(a, b))
+
+
+@pytest.mark.parametrize("mods,amax", [((3, 5, 7, 11, 13, 17, 19, 23, 29, 31), 60),
+                                       ((251, 241, 239, 233, 229), 127),
+                                       ((255, 253, 251, 247, 241, 239), 127),
+                                       ((127, 125, 121, 113), 127),
+                                       ((251, 241), 3)])
+@pytest.mark.parametrize("m", [5, 96])
+def test_channel_counts(backend, mods, amax, m):
+    gen = torch.Generator().manual_seed(len(mods) * 100 + m)
+    k, n = 64, 48
+    a = rand_i8(gen, (m, k), -amax, amax)
+    b = rand_i8(gen, (k, n), -amax, amax)
+    prepared = backend.prepare_weight(b.to(DEV), mods)
+    out = backend.matmul_prepared_fused(a.to(DEV), prepared, lut_channels=min(2, len(mods)))
+    np.testing.assert_array_equal(out.cpu().numpy(), ro.rns_matmul_centered(a.numpy(), b.numpy(), mods))
+
+
+def test_wraparound_matches_oracle(backend):
+    # product outside the centered range: the device reduces mod P exactly as
+    # the reference's Garner path does (both C and NumPy oracles agree)
+    mods = (3, 5, 7, 11)
+    gen = torch.Generator().manual_seed(8)
+    a = rand_i8(gen, (9, 16))
+    b = rand_i8(gen, (16, 5))
+    prepared = backend.prepare_weight(b.to(DEV), mods)
+    out = backend.matmul_prepared_fused(a.to(DEV), prepared).cpu().numpy()
+    np.testing.assert_array_equal(out, c_oracle.rns_matmul_centered(a.numpy(), b.numpy(), mods))
+
+
+def test_int16_wide_inputs(backend):
+    # tests/test_cuda_backend.py:49-58 and :73-94 (int12, lut 0/1/2)
+    gen = torch.Generator().manual_seed(12)
+    a = torch.randint(-2047, 2048, (24, 64), dtype=torch.int16, generator=gen)
+    b = torch.randint(-2047, 2048, (64, 32), dtype=torch.int16, generator=gen)
+    mods = choose_moduli_for_dot(64, 2047, 2047, strategy="dense_coprime")
+    want = exact(a, b)
+    np.testing.assert_array_equal(backend.matmul_wide(a.to(DEV), b.to(DEV), mods).cpu().numpy(), want)
+    prepared = backend.prepare_weight(b.to(DEV), mods)
+    for lut in (0, 1, 2):
+        out = backend.matmul_prepared_fused(a.to(DEV), prepared, lut_channels=lut)
+        np.testing.assert_array_equal(out.cpu().numpy(), want)
+
+
+def test_int16_source_five_six_channels(backend):
+    # quant_bits 12/16 style sources: K=768 needs 5 (int12) or 6+ channels
+    gen = torch.Generator().manual_seed(16)
+    for bits, amax in ((12, 2047), (16, 4000)):
+        k = 768
+        mods = choose_moduli_for_dot(k, amax, amax, strategy="dense_coprime")
+        assert len(mods) >= 5
+        a = torch.randint(-amax, amax + 1, (7, k), dtype=torch.int16, generator=gen)
+        b = torch.randint(-amax, amax + 1, (k, 40), dtype=torch.int16, generator=gen)
+        prepared = backend.prepare_weight(b.to(DEV), mods)
+        out = backend.matmul_prepared_fused(a.to(DEV), prepared, lut_channels=2)
+        np.testing.assert_array_equal(out.cpu().numpy(), exact(a, b))
+
+
+# --------------------------------------------------------------------------
+# reference backend contract
+# --------------------------------------------------------------------------
+def test_prepared_matches_uncached(backend):
+    # tests/test_cuda_backend.py:61-71
+    gen = torch.Generator().manual_seed(24)
+    a = rand_i8(gen, (24, 64)).to(DEV)
+    b = rand_i8(gen, (64, 32)).to(DEV)
+    mods = choose_moduli_for_dot(64, 127, 127)
+    prepared = backend.prepare_weight(b, mods)
+    torch.testing.assert_close(backend.matmul_prepared(a, prepared),
+                               backend.matmul_wide(a, b, mods), rtol=0, atol=0)
+
+
+def test_garner_decoder_matches_crt_decoder(backend):
+    # tests/test_cuda_backend.py:97-108
+    gen = torch.Generator().manual_seed(32)
+    a = rand_i8(gen, (32, 64)).to(DEV)
+    b = rand_i8(gen, (64, 32)).to(DEV)
+    mods = choose_moduli_for_dot(64, 127, 127, strategy="dense_coprime")
+    residues = backend.matmul_centered_residues(backend.encode_centered(a, mods),
+                                                backend.encode_centered(b, mods), mods)
+    np.testing.assert_array_equal(
+        residues.cpu().numpy(),
+        ro.encode_centered(ro.matmul_residues(ro.encode_canonical(a.cpu().numpy(), mods),
+                                              ro.encode_canonical(b.cpu().numpy(), mods), mods), mods))
+    new = backend.decode_garner(residues, mods)
+    old = backend.decode(residues, mods)
+    torch.testing.assert_close(new, old, rtol=0, atol=0)
+    np.testing.assert_array_equal(new.cpu().numpy(), exact(a.cpu(), b.cpu()))
+
+
+def test_decode_garner_known_answer(backend):
+    g = np.load(os.path.join(GOLDEN, "ref_garner_values.npz"))
+    mods = tuple(int(m) for m in g["moduli"])
+    res = torch.from_numpy(ro.encode_centered(g["values"], mods)).to(DEV)
+    np.testing.assert_array_equal(backend.decode_garner(res, mods).cpu().numpy(), g["values"])
+
+
+def test_continuous_batch_matches_independent_requests(backend):
+    # tests/test_cuda_backend.py:111-138
+    gen = torch.Generator().manual_seed(64)
+    mods = choose_moduli_for_dot(64, 127, 127, strategy="dense_coprime")
+    weight = rand_i8(gen, (64, 32))
+    prepared = backend.prepare_weight(weight.to(DEV), mods)
+    requests = [rand_i8(gen, (rows, 64)).to(DEV) for rows in (1, 3, 5, 2)]
+    ws = backend.create_request_batch_workspace(
+        device=torch.device(DEV), dtype=torch.int8, rows_per_request=[r.shape[0] for r in requests],
+        k=64, channels=len(mods), n=32)
+    merged = backend.matmul_prepared_fused_requests(requests, prepared, workspace=ws,
+                                                    clone_outputs=True)
+    for req, got in zip(requests, merged):
+        torch.testing.assert_close(got, backend.matmul_prepared_fused(req, prepared), rtol=0, atol=0)
+        np.testing.assert_array_equal(got.cpu().numpy(), exact(req.cpu(), weight))
+    stats = backend.stats_snapshot()
+    assert stats["continuous_batch_calls"] >= 1
+
+
+@pytest.mark.parametrize("requests", [1, 2, 4])
+def test_c3_decode_requests(backend, requests):
+    gen = torch.Generator().manual_seed(300 + requests)
+    w = rand_i8(gen, (768, 768))
+    prepared = backend.prepare_weight(w.to(DEV), DENSE4)
+    reqs = [rand_i8(gen, (1, 768)).to(DEV) for _ in range(requests)]
+    merged = backend.matmul_prepared_fused_requests(reqs, prepared, clone_outputs=True)
+    for req, got in zip(reqs, merged):
+        np.testing.assert_array_equal(got.cpu().numpy(), exact(req.cpu(), w))
+
+
+def test_adaptive_prefix_exact_and_falls_back(backend):
+    # tests/test_cuda_backend.py:141-162 (device-side selection)
+    gen = torch.Generator().manual_seed(141)
+    mods = choose_moduli_for_dot(64, 127, 127, strategy="dense_coprime")
+    weight = rand_i8(gen, (64, 32), -40, 40)
+    adaptive = backend.prepare_weight_adaptive(weight.to(DEV), mods, min_channels=3)
+    for lo, expect_c in ((8, 3), (127, None)):
+        a = rand_i8(gen, (16, 64), -lo, lo)
+        out, meta = backend.matmul_prepared_adaptive_fused(a.to(DEV), adaptive, return_metadata=True)
+        np.testing.assert_array_equal(out.cpu().numpy(), exact(a, weight))
+        c, bound, cap = ro.adaptive_select(a.numpy(), int(weight.abs().max()), mods, min_channels=3)
+        assert (meta["channels"], meta["bound"], meta["capacity"]) == (c, bound, cap)
+        assert meta["bound"] <= meta["capacity"]
+        if expect_c is not None:
+            assert meta["channels"] == expect_c
+    assert adaptive.max_abs_weight == int(weight.abs().max())
+
+
+def test_adaptive_adversarial_full_set_k4096(backend):
+    # C5 edge: all +-127 at K=4096 -> bound 66,064,384, prefix 3 cannot hold
+    # it, so the device must pick the full 4-channel set
+    k, n = 4096, 64
+    a = torch.full((3, k), 127, dtype=torch.int8)
+    a[1] = -127
+    a[2, ::2] = -127
+    b = torch.full((k, n), 127, dtype=torch.int8)
+    b[:, ::3] = -127
+    adaptive = backend.prepare_weight_adaptive(b.to(DEV), DENSE4, min_channels=3)
+    out, meta = backend.matmul_prepared_adaptive_fused(a.to(DEV), adaptive, return_metadata=True)
+    np.testing.assert_array_equal(out.cpu().numpy(), exact(a, b))
+    assert meta["channels"] == 4 and meta["bound"] == 4096 * 127 * 127
+
+
+def test_adaptive_overflow_is_reported(backend):
+    # a two-channel set cannot hold full-range products: the device flags it
+    mods = (251, 241)
+    gen = torch.Generator().manual_seed(5)
+    b = rand_i8(gen, (64, 8))
+    a = rand_i8(gen, (4, 64))
+    adaptive = backend.prepare_weight_adaptive(b.to(DEV), mods, min_channels=2)
+    _, meta = backend.matmul_prepared_adaptive_fused(a.to(DEV), adaptive, return_metadata=True)
+    assert meta.overflow
+    with pytest.raises(OverflowError):
+        meta["channels"]
+
+
+def test_streams_have_independent_workspaces(backend):
+    gen = torch.Generator().manual_seed(77)
+    w = rand_i8(gen, (768, 512))
+    prepared = backend.prepare_weight(w.to(DEV), DENSE4)
+    xs = [rand_i8(gen, (32, 768)) for _ in range(4)]
+    streams = [torch.cuda.Stream() for _ in range(4)]
+    outs = []
+    torch.cuda.synchronize()
+    for x, s in zip(xs, streams):
+        with torch.cuda.stream(s):
+            ws = backend.create_workspace(device=torch.device(DEV), channels=4, m=32, n=512, k=768)
+            xd = x.to(DEV, non_blocking=False)
+            outs.append((backend.matmul_prepared_fused(xd, prepared, workspace=ws), ws))
+    torch.cuda.synchronize()
+    for x, (o, _) in zip(xs, outs):
+        np.testing.assert_array_equal(o.cpu().numpy(), exact(x, w))
+
+
+def test_validation_errors(backend):
+    a = torch.zeros((4, 64), dtype=torch.int8, device=DEV)
+    prepared = backend.prepare_weight(torch.zeros((64, 8), dtype=torch.int8, device=DEV), DENSE4)
+    with pytest.raises(ValueError):
+        backend.matmul_prepared_fused(torch.zeros((4, 32), dtype=torch.int8, device=DEV), prepared)
+    with pytest.raises(ValueError):
+        backend.matmul_prepared_fused(a.float(), prepared)
+    with pytest.raises(ValueError):
+        backend.matmul_prepared_fused(a, prepared, lut_channels=3)
+    ws = backend.create_workspace(device=torch.device(DEV), channels=4, m=5, n=8)
+    with pytest.raises(ValueError):
+        backend.matmul_prepared_fused(a, prepared, workspace=ws)
+    with pytest.raises(ValueError):
+        backend.matmul_centered_fused(torch.zeros((3, 4, 64), dtype=torch.int8, device=DEV),
+                                      torch.zeros((4, 64, 8), dtype=torch.int8, device=DEV), DENSE4)
+
+
+# --------------------------------------------------------------------------
+# float epilogue and the RNSLinear / fused QKV layers
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_dequant_epilogue_matches_torch_chain(backend, out_dtype):
+    gen = torch.Generator().manual_seed(9)
+    m, k, n = 37, 768, 200
+    a = rand_i8(gen, (m, k)).to(DEV)
+    b = rand_i8(gen, (k, n)).to(DEV)
+    a_scale = torch.rand(1, generator=gen).to(DEV) * 0.01 + 1e-3
+    w_scale = (torch.rand(n, generator=gen) * 0.01 + 1e-4).to(DEV)
+    bias = torch.randn(n, generator=gen).to(DEV)
+    prepared = backend.prepare_weight(b, DENSE4)
+    integer = backend.matmul_prepared_fused(a, prepared).clone()
+    want = ((integer.float() * a_scale.view(1, 1)) * w_scale.unsqueeze(0) + bias).to(out_dtype)
+    out = torch.empty((m, n), dtype=out_dtype, device=DEV)
+    backend.matmul_prepared_fused(a, prepared, out=out, a_scale=a_scale, w_scale=w_scale, bias=bias)
+    assert torch.equal(out.view(torch.int16 if out_dtype != torch.float32 else torch.int32),
+                       want.view(torch.int16 if out_dtype != torch.float32 else torch.int32))
+
+
+def make_opt_linears(hidden=768, seed=17, dtype=torch.float16):
+    torch.manual_seed(seed)
+    return tuple(nn.Linear(hidden, hidden, bias=True, device=DEV, dtype=dtype).eval()
+                 for _ in range(3))
+
+
+@pytest.mark.parametrize("tokens", [1, 16, 128, 256])
+@pytest.mark.parametrize("fused_epilogue", [True, False])
+def test_fused_qkv_equals_three_rnslinear_and_oracle(backend, tokens, fused_epilogue):
+    originals = make_opt_linears()
+    kw = dict(backend=backend, mode="rns", fused=True, lut_channels=2, fused_epilogue=fused_epilogue)
+    separate = [RNSLinear.from_linear(l, **kw).eval() for l in originals]
+    fused = RNSQKVProjection.from_linears(*originals, **{k: v for k, v in kw.items()}).eval()
+    gen = torch.Generator().manual_seed(tokens)
+    x = torch.randn(1, tokens, 768, generator=gen).to(DEV, torch.float16)
+    fused_out = fused(x)
+    for part, layer, orig in zip(fused_out, separate, originals):
+        sep = layer(x)
+        assert torch.equal(part, sep)                     # fused == three separate, bit-exact
+        want, _ = linear_oracle.linear_forward(x.cpu(), orig.weight.cpu(), orig.bias.cpu())
+        assert torch.equal(sep.cpu(), want)               # == the reference float chain
+
+
+def test_rnslinear_adaptive_matches_oracle(backend):
+    torch.manual_seed(3)
+    lin = nn.Linear(256, 96, device=DEV).eval()
+    layer = RNSLinear.from_linear(lin, backend=backend, mode="rns", adaptive_channels=True).eval()
+    x = torch.randn(5, 256, device=DEV) * 0.05
+    y = layer(x)
+    want, integer = linear_oracle.linear_forward(x.cpu(), lin.weight.cpu(), lin.bias.cpu())
+    assert torch.equal(y.cpu(), want)
+    meta = layer.last_adaptive_metadata
+    assert meta["bound"] <= meta["capacity"]
+
+
+def test_rnslinear_weight_version_invalidates_cache(backend):
+    torch.manual_seed(4)
+    lin = nn.Linear(64, 32, device=DEV).eval()
+    layer = RNSLinear.from_linear(lin, backend=backend, mode="rns").eval()
+    x = torch.randn(3, 64, device=DEV)
+    layer(x)
+    first = layer._prepared_weight
+    layer(x)
+    assert layer._prepared_weight is first
+    with torch.no_grad():
+        layer.weight.mul_(2.0)
+    y = layer(x)
+    assert layer._prepared_weight is not first
+    want, _ = linear_oracle.linear_forward(x.cpu(), layer.weight.detach().cpu(), layer.bias.detach().cpu())
+    assert torch.equal(y.cpu(), want)

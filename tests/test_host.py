@@ -1,0 +1,221 @@
+"""CPU tests of the host side: the C-ABI library loads and exports every
+symbol include/rnsmx.h declares; its host-only constant builders agree with
+the oracle; the package's host logic keeps the reference's results and
+exception types; torch-mode QKV fusion mirrors tests/test_qkv_fusion.py."""
+import ctypes
+import os
+import re
+from math import prod
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from oracle import rns_oracle as ro
+from rns_llm_amd import _native, moduli as host_moduli
+from rns_llm_amd.backends.hip_backend import HipRNSBackend, RNSWorkspace
+from rns_llm_amd.layers import CachedRNSQKV, RNSLinear, RNSQKVProjection
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rnsmx.h")
+DENSE4 = (255, 253, 251, 247)
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(rnsmx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.lib()
+    names = declared_symbols()
+    assert names, "header declares no entry points"
+    for name in names:
+        assert hasattr(lib, name), f"librnsmx.so does not export {name}"
+    assert sorted(_native.EXPORTED_SYMBOLS) == names
+
+
+def test_abi_struct_layout_matches_header():
+    # sizeof(rnsmx_moduli_t) with natural alignment: 4 + 4*10*4 + 4*100 + pad + 8*11
+    assert ctypes.sizeof(_native.Moduli) == 4 + 40 * 4 + 400 + 4 + 88
+    assert _native.lib().rnsmx_abi_version() == _native.ABI_VERSION
+
+
+@pytest.mark.parametrize("mods", [DENSE4, (251, 241, 239, 233), (3, 5, 7, 11, 13, 17, 19, 23, 29, 31),
+                                  (127, 125, 121, 113), (2, 3), (254, 253, 251)])
+def test_native_moduli_constants(mods):
+    """rnsmx_moduli_init's Garner constants reproduce the oracle's mixed-radix
+    digits for random residues, and its Barrett magic / 2^31 offsets are the
+    closed forms."""
+    c = _native.make_moduli(mods)
+    r_count = len(mods)
+    assert c.channels == r_count
+    assert [c.prefix[i] for i in range(r_count + 1)] == [prod(mods[:i]) for i in range(r_count + 1)]
+    for i, m in enumerate(mods):
+        assert c.magic[i] == (1 << 32) // m
+        assert c.c31[i] == (1 << 31) % m
+    rng = np.random.default_rng(0)
+    res = np.stack([rng.integers(0, m, 300) for m in mods])
+    # digits from the native constants: d_i = (r_i q_i + sum_j d_j u_ji) mod m_i
+    digits = []
+    for i, m in enumerate(mods):
+        s = res[i] * c.qinv[i]
+        for j in range(i):
+            s = s + digits[j] * c.ucoef[j][i]
+        digits.append(np.mod(s, m))
+    x = sum(d.astype(object) * prod(mods[:i]) for i, d in enumerate(digits))
+    np.testing.assert_array_equal(np.array(x, dtype=object) % prod(mods),
+                                  ro.decode_garner(res, mods, signed=False).astype(object))
+
+
+def test_native_lut_matches_oracle():
+    c = _native.make_moduli(DENSE4)
+    lut = np.empty((4, 4, 256), dtype=np.int16)
+    _native.check(_native.lib().rnsmx_compact_lut(ctypes.byref(c), lut.ctypes.data))
+    np.testing.assert_array_equal(lut, ro.compact_byte_mod_lut(DENSE4))
+
+
+@pytest.mark.parametrize("bad,exc", [((), ValueError), ((256, 3), ValueError), ((1, 3), ValueError),
+                                     ((255, 15), ValueError), ((251,) * 11, ValueError),
+                                     ((251, 241, 239, 233, 229, 227, 223, 211, 199), OverflowError)])
+def test_native_moduli_errors(bad, exc):
+    with pytest.raises(exc):
+        _native.make_moduli(bad)
+
+
+def test_workspace_bytes_queries():
+    lib = _native.lib()
+    assert lib.rnsmx_prepared_workspace_bytes(256, 768, 4) >= 4 * 256 * 768 + 8 * 256
+    assert lib.rnsmx_prepared_workspace_bytes(1, 100, 3) >= 3 * 128 + 8
+    assert lib.rnsmx_fused_workspace_bytes(16, 768, 2304, 4) >= 4 * 2304 * 768
+    assert lib.rnsmx_fused_workspace_bytes(16, 100, 37, 3) >= 3 * 37 * 128 + 3 * 16 * 128
+    assert lib.rnsmx_prepared_workspace_bytes(-1, 5, 4) == -1
+
+
+def test_c_abi_rejects_bad_arguments_without_gpu():
+    """Argument validation happens before any HIP call, so it is testable on CPU."""
+    lib = _native.lib()
+    c = _native.make_moduli(DENSE4)
+    rc = lib.rnsmx_matmul_centered_fused_out(None, None, 4, 64, 4, ctypes.byref(c), None, 3,
+                                             None, 0, None, None)
+    assert rc == _native.EINVAL and b"lut_channels" in lib.rnsmx_last_error()
+    rc = lib.rnsmx_matmul_prepared_fused(None, _native.INT8, 4, 200_000, 4, None, ctypes.byref(c),
+                                         None, 0, None, None, None, 0, None, None)
+    assert rc == _native.ERANGE
+    rc = lib.rnsmx_encode_centered(None, _native.INT64, 1, 4, 4, ctypes.byref(c), None, None,
+                                   None, None)
+    assert rc == _native.EINVAL
+    # zero-size problems are accepted and launch nothing
+    assert lib.rnsmx_matmul_prepared_fused(None, _native.INT8, 0, 64, 8, None, ctypes.byref(c),
+                                           None, 0, None, None, None, 0, None, None) == _native.OK
+
+
+# --------------------------------------------------------------------------
+# host logic: moduli.py against the oracle
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("k,a,b,strategy", [(768, 127, 127, "dense_coprime"), (64, 2047, 2047, "dense_coprime"),
+                                            (768, 2047, 2047, "large_primes"), (501, 127, 127, "dense_coprime"),
+                                            (4096, 32767, 32767, "dense_coprime"), (64, 127, 127, "small_primes")])
+def test_choose_moduli_matches_oracle(k, a, b, strategy):
+    assert host_moduli.choose_moduli_for_dot(k, a, b, strategy=strategy) == \
+        ro.choose_moduli_for_dot(k, a, b, strategy=strategy)
+
+
+def test_prefix_and_capacity_match_oracle():
+    for bound in (0, 5_000_000, 8_096_632, 8_096_633, 1_999_868_227):
+        assert host_moduli.minimal_prefix_channels(DENSE4, bound, min_channels=2) == \
+            ro.minimal_prefix_channels(DENSE4, bound, min_channels=2)
+    with pytest.raises(OverflowError):
+        host_moduli.minimal_prefix_channels(DENSE4, 1_999_868_228)
+    assert host_moduli.signed_capacity(DENSE4) == ro.signed_capacity(DENSE4)
+    with pytest.raises(ValueError):
+        host_moduli.validate_moduli((255, 253, 51))
+
+
+def test_check_workspace_rejects_mismatch():
+    ws = RNSWorkspace(accumulators=torch.empty(0, dtype=torch.uint8),
+                      output=torch.empty((4, 8), dtype=torch.int64), channels=4, m=4, n=8)
+    HipRNSBackend._check_workspace(ws, channels=4, m=4, n=8, device=torch.device("cpu"))
+    with pytest.raises(ValueError):
+        HipRNSBackend._check_workspace(ws, channels=3, m=4, n=8, device=torch.device("cpu"))
+
+
+def test_backend_requires_gpu():
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    with pytest.raises(RuntimeError):
+        HipRNSBackend()
+
+
+def test_rns_linear_rns_mode_errors_on_cpu():
+    layer = RNSLinear(16, 8, mode="rns").eval()
+    with pytest.raises(RuntimeError):
+        layer(torch.randn(2, 16))            # no backend
+    layer.backend = object()
+    with pytest.raises(RuntimeError):
+        layer(torch.randn(2, 16))            # CPU weights
+    layer.train()
+    with pytest.raises(RuntimeError):
+        layer(torch.randn(2, 16))            # training mode
+    with pytest.raises(ValueError):
+        RNSLinear(16, 8, quant_bits=10)
+    with pytest.raises(ValueError):
+        RNSLinear(16, 8, lut_channels=3)
+
+
+def test_rns_linear_default_moduli():
+    assert RNSLinear(768, 768).moduli == DENSE4
+    assert RNSLinear(4096, 64).moduli == DENSE4
+    assert RNSLinear(768, 8, quant_bits=12).moduli == ro.choose_moduli_for_dot(
+        768, 2047, 2047, strategy="dense_coprime")
+
+
+# --------------------------------------------------------------------------
+# torch-mode QKV fusion (mirrors the reference tests/test_qkv_fusion.py)
+# --------------------------------------------------------------------------
+def make_linears():
+    torch.manual_seed(123)
+    return tuple(nn.Linear(16, 16, bias=True).eval() for _ in range(3))
+
+
+def test_torch_qkv_fusion_matches_three_linears():
+    q, k, v = make_linears()
+    fused = RNSQKVProjection.from_linears(q, k, v, mode="torch").eval()
+    x = torch.randn(2, 5, 16)
+    for left, right in zip(fused(x), (q(x), k(x), v(x))):
+        torch.testing.assert_close(left, right, rtol=1e-6, atol=2e-7)
+
+
+def test_cached_qkv_computes_once_and_recomputes_next_call():
+    q, k, v = make_linears()
+    projection = RNSQKVProjection.from_linears(q, k, v, mode="torch").eval()
+    coord = CachedRNSQKV(projection).eval()
+    qp, kp, vp = coord.slices()
+    x = torch.randn(2, 5, 16)
+    out = (qp(x), kp(x), vp(x))
+    assert projection.compute_count == 1 and coord.cache_misses == 1 and coord.cache_hits == 2
+    for left, right in zip(out, (q(x), k(x), v(x))):
+        torch.testing.assert_close(left, right, rtol=1e-6, atol=2e-7)
+    qp(x)
+    qp(x)  # repeated index: new logical call
+    assert projection.compute_count == 3
+
+
+def test_qkv_proxy_detects_destroyed_coordinator():
+    q, k, v = make_linears()
+    coord = CachedRNSQKV(RNSQKVProjection.from_linears(q, k, v, mode="torch"))
+    proxy = coord.slices()[0]
+    del coord
+    import gc
+    gc.collect()
+    with pytest.raises(RuntimeError):
+        proxy(torch.randn(1, 16))
+
+
+def test_from_linears_validation():
+    q, k, v = make_linears()
+    with pytest.raises(ValueError):
+        RNSQKVProjection.from_linears(q, k, nn.Linear(8, 16), mode="torch")
+    with pytest.raises(TypeError):
+        RNSQKVProjection.from_linears(q, k, nn.Identity(), mode="torch")
