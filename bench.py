@@ -128,7 +128,7 @@ def measure_shape(backend, name, m, k, n_each, parts, steps, warmup, rotate_byte
     prepared, w0 = make_weights(backend, k, n_each, parts, count, seed, device)
     a = make_tokens(m, k, seed + 1, device)
     ws = backend.create_workspace(device=device, channels=r, m=m, n=n, k=k)
-    out0 = backend.matmul_prepared_fused(a, prepared[0], workspace=ws)
+    out0 = backend.matmul_prepared_fused(a, prepared[0], workspace=ws).clone()
     if check:
         exact_check(out0, a, w0, max_rows=256 if k * n < 4_000_000 else 16)
 

@@ -7,7 +7,8 @@ CPU with torch float32 tensors, so the same IEEE operations run as on the GPU:
 
   * ``_symmetric_scale`` (``rns_linear.py:154-159``): amax(|v|) / 127,
     clamped below at float32 eps; per tensor for activations, per output
-    channel (dim=1) for weights;
+    channel (dim=1) for weights; the division by the Python float 127.0 is
+    restated with the GPU rounding (see ``symmetric_scale``);
   * ``_quantize`` (``:161-166``): round-half-to-even(v / s) clamped to
     +-quant_max, cast to int8 (int16 for 12/16-bit);
   * weight preparation (``:183-185``): B = quantized(W).T, contiguous;
@@ -30,8 +31,17 @@ def quant_max(bits: int) -> int:
 
 
 def symmetric_scale(values: torch.Tensor, bits: int = 8, dim=None) -> torch.Tensor:
+    """amax(|v|) / quant_max, clamped at float32 eps, with the rounding of
+    the device the reference runs this on.  ``RNSLinear`` requires GPU
+    weights (``rns_linear.py:172-173``), and on the GPU torch evaluates
+    ``tensor / python_float`` as ``tensor * fl32(1 / python_float)`` (ATen's
+    true-divide kernel multiplies by the reciprocal of a CPU scalar), which
+    differs in the last bit from a correctly rounded division for about 4%
+    of inputs; the CPU ``/`` divides.  The GPU form is restated here."""
     amax = values.detach().abs().amax(dim=dim, keepdim=True)
-    return torch.clamp(amax / float(quant_max(bits)), min=torch.finfo(torch.float32).eps)
+    inv = torch.tensor(1.0, dtype=torch.float32) / torch.tensor(float(quant_max(bits)),
+                                                                dtype=torch.float32)
+    return torch.clamp(amax * inv, min=torch.finfo(torch.float32).eps)
 
 
 def quantize(values: torch.Tensor, scale: torch.Tensor, bits: int = 8) -> torch.Tensor:

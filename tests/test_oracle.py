@@ -292,3 +292,14 @@ def test_quantize_is_half_to_even_and_clamped():
     s = torch.tensor([[0.5]])
     q = linear_oracle.quantize(torch.tensor([[0.25, 0.75, -0.25, 1000.0, -1000.0]]), s)
     assert q.tolist() == [[0, 2, 0, 127, -127]]
+
+
+def test_scale_uses_gpu_reciprocal_rounding():
+    # Measured on the MI355X (torch 2.10 ROCm): for this amax, torch on the GPU
+    # gives amax / 127.0 == amax * fl32(1/127) == 0x3B1BAAA0 (bits below), while
+    # a correctly rounded division gives the next float up.  RNSLinear runs on
+    # the GPU, so the oracle must produce the GPU value.
+    amax = torch.tensor([np.int32(1050309102)], dtype=torch.int32).view(torch.float32)
+    s = linear_oracle.symmetric_scale(amax.reshape(1, 1))
+    assert s.view(torch.int32).item() != (amax / 127.0).view(torch.int32).item()
+    assert s.item() == (amax * (torch.tensor(1.0) / torch.tensor(127.0))).item()
