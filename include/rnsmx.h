@@ -193,6 +193,18 @@ int32_t rnsmx_matmul_residues_prepared(
     const rnsmx_epilogue_t *epilogue, void *out_dev, void *stream);
 
 /*
+ * Process-wide override of the GEMM kernel choice, for tuning sweeps and
+ * for tests that run every kernel family on the same inputs.  kind 0
+ * restores the automatic choice; kind 1 = stream kernel (tile 16*mb x 16*nb,
+ * ks waves splitting K), kind 2 = MFMA kernel (tile 16*mb x 64*nb).  A tile
+ * that is not built makes the next GEMM call fail with RNSMX_EINVAL.  Not
+ * thread-safe; results never depend on it.  No counterpart in the reference
+ * (cuBLAS picks its own kernels there).
+ */
+int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb,
+                                int32_t ks);
+
+/*
  * Garner reconstruction of centered residues [R][count] int8 -> int64.
  * Replaces _C.decode_garner (csrc/rns_cuda.cu:818-885, kernel 416-440).
  */

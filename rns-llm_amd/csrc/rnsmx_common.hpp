@@ -37,4 +37,10 @@ inline bool accumulator_fits(const rnsmx_moduli_t &mods, int64_t k) {
   return k * h * h <= 0x7FFFFFFFLL;
 }
 
+// The same bound when A enters the MFMA as raw int8 (|a| <= 128) against
+// centered weight residues: K * 128 * max_half <= 2^31 - 1.
+inline bool raw_accumulator_fits(const rnsmx_moduli_t &mods, int64_t k) {
+  return k * 128 * static_cast<int64_t>(max_half(mods)) <= 0x7FFFFFFFLL;
+}
+
 }  // namespace rnsmx

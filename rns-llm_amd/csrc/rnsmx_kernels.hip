@@ -31,11 +31,13 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // Argument blocks (passed by value; kernarg memory)
 // ---------------------------------------------------------------------------
 struct GemmArgs {
-  const int8_t *a;  // [R][M][a_ld]
+  const int8_t *a;  // [R][M][a_ld] residue planes, or [M][a_ld] int8 (a_cs = 0)
   int64_t a_ld, a_cs;
   const int8_t *b;  // [R][N][b_ld]
   int64_t b_ld, b_cs;
-  int32_t m, n, kp;  // kp: multiple of 64, <= a_ld, b_ld
+  int32_t m, n, kp;  // kp: multiple of 64, <= b_ld
+  int32_t a_k;       // A bytes per row that are read; 16-byte chunks at or past it load as 0
+  int32_t tiles_m, tiles_n;  // output tile grid (set at launch)
   int32_t lut_channels;
   const int16_t *lut;  // [R][4][256]
   // adaptive prefix
@@ -65,6 +67,19 @@ struct EncodeArgs {
 // ---------------------------------------------------------------------------
 // Helpers
 // ---------------------------------------------------------------------------
+// Kernel arguments read in place from the kernarg segment (constant address
+// space, scalar loads).  A by-value struct parameter used as an ordinary
+// object can be copied whole into per-lane scratch memory by the compiler
+// (it does so for the larger GEMM instances); a reference to the segment
+// never is.  Valid for kernels whose only parameter is the struct, which
+// then sits at offset 0 of the segment.
+#define RNSMX_KARG(T) const __attribute__((address_space(4))) T
+template <typename T>
+__device__ __forceinline__ RNSMX_KARG(T) & kernel_args() {
+  return *(RNSMX_KARG(T) *)(__builtin_amdgcn_kernarg_segment_ptr());
+}
+typedef RNSMX_KARG(GemmArgs) KGemmArgs;
+
 __device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
@@ -80,6 +95,18 @@ __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
   return v;
 }
 
+// prefix[idx] for a runtime idx <= RCAP, as a select chain over constant
+// indices: a runtime index into the kernel-argument block would make the
+// compiler copy the whole block to scratch memory.
+template <int RCAP, typename Mods>
+__device__ __forceinline__ int64_t prefix_at(const Mods &mods, int idx) {
+  int64_t p = mods.prefix[0];
+  static_for<RCAP + 1>([&](auto I) {
+    if (idx == decltype(I)::value) p = mods.prefix[decltype(I)::value];
+  });
+  return p;
+}
+
 // Number of moduli channels to use.  Without the adaptive prefix this is the
 // full set.  With it, every workgroup derives the same answer from the row
 // L1 norms written by the encoder and max|B| written at weight preparation:
@@ -88,7 +115,8 @@ __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
 // (adaptive.py:15-41), i.e. bound <= (P_c - 1) / 2.  When no prefix fits,
 // the full set is used and meta[3] flags the overflow (the reference raises
 // OverflowError on the host, which a device-side selector cannot).
-__device__ int active_channels(const GemmArgs &g, int64_t *red, int *bcast) {
+template <int RCAP>
+__device__ __forceinline__ int active_channels(KGemmArgs &g, int64_t *red, int *bcast) {
   const int full = g.mods.channels;
   if (g.min_channels <= 0) return full;
   int64_t mx = 0;
@@ -107,18 +135,18 @@ __device__ int active_channels(const GemmArgs &g, int64_t *red, int *bcast) {
     const int64_t bound =
         (wmax != 0 && best > LLONG_MAX / wmax) ? LLONG_MAX : best * wmax;
     int c = full, overflow = 1;
-    for (int i = g.min_channels; i <= full; ++i) {
-      if (bound <= (g.mods.prefix[i] - 1) / 2) {
+    static_for<RCAP + 1>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if (overflow && i >= g.min_channels && i <= full && bound <= (g.mods.prefix[i] - 1) / 2) {
         c = i;
         overflow = 0;
-        break;
       }
-    }
+    });
     *bcast = c;
-    if (g.meta != nullptr && blockIdx.x == 0 && blockIdx.y == 0) {
+    if (g.meta != nullptr && blockIdx.x == 0) {
       g.meta[0] = c;
       g.meta[1] = bound;
-      g.meta[2] = (g.mods.prefix[c] - 1) / 2;
+      g.meta[2] = (prefix_at<RCAP>(g.mods, c) - 1) / 2;
       g.meta[3] = overflow;
     }
   }
@@ -131,14 +159,14 @@ __device__ int active_channels(const GemmArgs &g, int64_t *red, int *bcast) {
 // ((float)x * a_scale) * w_scale[col] + bias[col], each step rounded to
 // nearest even with no contraction: the op order of rns_linear.py:272-275.
 template <int RCAP>
-__device__ __forceinline__ void store_element(const GemmArgs &g, int c_act,
+__device__ __forceinline__ void store_element(KGemmArgs &g, int c_act,
                                               const uint32_t (&d)[RCAP], int row,
                                               int col) {
   uint64_t x = 0;
 #pragma unroll
   for (int c = 0; c < RCAP; ++c)
     if (c < c_act) x += static_cast<uint64_t>(d[c]) * static_cast<uint64_t>(g.mods.prefix[c]);
-  const int64_t p = g.mods.prefix[c_act];
+  const int64_t p = prefix_at<RCAP>(g.mods, c_act);
   int64_t y = static_cast<int64_t>(x);
   if (y > (p >> 1)) y -= p;
   const int64_t idx = static_cast<int64_t>(row) * g.out_ld + col;
@@ -163,9 +191,8 @@ __device__ __forceinline__ void store_element(const GemmArgs &g, int c_act,
 // digits: d_C = (r * q_C + sum_{j<C} d_j * u_{j,C}) mod m_C, where
 // q_C = P_C^-1 mod m_C and u_{j,C} = -P_j q_C mod m_C.  Every term is below
 // 2^16 and there are at most 10, so one Barrett reduction suffices.
-template <int C, typename DigitAt>
-__device__ __forceinline__ uint32_t garner_digit(const rnsmx_moduli_t &mods, uint32_t r,
-                                                 DigitAt &&digit_at) {
+template <int C, typename Mods, typename DigitAt>
+__device__ __forceinline__ uint32_t garner_digit(const Mods &mods, uint32_t r, DigitAt &&digit_at) {
   uint32_t s = r * mods.qinv[C];
 #pragma unroll
   for (int j = 0; j < C; ++j) s += digit_at(j) * mods.ucoef[j][C];
@@ -173,267 +200,356 @@ __device__ __forceinline__ uint32_t garner_digit(const rnsmx_moduli_t &mods, uin
 }
 
 // ---------------------------------------------------------------------------
-// Tiled GEMM: one workgroup computes a BM x BN output tile for every channel
-// in turn (4 waves, 2 x 2, each (BM/2) x (BN/2)).  A and B K-steps of 64
-// bytes are staged through double-buffered LDS with 16-byte global loads;
-// rows are padded to 80 bytes so the 16-byte fragment reads of 8 lanes hit
-// disjoint banks.  The global prefetch runs one step ahead and flows across
-// channel boundaries.  After each channel's K loop the int32 accumulators are
-// reduced mod m_c and turned into that channel's Garner digit in registers
-// (one byte per element); after the last channel the digits are recombined
-// and stored.
+// Workgroup -> output tile.  Workgroups are handed to the 8 XCDs round-robin
+// (workgroup b runs on XCD b % 8), and each XCD has its own L2.  Tiles are
+// numbered M-block fastest, so giving every XCD one contiguous run of tile
+// numbers keeps the workgroups that read the same weight columns on the
+// same L2.  The map is a bijection on [0, tiles) for any tile count.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int &mt, int &nt) {
+  const int total = tiles_m * tiles_n;
+  const int b = blockIdx.x;
+  const int xcd = b & 7, local = b >> 3;
+  const int base = total >> 3, rem = total & 7;
+  const int t = xcd * base + min(xcd, rem) + local;
+  mt = t % tiles_m;
+  nt = t / tiles_m;
+}
+
+__device__ __forceinline__ i32x4 load16(const int8_t *p) {
+  return *reinterpret_cast<const i32x4 *>(p);
+}
+
+// Canonical residue of one int32 accumulator of channel c (LUT or Barrett).
+__device__ __forceinline__ uint32_t reduce_acc(KGemmArgs &g, int c, int32_t v) {
+  const uint32_t m = static_cast<uint32_t>(g.mods.moduli[c]);
+  return c < g.lut_channels ? canon_i32_lut(v, g.lut + c * 1024, m, g.mods.c31[c])
+                            : canon_i32(v, m, g.mods.magic[c], g.mods.c31[c]);
+}
+
+// ---------------------------------------------------------------------------
+// Stream GEMM (small and medium M: decode, continuous batches, C2 shapes).
+// The bound is HBM latency: the weight residues are read once and the
+// problem is a few MB, so every wave issues all the loads of its K slice
+// before its first MFMA.  A workgroup owns a (16*MB) x (16*NB) output tile;
+// its waves split K (wave w takes K-step chunks w, w + KS, ... of U steps)
+// and each wave accumulates every channel.  Channel partial sums are reduced
+// mod m_c to canonical bytes in LDS ((sum of partials) mod m = (sum of
+// (partial mod m)) mod m), then each thread combines the slices of four
+// adjacent outputs, runs Garner and stores them.
+//
+// ARAW: A is one int8 matrix shared by every channel (an int8 activation is
+// its own representative mod every m_c, so the channel-c product of the raw
+// activations has the same residue as the product of the centered residues);
+// otherwise A holds one centered residue plane per channel.
+// ---------------------------------------------------------------------------
+// K steps per chunk of the stream kernel: as many as fit next to the
+// accumulators in 240 registers (two waves per SIMD), at most 4.
+constexpr int stream_u_of(int rcap, bool araw, int mb, int nb) {
+  const int frags = (araw ? 1 : rcap) * mb + rcap * nb;  // 16-byte loads per K step
+  const int u = (240 - 4 * rcap * mb * nb) / (4 * frags);
+  return u < 1 ? 1 : (u > 4 ? 4 : u);
+}
+
+template <int RCAP, int MB, int NB, bool ARAW>
+struct StreamCfg {
+  static constexpr int AP = ARAW ? 1 : RCAP;
+  static constexpr int U = stream_u_of(RCAP, ARAW, MB, NB);
+  static constexpr int TILE = 16 * MB * 16 * NB;
+};
+
+template <int RCAP, int MB, int NB, bool ARAW>
+__global__ __launch_bounds__(256) void gemm_stream_kernel(const GemmArgs args) {
+  KGemmArgs &g = kernel_args<GemmArgs>();
+  using Cfg = StreamCfg<RCAP, MB, NB, ARAW>;
+  constexpr int BM = 16 * MB, BN = 16 * NB, TILE = Cfg::TILE, AP = Cfg::AP, U = Cfg::U;
+  extern __shared__ __attribute__((aligned(16))) uint8_t sres[];  // [KS][RCAP][TILE]
+  __shared__ int64_t red[4];
+  __shared__ int bcast;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ks_n = blockDim.x >> 6;
+  const int c_act = active_channels<RCAP>(g, red, &bcast);
+  int mt, nt;
+  tile_of(g.tiles_m, g.tiles_n, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int nk = g.kp >> 6;
+  const int kofs = (lane >> 4) * 16;
+
+  const int8_t *ap[MB];
+  const int8_t *bp[NB];
+  static_for<MB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    const int row = min(m0 + i * 16 + (lane & 15), g.m - 1);
+    ap[i] = g.a + static_cast<int64_t>(row) * g.a_ld + kofs;
+  });
+  static_for<NB>([&](auto J) {
+    constexpr int j = decltype(J)::value;
+    const int col = min(n0 + j * 16 + (lane & 15), g.n - 1);
+    bp[j] = g.b + static_cast<int64_t>(col) * g.b_ld + kofs;
+  });
+
+  const i32x4 zero = {0, 0, 0, 0};
+  i32x4 acc[RCAP][MB][NB];
+  static_for<RCAP>([&](auto C) {
+    static_for<MB>([&](auto I) {
+      static_for<NB>([&](auto J) { acc[C][I][J] = zero; });
+    });
+  });
+
+  for (int q = wave * U; q < nk; q += ks_n * U) {
+    i32x4 fa[U][AP][MB], fb[U][RCAP][NB];
+    static_for<U>([&](auto UU) {
+      constexpr int u = decltype(UU)::value;
+      const int ks = q + u;
+      const bool kv = ks < nk;
+      const int ko = ks * 64;
+      const bool av = kv && (ko + kofs < g.a_k);
+      static_for<AP>([&](auto PP) {
+        constexpr int p = decltype(PP)::value;
+        static_for<MB>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          fa[u][p][i] = (av && p < c_act) ? load16(ap[i] + p * g.a_cs + ko) : zero;
+        });
+      });
+      static_for<RCAP>([&](auto C) {
+        constexpr int c = decltype(C)::value;
+        static_for<NB>([&](auto J) {
+          constexpr int j = decltype(J)::value;
+          fb[u][c][j] = (kv && c < c_act) ? load16(bp[j] + c * g.b_cs + ko) : zero;
+        });
+      });
+    });
+    static_for<U>([&](auto UU) {
+      constexpr int u = decltype(UU)::value;
+      static_for<RCAP>([&](auto C) {
+        constexpr int c = decltype(C)::value;
+        if (c >= c_act) return;
+        static_for<MB>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          static_for<NB>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][ARAW ? 0 : c][i], fb[u][c][j],
+                                                                 acc[c][i][j], 0, 0, 0);
+          });
+        });
+      });
+    });
+  }
+
+  // this wave's K slice: canonical residues, one byte per (channel, element)
+  uint8_t *mine = sres + wave * (RCAP * TILE);
+  static_for<RCAP>([&](auto C) {
+    constexpr int c = decltype(C)::value;
+    if (c >= c_act) return;
+    static_for<MB>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      static_for<NB>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        static_for<4>([&](auto T) {
+          constexpr int t = decltype(T)::value;
+          mine[c * TILE + (i * 16 + 4 * (lane >> 4) + t) * BN + j * 16 + (lane & 15)] =
+              static_cast<uint8_t>(reduce_acc(g, c, acc[c][i][j][t]));
+        });
+      });
+    });
+  });
+  __syncthreads();
+
+  // combine slices, Garner, store: each thread takes 4 adjacent columns
+  const int rows_here = min(BM, g.m - m0);
+  for (int e = threadIdx.x * 4; e < rows_here * BN; e += blockDim.x * 4) {
+    const int row = e / BN, col = e % BN;
+    uint32_t d[4][RCAP];
+    static_for<RCAP>([&](auto CC) {
+      constexpr int cc = decltype(CC)::value;
+      if (cc >= c_act) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) d[v][cc] = 0;
+        return;
+      }
+      // byte sums in 16-bit lanes: even bytes and odd bytes of the 4 outputs
+      uint32_t lo = 0, hi = 0;
+      for (int s = 0; s < ks_n; ++s) {
+        const uint32_t w = *reinterpret_cast<const uint32_t *>(sres + s * (RCAP * TILE) + cc * TILE + e);
+        lo += w & 0x00FF00FFu;
+        hi += (w >> 8) & 0x00FF00FFu;
+      }
+      const uint32_t sums[4] = {lo & 0xFFFFu, hi & 0xFFFFu, lo >> 16, hi >> 16};
+      const uint32_t m = static_cast<uint32_t>(g.mods.moduli[cc]);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const uint32_t r = mod_u32(sums[v], m, g.mods.magic[cc]);
+        d[v][cc] = garner_digit<cc>(g.mods, r, [&](int jj) { return d[v][jj]; });
+      }
+    });
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      if (n0 + col + v < g.n) store_element<RCAP>(g, c_act, d[v], m0 + row, n0 + col + v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA GEMM (large M: prefill, C4/C5 shapes).  Bound by MFMA throughput, so
+// operands are reused from registers and LDS.  A workgroup of 4 waves owns a
+// (16*MB) x (4*16*NB) tile: the A rows (shared by all waves, and in ARAW
+// mode by all channels) are staged through double-buffered LDS with rows
+// padded to 80 bytes (the 16-byte fragment reads of 16 lanes hit disjoint
+// banks); each wave owns 16*NB columns and streams their weight residues
+// straight from global memory into a P-deep register ring.  Every K step
+// feeds all channels, so all channel accumulators finish together and the
+// reduction + Garner + store run from registers.
 // ---------------------------------------------------------------------------
 constexpr int kLdsRow = 80;
 
-template <int RCAP, int BM, int BN>
-__global__ __launch_bounds__(256) void gemm_tile_kernel(const GemmArgs g) {
-  constexpr int WM = BM / 32, WN = BN / 32;
-  constexpr int AC = BM * 4 / 256, BC = BN * 4 / 256;  // 16-byte chunks per thread
-  static_assert(AC >= 1 && BC >= 1, "tile too small for 256 threads");
-  __shared__ __attribute__((aligned(16))) int8_t As[2][BM * kLdsRow];
-  __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN * kLdsRow];
+template <int RCAP, int MB, int NB, int P, bool ARAW>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(const GemmArgs args) {
+  KGemmArgs &g = kernel_args<GemmArgs>();
+  constexpr int BM = 16 * MB, BNW = 16 * NB;
+  constexpr int AP = ARAW ? 1 : RCAP;
+  constexpr int PLANE = BM * kLdsRow;
+  constexpr int ACH = AP * BM * 4;  // 16-byte A chunks per K step
+  constexpr int AC = (ACH + 255) / 256;
+  __shared__ __attribute__((aligned(16))) int8_t As[2][AP * PLANE];
   __shared__ int64_t red[4];
   __shared__ int bcast;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int c_act = active_channels(g, red, &bcast);
+  const int c_act = active_channels<RCAP>(g, red, &bcast);
+  int mt, nt;
+  tile_of(g.tiles_m, g.tiles_n, mt, nt);
+  const int m0 = mt * BM, n0 = nt * (4 * BNW) + wave * BNW;
   const int nk = g.kp >> 6;
+  const int kofs = (lane >> 4) * 16;
 
+  // A staging: chunk q -> plane p, row, 16-byte part
   const int8_t *asrc[AC];
-  const int8_t *bsrc[BC];
-  int alds[AC], blds[BC];
-#pragma unroll
-  for (int i = 0; i < AC; ++i) {
-    const int q = tid + 256 * i, row = q >> 2, part = q & 3;
+  int alds[AC], apart[AC];
+  bool aon[AC];
+  static_for<AC>([&](auto II) {
+    constexpr int i = decltype(II)::value;
+    const int q = tid + 256 * i;
+    aon[i] = q < ACH;
+    const int qq = aon[i] ? q : 0;
+    const int p = qq / (BM * 4), w = qq % (BM * 4), row = w >> 2, part = w & 3;
     const int grow = min(m0 + row, g.m - 1);
-    asrc[i] = g.a + grow * g.a_ld + part * 16;
-    alds[i] = row * kLdsRow + part * 16;
-  }
-#pragma unroll
-  for (int i = 0; i < BC; ++i) {
-    const int q = tid + 256 * i, row = q >> 2, part = q & 3;
-    const int gcol = min(n0 + row, g.n - 1);
-    bsrc[i] = g.b + gcol * g.b_ld + part * 16;
-    blds[i] = row * kLdsRow + part * 16;
-  }
-
-  i32x4 ra[AC], rb[BC];
-  auto gload = [&](int c, int ks) {
-    const int64_t aoff = c * g.a_cs + ks * 64, boff = c * g.b_cs + ks * 64;
-#pragma unroll
-    for (int i = 0; i < AC; ++i) ra[i] = *reinterpret_cast<const i32x4 *>(asrc[i] + aoff);
-#pragma unroll
-    for (int i = 0; i < BC; ++i) rb[i] = *reinterpret_cast<const i32x4 *>(bsrc[i] + boff);
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < AC; ++i) *reinterpret_cast<i32x4 *>(&As[buf][alds[i]]) = ra[i];
-#pragma unroll
-    for (int i = 0; i < BC; ++i) *reinterpret_cast<i32x4 *>(&Bs[buf][blds[i]]) = rb[i];
-  };
-
-  const int a_frag = (wm * (BM / 2) + (lane & 15)) * kLdsRow + (lane >> 4) * 16;
-  const int b_frag = (wn * (BN / 2) + (lane & 15)) * kLdsRow + (lane >> 4) * 16;
-
-  uint32_t dig[RCAP][WM * WN];
-  i32x4 acc[WM][WN];
-
-  gload(0, 0);
-  lstore(0);
-  __syncthreads();
-  int step = 0;
-
-  static_for<RCAP>([&](auto CC) {
-    constexpr int c = decltype(CC)::value;
-    if (c >= c_act) return;
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-      for (int j = 0; j < WN; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
-
-    for (int ks = 0; ks < nk; ++ks, ++step) {
-      const int buf = step & 1;
-      const bool last_k = (ks + 1 == nk);
-      const bool has_next = !last_k || (c + 1 < c_act);
-      if (has_next) gload(last_k ? c + 1 : c, last_k ? 0 : ks + 1);
-      i32x4 fa[WM], fb[WN];
-#pragma unroll
-      for (int i = 0; i < WM; ++i)
-        fa[i] = *reinterpret_cast<const i32x4 *>(&As[buf][a_frag + i * 16 * kLdsRow]);
-#pragma unroll
-      for (int j = 0; j < WN; ++j)
-        fb[j] = *reinterpret_cast<const i32x4 *>(&Bs[buf][b_frag + j * 16 * kLdsRow]);
-#pragma unroll
-      for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
-      if (has_next) lstore(buf ^ 1);
-      __syncthreads();
-    }
-
-    // channel epilogue: canonical residue -> Garner digit (bytes in dig[c])
-    const uint32_t m = static_cast<uint32_t>(g.mods.moduli[c]);
-    const uint32_t magic = g.mods.magic[c], c31 = g.mods.c31[c];
-    const bool use_lut = c < g.lut_channels;
-    const int16_t *lut = g.lut + c * 1024;
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-      for (int j = 0; j < WN; ++j) {
-        uint32_t packed = 0;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int32_t v = acc[i][j][t];
-          const uint32_t r = use_lut ? canon_i32_lut(v, lut, m, c31) : canon_i32(v, m, magic, c31);
-          const uint32_t d = garner_digit<c>(g.mods, r, [&](int jj) {
-            return byte_of(dig[jj][i * WN + j], t);
-          });
-          packed |= d << (8 * t);
-        }
-        dig[c][i * WN + j] = packed;
-      }
+    asrc[i] = g.a + p * g.a_cs + static_cast<int64_t>(grow) * g.a_ld + part * 16;
+    alds[i] = p * PLANE + row * kLdsRow + part * 16;
+    apart[i] = part * 16;
+    aon[i] = aon[i] && (ARAW || p < c_act);
+  });
+  const int8_t *bp[NB];
+  static_for<NB>([&](auto J) {
+    constexpr int j = decltype(J)::value;
+    const int col = min(n0 + j * 16 + (lane & 15), g.n - 1);
+    bp[j] = g.b + static_cast<int64_t>(col) * g.b_ld + kofs;
   });
 
-  // recombine and store
-#pragma unroll
-  for (int i = 0; i < WM; ++i)
-#pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int col = n0 + wn * (BN / 2) + j * 16 + (lane & 15);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + t;
-        if (row < g.m && col < g.n) {
-          uint32_t d[RCAP];
-#pragma unroll
-          for (int c = 0; c < RCAP; ++c) d[c] = byte_of(dig[c][i * WN + j], t);
-          store_element<RCAP>(g, c_act, d, row, col);
-        }
-      }
-    }
-}
+  const i32x4 zero = {0, 0, 0, 0};
+  i32x4 ra[AC];
+  i32x4 fb[P][RCAP][NB];
+  auto gload_a = [&](int ks) {
+    const int ko = ks * 64;
+    static_for<AC>([&](auto II) {
+      constexpr int i = decltype(II)::value;
+      ra[i] = (aon[i] && ko + apart[i] < g.a_k) ? load16(asrc[i] + ko) : zero;
+    });
+  };
+  auto lstore_a = [&](int buf) {
+    static_for<AC>([&](auto II) {
+      constexpr int i = decltype(II)::value;
+      if (aon[i]) *reinterpret_cast<i32x4 *>(&As[buf][alds[i]]) = ra[i];
+    });
+  };
 
-// ---------------------------------------------------------------------------
-// Skinny GEMM (M <= 16 * MB rows per workgroup; decode and small batches).
-// Waves are split over (channel, K slice): wave w owns channel w % R and K
-// slice w / R, loads its MFMA fragments straight from global memory (the
-// 16-byte K-contiguous layout makes each fragment one load) and keeps several
-// K steps of loads in flight.  Each wave reduces its partial sums mod m_c to
-// canonical bytes in LDS; (sum_s p_s) mod m = (sum_s (p_s mod m)) mod m, so
-// the slices combine with one more reduction.  All threads then run Garner
-// per output element and write coalesced rows.
-// ---------------------------------------------------------------------------
-template <int RCAP, int MB, int WN>
-__global__ __launch_bounds__(1024) void gemm_skinny_kernel(const GemmArgs g) {
-  constexpr int BMS = 16 * MB, BNS = 16 * WN;
-  constexpr int U = (MB + WN <= 3) ? 4 : 2;  // K steps in flight per wave
-  __shared__ uint8_t res[16][BMS * BNS];
-  __shared__ int64_t red[16];
-  __shared__ int bcast;
+  i32x4 acc[RCAP][MB][NB];
+  static_for<RCAP>([&](auto C) {
+    static_for<MB>([&](auto I) {
+      static_for<NB>([&](auto J) { acc[C][I][J] = zero; });
+    });
+  });
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nw = blockDim.x >> 6;
-  const int R = g.mods.channels;
-  const int ks_n = nw / R;
-  const int c = wave % R, s = wave / R;
-  const int c_act = active_channels(g, red, &bcast);
-  const int m0 = blockIdx.y * BMS, n0 = blockIdx.x * BNS;
-  const int nk = g.kp >> 6;
-
-  if (c < c_act && s < ks_n) {
-    const int k_begin = s * nk / ks_n, k_end = (s + 1) * nk / ks_n;
-    const int8_t *ap[MB];
-    const int8_t *bp[WN];
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-      const int row = min(m0 + i * 16 + (lane & 15), g.m - 1);
-      ap[i] = g.a + c * g.a_cs + row * g.a_ld + (lane >> 4) * 16;
+  gload_a(0);
+  lstore_a(0);
+  static_for<P>([&](auto SS) {
+    constexpr int s = decltype(SS)::value;
+    if (s < nk) {
+      static_for<RCAP>([&](auto C) {
+        constexpr int c = decltype(C)::value;
+        static_for<NB>([&](auto J) {
+          constexpr int j = decltype(J)::value;
+          fb[s][c][j] = c < c_act ? load16(bp[j] + c * g.b_cs + s * 64) : zero;
+        });
+      });
     }
-#pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int col = min(n0 + j * 16 + (lane & 15), g.n - 1);
-      bp[j] = g.b + c * g.b_cs + col * g.b_ld + (lane >> 4) * 16;
-    }
-    i32x4 acc[MB][WN];
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-      for (int j = 0; j < WN; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
-
-    int ks = k_begin;
-    for (; ks + U <= k_end; ks += U) {
-      i32x4 fa[U][MB], fb[U][WN];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int j = 0; j < WN; ++j)
-          fb[u][j] = *reinterpret_cast<const i32x4 *>(bp[j] + (ks + u) * 64);
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-          fa[u][i] = *reinterpret_cast<const i32x4 *>(ap[i] + (ks + u) * 64);
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-#pragma unroll
-          for (int j = 0; j < WN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][i], fb[u][j], acc[i][j], 0, 0, 0);
-    }
-    for (; ks < k_end; ++ks) {
-      i32x4 fa[MB], fb[WN];
-#pragma unroll
-      for (int j = 0; j < WN; ++j) fb[j] = *reinterpret_cast<const i32x4 *>(bp[j] + ks * 64);
-#pragma unroll
-      for (int i = 0; i < MB; ++i) fa[i] = *reinterpret_cast<const i32x4 *>(ap[i] + ks * 64);
-#pragma unroll
-      for (int i = 0; i < MB; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
-    }
-
-    const uint32_t m = static_cast<uint32_t>(g.mods.moduli[c]);
-    const uint32_t magic = g.mods.magic[c], c31 = g.mods.c31[c];
-    const bool use_lut = c < g.lut_channels;
-    const int16_t *lut = g.lut + c * 1024;
-    uint8_t *rw = res[wave];
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-      for (int j = 0; j < WN; ++j)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int32_t v = acc[i][j][t];
-          const uint32_t r = use_lut ? canon_i32_lut(v, lut, m, c31) : canon_i32(v, m, magic, c31);
-          rw[(i * 16 + 4 * (lane >> 4) + t) * BNS + j * 16 + (lane & 15)] = static_cast<uint8_t>(r);
-        }
-  }
+  });
   __syncthreads();
 
-  const int rows_here = min(BMS, g.m - m0);
-  for (int e = tid; e < rows_here * BNS; e += blockDim.x) {
-    const int row = e / BNS, col = e % BNS;
-    const int gcol = n0 + col;
-    if (gcol >= g.n) continue;
-    uint32_t d[RCAP];
-    static_for<RCAP>([&](auto CC) {
-      constexpr int cc = decltype(CC)::value;
-      if (cc >= c_act) {
-        d[cc] = 0;
-        return;
+  const int a_frag = (lane & 15) * kLdsRow + kofs;
+  for (int ks0 = 0; ks0 < nk; ks0 += P) {
+    static_for<P>([&](auto SS) {
+      constexpr int s = decltype(SS)::value;
+      const int ks = ks0 + s;
+      if (ks >= nk) return;
+      const int buf = ks & 1;
+      const bool more = ks + 1 < nk;
+      if (more) gload_a(ks + 1);
+      i32x4 fa[MB];
+      static_for<RCAP>([&](auto C) {
+        constexpr int c = decltype(C)::value;
+        if (c >= c_act) return;
+        if (!ARAW || c == 0) {
+          static_for<MB>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            fa[i] = *reinterpret_cast<const i32x4 *>(
+                &As[buf][(ARAW ? 0 : c) * PLANE + a_frag + i * 16 * kLdsRow]);
+          });
+        }
+        static_for<MB>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          static_for<NB>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[s][c][j], acc[c][i][j], 0, 0, 0);
+          });
+        });
+      });
+      if (ks + P < nk) {
+        static_for<RCAP>([&](auto C) {
+          constexpr int c = decltype(C)::value;
+          static_for<NB>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            fb[s][c][j] = c < c_act ? load16(bp[j] + c * g.b_cs + (ks + P) * 64) : zero;
+          });
+        });
       }
-      uint32_t sum = 0;
-      for (int s2 = 0; s2 < ks_n; ++s2) sum += res[s2 * R + cc][e];
-      const uint32_t m = static_cast<uint32_t>(g.mods.moduli[cc]);
-      const uint32_t r = mod_u32(sum, m, g.mods.magic[cc]);
-      d[cc] = garner_digit<cc>(g.mods, r, [&](int jj) { return d[jj]; });
+      if (more) lstore_a(buf ^ 1);
+      __syncthreads();
     });
-    store_element<RCAP>(g, c_act, d, m0 + row, gcol);
   }
+
+  // epilogue from registers: lane holds rows 4*(lane>>4)+t of column lane&15
+  static_for<MB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    static_for<NB>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      const int col = n0 + j * 16 + (lane & 15);
+      static_for<4>([&](auto T) {
+        constexpr int t = decltype(T)::value;
+        const int row = m0 + i * 16 + 4 * (lane >> 4) + t;
+        uint32_t d[RCAP];
+        static_for<RCAP>([&](auto CC) {
+          constexpr int cc = decltype(CC)::value;
+          if (cc >= c_act) {
+            d[cc] = 0;
+            return;
+          }
+          const uint32_t r = reduce_acc(g, cc, acc[cc][i][j][t]);
+          d[cc] = garner_digit<cc>(g.mods, r, [&](int jj) { return d[jj]; });
+        });
+        if (row < g.m && col < g.n) store_element<RCAP>(g, c_act, d, row, col);
+      });
+    });
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -491,7 +607,7 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(const EncodeArgs e) {
       l1 += a64;
       amax = static_cast<uint32_t>(a) > static_cast<uint32_t>(amax) ? a : amax;
     }
-    for (int c = 0; c < R; ++c) {
+    for (int c = 0; c < R && e.out != nullptr; ++c) {
       const uint32_t m = static_cast<uint32_t>(e.mods.moduli[c]);
       const uint32_t magic = e.mods.magic[c], c31 = e.mods.c31[c];
       i32x4 w;
@@ -599,7 +715,7 @@ __global__ __launch_bounds__(256) void decode_garner_kernel(const DecodeArgs a) 
 #pragma unroll
     for (int c = 0; c < RCAP; ++c)
       if (c < R) x += static_cast<uint64_t>(d[c]) * static_cast<uint64_t>(a.mods.prefix[c]);
-    const int64_t p = a.mods.prefix[R];
+    const int64_t p = prefix_at<RCAP>(a.mods, R);
     int64_t y = static_cast<int64_t>(x);
     if (y > (p >> 1)) y -= p;
     a.out[e] = y;
@@ -661,68 +777,132 @@ static int32_t check_launch(const char *what) {
   return RNSMX_OK;
 }
 
-template <int RCAP>
-static void launch_skinny(const GemmArgs &g, int mb, int wn, int waves, hipStream_t st) {
-  const dim3 block(64 * waves);
-#define RNSMX_SKINNY(MB_, WN_)                                                           \
-  if (mb == MB_ && wn == WN_) {                                                          \
-    const dim3 grid((g.n + 16 * WN_ - 1) / (16 * WN_), (g.m + 16 * MB_ - 1) / (16 * MB_)); \
-    hipLaunchKernelGGL((gemm_skinny_kernel<RCAP, MB_, WN_>), grid, block, 0, st, g);      \
-    return;                                                                              \
-  }
-  RNSMX_SKINNY(1, 1)
-  RNSMX_SKINNY(1, 2)
-  RNSMX_SKINNY(2, 1)
-  RNSMX_SKINNY(2, 2)
-  RNSMX_SKINNY(4, 1)
-  RNSMX_SKINNY(4, 2)
-#undef RNSMX_SKINNY
+enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2 };
+
+struct GemmChoice {
+  int kind, mb, nb, ks;
+};
+
+// Process-wide override of the kernel choice (rnsmx_set_gemm_override).
+static GemmChoice g_override = {kAuto, 0, 0, 0};
+
+static constexpr int kStreamLdsMax = 65536;
+
+static int stream_ks_cap(int rcap, int mb, int nb) {
+  const int per_wave = rcap * 256 * mb * nb;
+  return std::max(1, std::min(4, kStreamLdsMax / per_wave));
 }
 
-template <int RCAP>
-static void launch_tile(const GemmArgs &g, int bm, int bn, hipStream_t st) {
-  const dim3 block(256);
-#define RNSMX_TILE(BM_, BN_)                                                  \
-  if (bm == BM_ && bn == BN_) {                                               \
-    const dim3 grid((g.n + BN_ - 1) / BN_, (g.m + BM_ - 1) / BM_);            \
-    hipLaunchKernelGGL((gemm_tile_kernel<RCAP, BM_, BN_>), grid, block, 0, st, g); \
-    return;                                                                   \
+// Kernel family and tile for an M x N x kp problem.  Small M streams the
+// weights (stream kernel, K split over waves); large M is MFMA-bound (mfma
+// kernel, 128-row tiles for up to 4 channels).
+static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
+  const int rcap = rcap_for(g.mods.channels);
+  const int nk = g.kp / 64;
+  GemmChoice c{};
+  if (g.m <= 256) {
+    // 16- or 32-row tiles of 16 columns: the most workgroups in flight
+    c.kind = kStream;
+    c.mb = g.m <= 16 ? 1 : 2;
+    c.nb = 1;
+    const int u = stream_u_of(rcap, araw, c.mb, c.nb);
+    const int want = g.m <= 16 ? 4 : (g.m < 256 ? 2 : 1);
+    c.ks = std::min(std::min(want, stream_ks_cap(rcap, c.mb, c.nb)), std::max(1, (nk + u - 1) / u));
+    return c;
   }
-  RNSMX_TILE(64, 64)
+  c.kind = kMfma;
+  if (rcap <= 4) {
+    c.mb = 8;
+    c.nb = 2;
+  } else if (rcap == 6) {
+    c.mb = 4;
+    c.nb = 2;
+  } else {
+    c.mb = 2;
+    c.nb = 2;
+  }
+  return c;
+}
+
+template <int RCAP, bool ARAW>
+static bool launch_stream(GemmArgs g, int mb, int nb, int ks, hipStream_t st) {
+#define RNSMX_STREAM(MB_, NB_)                                                             \
+  if (mb == MB_ && nb == NB_) {                                                            \
+    g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                                         \
+    g.tiles_n = (g.n + 16 * NB_ - 1) / (16 * NB_);                                         \
+    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));                         \
+    const size_t lds = static_cast<size_t>(ks) * RCAP * StreamCfg<RCAP, MB_, NB_, ARAW>::TILE; \
+    hipLaunchKernelGGL((gemm_stream_kernel<RCAP, MB_, NB_, ARAW>), grid, dim3(64 * ks), lds, st, g); \
+    return true;                                                                           \
+  }
+  RNSMX_STREAM(1, 1)
+  RNSMX_STREAM(2, 1)
+  RNSMX_STREAM(4, 1)
   if constexpr (RCAP <= 4) {
-    RNSMX_TILE(128, 128)
+    RNSMX_STREAM(1, 2)
+    RNSMX_STREAM(1, 4)
+    RNSMX_STREAM(2, 2)
+    RNSMX_STREAM(4, 2)
   }
-#undef RNSMX_TILE
+#undef RNSMX_STREAM
+  return false;
 }
 
-// Chooses the kernel family and tile for an M x N x kp problem.
-static int32_t launch_gemm(const GemmArgs &g, hipStream_t st) {
-  const int R = g.mods.channels;
-  const int rc = rcap_for(R);
-  if (g.m <= 64) {
-    const int mb = g.m <= 16 ? 1 : (g.m <= 32 ? 2 : 4);
-    const int wn = 1;
-    const int nk = g.kp / 64;
-    int ks = std::max(1, 16 / R);
-    ks = std::min(ks, std::max(1, nk));
-    const int waves = R * ks;
-    switch (rc) {
-      case 3: launch_skinny<3>(g, mb, wn, waves, st); break;
-      case 4: launch_skinny<4>(g, mb, wn, waves, st); break;
-      case 6: launch_skinny<6>(g, mb, wn, waves, st); break;
-      default: launch_skinny<10>(g, mb, wn, waves, st); break;
+template <int RCAP, bool ARAW>
+static bool launch_mfma(GemmArgs g, int mb, int nb, hipStream_t st) {
+#define RNSMX_MFMA(MB_, NB_)                                                         \
+  if (mb == MB_ && nb == NB_) {                                                      \
+    g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                                   \
+    g.tiles_n = (g.n + 64 * NB_ - 1) / (64 * NB_);                                   \
+    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));                   \
+    hipLaunchKernelGGL((gemm_mfma_kernel<RCAP, MB_, NB_, 2, ARAW>), grid, dim3(256), 0, st, g); \
+    return true;                                                                     \
+  }
+  if constexpr (RCAP <= 4) {
+    RNSMX_MFMA(8, 2)
+    RNSMX_MFMA(4, 2)
+    RNSMX_MFMA(4, 4)
+  } else if constexpr (RCAP == 6) {
+    RNSMX_MFMA(4, 2)
+  } else {
+    RNSMX_MFMA(2, 2)
+  }
+#undef RNSMX_MFMA
+  return false;
+}
+
+template <int RCAP>
+static bool launch_rcap(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st) {
+  if (c.kind == kStream)
+    return araw ? launch_stream<RCAP, true>(g, c.mb, c.nb, c.ks, st)
+                : launch_stream<RCAP, false>(g, c.mb, c.nb, c.ks, st);
+  return araw ? launch_mfma<RCAP, true>(g, c.mb, c.nb, st) : launch_mfma<RCAP, false>(g, c.mb, c.nb, st);
+}
+
+// Launches the GEMM for `g`.  araw: A is one int8 matrix for all channels.
+static int32_t launch_gemm(const GemmArgs &g, bool araw, hipStream_t st) {
+  const int rcap = rcap_for(g.mods.channels);
+  GemmChoice c = g_override.kind != kAuto ? g_override : choose_gemm(g, araw);
+  if (c.kind == kStream) {
+    const int cap = stream_ks_cap(rcap, c.mb, c.nb);
+    if (c.ks < 1 || c.ks > cap) {
+      set_error("stream GEMM needs 1 <= ks <= %d for this tile", cap);
+      return RNSMX_EINVAL;
     }
-    return check_launch("gemm_skinny");
   }
-  const int64_t tiles128 = static_cast<int64_t>((g.m + 127) / 128) * ((g.n + 127) / 128);
-  const int t = (tiles128 >= 256 && rc <= 4) ? 128 : 64;
-  switch (rc) {
-    case 3: launch_tile<3>(g, t, t, st); break;
-    case 4: launch_tile<4>(g, t, t, st); break;
-    case 6: launch_tile<6>(g, t, t, st); break;
-    default: launch_tile<10>(g, t, t, st); break;
+  bool ok = false;
+  switch (rcap) {
+    case 3: ok = launch_rcap<3>(g, araw, c, st); break;
+    case 4: ok = launch_rcap<4>(g, araw, c, st); break;
+    case 6: ok = launch_rcap<6>(g, araw, c, st); break;
+    default: ok = launch_rcap<10>(g, araw, c, st); break;
   }
-  return check_launch("gemm_tile");
+  if (!ok) {
+    set_error("no GEMM kernel for kind %d, tile %d x %d, %d channels", c.kind, c.mb, c.nb,
+              g.mods.channels);
+    return RNSMX_EINVAL;
+  }
+  return check_launch(c.kind == kStream ? "gemm_stream" : "gemm_mfma");
 }
 
 static int32_t launch_encode_rows(int32_t dtype, const EncodeArgs &e, hipStream_t st) {
@@ -801,7 +981,9 @@ int32_t rnsmx_encode_centered(const void *values_dev, int32_t dtype, int64_t row
 int64_t rnsmx_fused_workspace_bytes(int64_t m, int64_t k, int64_t n, int32_t channels) {
   if (m < 0 || k < 0 || n < 0 || channels < 1) return -1;
   const int64_t kp = round_up(std::max<int64_t>(k, 1), RNSMX_K_ALIGN);
-  const int64_t a = (k % RNSMX_K_ALIGN == 0) ? 0 : round_up(channels * m * kp, 256);
+  // room for a padded copy of A (used when K % 16 != 0 or A is not 16-byte
+  // aligned) followed by B repacked to [R][N][kp]
+  const int64_t a = round_up(channels * m * kp, 256);
   const int64_t b = round_up(channels * n * kp, 256);
   return a + b;
 }
@@ -831,10 +1013,12 @@ int32_t rnsmx_matmul_centered_fused_out(const int8_t *a_dev, const int8_t *b_dev
   const int64_t kp = round_up(k, RNSMX_K_ALIGN);
   int8_t *ws = static_cast<int8_t *>(workspace_dev);
   const int8_t *a_use = a_dev;
-  int64_t a_ld = k;
-  if (k % RNSMX_K_ALIGN != 0 || !aligned16(a_dev)) {
+  int64_t a_ld = k, a_k = k;
+  int8_t *b_nk = ws + round_up(R * static_cast<int64_t>(m) * kp, 256);
+  if (k % 16 != 0 || !aligned16(a_dev)) {
+    // rows of 16-byte chunks are read straight from the caller's planes
+    // otherwise (chunks past K load as zero)
     int8_t *a_pad = ws;
-    ws += round_up(R * static_cast<int64_t>(m) * kp, 256);
     const int64_t total = R * static_cast<int64_t>(m) * kp;
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 16384));
     hipLaunchKernelGGL(pad_rows_kernel, dim3(blocks), dim3(256), 0, st, a_dev, static_cast<int64_t>(m),
@@ -842,8 +1026,8 @@ int32_t rnsmx_matmul_centered_fused_out(const int8_t *a_dev, const int8_t *b_dev
     if (int32_t rc = check_launch("pad_rows")) return rc;
     a_use = a_pad;
     a_ld = kp;
+    a_k = kp;
   }
-  int8_t *b_nk = ws;
   {
     const dim3 grid((n + 63) / 64, static_cast<unsigned>((kp + 63) / 64), R);
     hipLaunchKernelGGL(transpose_kn_kernel, grid, dim3(256), 0, st, b_dev, static_cast<int64_t>(k),
@@ -854,6 +1038,7 @@ int32_t rnsmx_matmul_centered_fused_out(const int8_t *a_dev, const int8_t *b_dev
   g.a = a_use;
   g.a_ld = a_ld;
   g.a_cs = a_ld * m;
+  g.a_k = static_cast<int32_t>(a_k);
   g.b = b_nk;
   g.b_ld = kp;
   g.b_cs = kp * n;
@@ -867,7 +1052,7 @@ int32_t rnsmx_matmul_centered_fused_out(const int8_t *a_dev, const int8_t *b_dev
   g.out_ld = n;
   g.out_dtype = RNSMX_INT64;
   g.mods = *mods;
-  return launch_gemm(g, st);
+  return launch_gemm(g, false, st);
 }
 
 int32_t rnsmx_prepare_weight(const void *b_nk_dev, int32_t dtype, int32_t n, int32_t k,
@@ -939,24 +1124,37 @@ int32_t rnsmx_matmul_prepared_fused(const void *a_dev, int32_t a_dtype, int32_t 
   const int64_t kp = round_up(k, RNSMX_K_ALIGN);
   int8_t *a_res = static_cast<int8_t *>(workspace_dev);
   int64_t *row_l1 = reinterpret_cast<int64_t *>(a_res + round_up(R * static_cast<int64_t>(m) * kp, 256));
+  if (!aligned16(a_dev)) return fail(RNSMX_EINVAL, "activations must be 16-byte aligned");
 
+  // int8 activations with 16-byte rows feed the MFMA directly (they are
+  // their own representatives mod every m_c); the encoder then only runs for
+  // the adaptive row L1 norms.  Other sources are encoded to residue planes.
+  const bool araw = a_dtype == RNSMX_INT8 && k % 16 == 0 && raw_accumulator_fits(*mods, k);
   EncodeArgs e{};
   e.values = a_dev;
   e.rows = m;
   e.cols = k;
   e.out_ld = kp;
   e.plane = static_cast<int64_t>(m) * kp;
-  e.out = a_res;
+  e.out = araw ? nullptr : a_res;
   e.row_l1 = min_ch != 0 ? row_l1 : nullptr;
   e.absmax = nullptr;
   e.mods = *mods;
-  if (!aligned16(a_dev)) return fail(RNSMX_EINVAL, "activations must be 16-byte aligned");
-  if (int32_t rc = launch_encode_rows(a_dtype, e, st)) return rc;
+  if (!araw || min_ch != 0)
+    if (int32_t rc = launch_encode_rows(a_dtype, e, st)) return rc;
 
   GemmArgs g{};
-  g.a = a_res;
-  g.a_ld = kp;
-  g.a_cs = kp * m;
+  if (araw) {
+    g.a = static_cast<const int8_t *>(a_dev);
+    g.a_ld = k;
+    g.a_cs = 0;
+    g.a_k = k;
+  } else {
+    g.a = a_res;
+    g.a_ld = kp;
+    g.a_cs = kp * m;
+    g.a_k = static_cast<int32_t>(kp);
+  }
   g.b = packed_dev;
   g.b_ld = kp;
   g.b_cs = kp * n;
@@ -976,7 +1174,7 @@ int32_t rnsmx_matmul_prepared_fused(const void *a_dev, int32_t a_dtype, int32_t 
   g.w_scale = epilogue ? epilogue->w_scale_dev : nullptr;
   g.bias = epilogue ? epilogue->bias_dev : nullptr;
   g.mods = *mods;
-  return launch_gemm(g, st);
+  return launch_gemm(g, araw, st);
 }
 
 int32_t rnsmx_matmul_residues_prepared(const int8_t *a_res_dev, int64_t a_ld, int32_t m, int32_t k,
@@ -1009,6 +1207,7 @@ int32_t rnsmx_matmul_residues_prepared(const int8_t *a_res_dev, int64_t a_ld, in
   g.a = a_res_dev;
   g.a_ld = a_ld;
   g.a_cs = a_ld * m;
+  g.a_k = static_cast<int32_t>(kp);
   g.b = packed_dev;
   g.b_ld = kp;
   g.b_cs = kp * n;
@@ -1025,7 +1224,19 @@ int32_t rnsmx_matmul_residues_prepared(const int8_t *a_res_dev, int64_t a_ld, in
   g.w_scale = epilogue ? epilogue->w_scale_dev : nullptr;
   g.bias = epilogue ? epilogue->bias_dev : nullptr;
   g.mods = *mods;
-  return launch_gemm(g, static_cast<hipStream_t>(stream));
+  return launch_gemm(g, false, static_cast<hipStream_t>(stream));
+}
+
+int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb, int32_t ks) {
+  clear_error();
+  if (kind == kAuto) {
+    g_override = GemmChoice{kAuto, 0, 0, 0};
+    return RNSMX_OK;
+  }
+  if (kind != kStream && kind != kMfma) return fail(RNSMX_EINVAL, "kind must be 0 (auto), 1 (stream) or 2 (mfma)");
+  if (mb < 1 || nb < 1) return fail(RNSMX_EINVAL, "tile blocks must be positive");
+  g_override = GemmChoice{kind, mb, nb, ks};
+  return RNSMX_OK;
 }
 
 int32_t rnsmx_decode_garner(const int8_t *residues_dev, int64_t count, const rnsmx_moduli_t *mods,

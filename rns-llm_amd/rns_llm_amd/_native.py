@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "rnsmx_prepared_workspace_bytes",
     "rnsmx_matmul_prepared_fused",
     "rnsmx_matmul_residues_prepared",
+    "rnsmx_set_gemm_override",
     "rnsmx_decode_garner",
 )
 
@@ -96,6 +97,7 @@ _SIGNATURES = {
     "rnsmx_matmul_residues_prepared": (
         _I32, [_P, _I64, _I32, _I32, _I32, _P, ctypes.POINTER(Moduli), _P, _I32,
                ctypes.POINTER(Epilogue), _P, _P]),
+    "rnsmx_set_gemm_override": (_I32, [_I32, _I32, _I32, _I32]),
     "rnsmx_decode_garner": (_I32, [_P, _I64, ctypes.POINTER(Moduli), _P, _P]),
 }
 
