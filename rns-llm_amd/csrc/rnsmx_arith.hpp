@@ -36,6 +36,44 @@ __device__ __forceinline__ uint32_t mod_u32(uint32_t x, uint32_t m, uint32_t mag
   return r >= m ? r - m : r;
 }
 
+// x mod m for 0 <= x < 2^24 with 24-bit multiplies (full rate on CDNA;
+// 32-bit integer multiplies are quarter rate).  m24 = floor(2^24 / m).
+// Writing 2^24/m = m24 + f with 0 <= f < 1, x*m24/2^24 = x/m - x*f/2^24 and
+// x*f/2^24 < 1, so q = floor(x*m24/2^24) is floor(x/m) or floor(x/m) - 1 and
+// x - q*m lies in [0, 2m): one conditional subtraction finishes.
+__device__ __forceinline__ uint32_t mod_small(uint32_t x, uint32_t m, uint32_t m24) {
+  const uint64_t p = static_cast<uint64_t>(x & 0xFFFFFFu) * static_cast<uint64_t>(m24 & 0xFFFFFFu);
+  const uint32_t q = static_cast<uint32_t>(p >> 24);
+  const uint32_t r = x - __umul24(q, m);
+  return r >= m ? r - m : r;
+}
+
+// Constants of the 24-bit reduction of one modulus, all derived from
+// magic = floor(2^32 / m) (floor(2^k / m) = magic >> (32 - k)).
+struct FastMod {
+  uint32_t m;     // modulus, 2 <= m <= 255
+  uint32_t m24;   // floor(2^24 / m)
+  uint32_t c16;   // 2^16 mod m
+  uint32_t bias;  // m * floor(2^23 / m), a multiple of m in (2^23 - m, 2^23]
+};
+
+__device__ __forceinline__ FastMod fast_mod_of(uint32_t m, uint32_t magic) {
+  return FastMod{m, magic >> 8, 65536u - (magic >> 16) * m, m * (magic >> 9)};
+}
+
+// Canonical residue in [0, m) of any int32 v.  v = hi * 2^16 + lo with
+// hi = v >> 16 in [-2^15, 2^15) and lo in [0, 2^16), so v = hi * c16 + lo
+// (mod m).  hi * c16 lies in [-32768 * 254, 32767 * 254]; adding
+// bias >= 2^23 - 255 > 32768 * 254 makes t non-negative, and
+// t <= 32767 * 254 + 65535 + 2^23 = 16,776,961 < 2^24, the domain of
+// mod_small.  Every multiply is 24-bit.
+__device__ __forceinline__ uint32_t canon_fast(int32_t v, const FastMod &f) {
+  const int32_t hi = v >> 16;
+  const uint32_t lo = static_cast<uint32_t>(v) & 0xFFFFu;
+  const uint32_t t = static_cast<uint32_t>(__mul24(hi, static_cast<int32_t>(f.c16))) + lo + f.bias;
+  return mod_small(t, f.m, f.m24);
+}
+
 // Canonical residue in [0, m) of a signed 32-bit value.
 __device__ __forceinline__ uint32_t canon_i32(int32_t v, uint32_t m, uint32_t magic,
                                               uint32_t c31) {

@@ -1,0 +1,875 @@
+// RNS GEMM kernels for gfx950 (MI355X): per-channel int8 products with the
+// modular reduction, Garner mixed-radix reconstruction, signed correction
+// and optional dequantization fused into the epilogue.
+//
+// Three families, chosen by the number of output rows M:
+//   gemv_kernel    M <= 8       one wave per output column, dot4 on VALU,
+//                               every channel's column read as one contiguous
+//                               run (weight streaming, HBM bound)
+//   stream_kernel  M <= 256     MFMA tiles of (16*MB) x (16*NB), K split over
+//                               the waves of a workgroup, every wave issuing
+//                               all loads of its K slice before its first MFMA
+//   mfma_kernel    M > 256      MFMA tiles of (16*MB) x (64*NB), A staged
+//                               through LDS, B streamed into a register ring,
+//                               P K steps of loads in flight (MFMA bound)
+//
+// Layouts: A is [M][a_ld] int8 activations shared by every channel (a_cs = 0;
+// an int8 value is its own representative mod every m_c, so the channel-c
+// product of raw activations has the residue of the product of centered
+// residues) or [R][M][a_ld] centered residue planes.  B is the prepared
+// weight [R][N][b_ld], K contiguous, zero padded to kp (a multiple of 64).
+//
+// MFMA v_mfma_i32_16x16x64_i8: lane l feeds A row (l & 15) and B column
+// (l & 15), both with K bytes [16 * (l >> 4), +16) of a 64-byte step, and
+// receives D rows 4 * (l >> 4) + t (t = 0..3) of column (l & 15).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <climits>
+
+#include "rnsmx_arith.hpp"
+#include "rnsmx_common.hpp"
+
+namespace rnsmx {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+struct GemmArgs {
+  const int8_t *a;  // [R][M][a_ld] residue planes, or [M][a_ld] int8 (a_cs = 0)
+  int64_t a_ld, a_cs;
+  const int8_t *b;  // [R][N][b_ld]
+  int64_t b_ld, b_cs;
+  int32_t m, n, kp;  // kp: multiple of 64, <= b_ld
+  int32_t a_k;       // A bytes per row that are read; 16-byte chunks at or past it load as 0
+  int32_t tiles_m, tiles_n;  // output tile grid (set at launch)
+  int32_t lut_channels;
+  const int16_t *lut;  // [R][4][256]
+  // adaptive prefix
+  int32_t min_channels;  // 0: all channels
+  const int64_t *row_l1;
+  const int32_t *w_absmax;
+  int64_t *meta;
+  // epilogue
+  void *out;
+  int64_t out_ld;
+  int32_t out_dtype;
+  const float *a_scale;
+  const float *w_scale;
+  const float *bias;
+  rnsmx_moduli_t mods;
+};
+
+enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kGemv = 3 };
+
+struct GemmChoice {
+  int kind, mb, nb, ks;  // gemv: mb = rows per wave (1, 2, 4, 8)
+};
+
+// Per channel-capacity launchers, one translation unit each.
+bool launch_gemm_r3(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st);
+bool launch_gemm_r4(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st);
+bool launch_gemm_r6(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st);
+bool launch_gemm_r10(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st);
+
+// Kernel arguments read in place from the kernarg segment (constant address
+// space, scalar loads).  A by-value struct parameter used as an ordinary
+// object can be copied whole into per-lane scratch memory by the compiler
+// (it does so for the larger GEMM instances); a reference to the segment
+// never is.  Valid for kernels whose only parameter is the struct, which
+// then sits at offset 0 of the segment.
+#define RNSMX_KARG(T) const __attribute__((address_space(4))) T
+template <typename T>
+__device__ __forceinline__ RNSMX_KARG(T) & kernel_args() {
+  return *(RNSMX_KARG(T) *)(__builtin_amdgcn_kernarg_segment_ptr());
+}
+typedef RNSMX_KARG(GemmArgs) KGemmArgs;
+
+__device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const int64_t o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ i32x4 load16(const int8_t *p) { return *reinterpret_cast<const i32x4 *>(p); }
+
+// prefix[idx] for a runtime idx <= RCAP, as a select chain over constant
+// indices: a runtime index into the kernel-argument block would make the
+// compiler copy the whole block to scratch memory.
+template <int RCAP, typename Mods>
+__device__ __forceinline__ int64_t prefix_at(const Mods &mods, int idx) {
+  int64_t p = mods.prefix[0];
+  static_for<RCAP + 1>([&](auto I) {
+    if (idx == decltype(I)::value) p = mods.prefix[decltype(I)::value];
+  });
+  return p;
+}
+
+// Number of moduli channels to use.  Without the adaptive prefix this is the
+// full set.  With it, every workgroup derives the same answer from the row
+// L1 norms written by the encoder and max|B| written at weight preparation:
+// bound = max_i sum_k |a_ik| * max|B| (adaptive.py:44-52); the answer is the
+// smallest c >= min_channels with 2 * bound < prod_{i<c} m_i
+// (adaptive.py:15-41), i.e. bound <= (P_c - 1) / 2.  When no prefix fits,
+// the full set is used and meta[3] flags the overflow (the reference raises
+// OverflowError on the host, which a device-side selector cannot).
+template <int RCAP>
+__device__ __forceinline__ int active_channels(KGemmArgs &g, int64_t *red, int *bcast) {
+  const int full = g.mods.channels;
+  if (g.min_channels <= 0) return full;
+  int64_t mx = 0;
+  for (int r = threadIdx.x; r < g.m; r += blockDim.x) {
+    const int64_t v = g.row_l1[r];
+    mx = v > mx ? v : mx;
+  }
+  mx = wave_max_i64(mx);
+  const int nw = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t best = 0;
+    for (int w = 0; w < nw; ++w) best = red[w] > best ? red[w] : best;
+    const int64_t wmax = *g.w_absmax;
+    const int64_t bound = (wmax != 0 && best > LLONG_MAX / wmax) ? LLONG_MAX : best * wmax;
+    int c = full, overflow = 1;
+    static_for<RCAP + 1>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if (overflow && i >= g.min_channels && i <= full && bound <= (g.mods.prefix[i] - 1) / 2) {
+        c = i;
+        overflow = 0;
+      }
+    });
+    *bcast = c;
+    if (g.meta != nullptr && blockIdx.x == 0) {
+      g.meta[0] = c;
+      g.meta[1] = bound;
+      g.meta[2] = (prefix_at<RCAP>(g.mods, c) - 1) / 2;
+      g.meta[3] = overflow;
+    }
+  }
+  __syncthreads();
+  return *bcast;
+}
+
+// Everything the epilogue needs, read from the kernel arguments once per
+// kernel and pinned in scalar registers (pin_epi) right after the first
+// global loads are issued: left to itself the compiler re-issues these
+// scalar loads at their first use in the epilogue, where each dependent
+// round of scalar-cache misses is exposed.
+template <int RCAP>
+struct Epi {
+  uint32_t m[RCAP], m24[RCAP], c16[RCAP], bias[RCAP], qinv[RCAP];
+  uint32_t u[RCAP][RCAP];  // u[j][c], j < c
+  int64_t prefix[RCAP + 1];
+  int64_t p_act;  // prefix[c_act], the modulus of the signed correction
+  int32_t lut_channels, out_dtype;
+  int64_t out_ld;
+  void *out;
+  const float *w_scale;
+  const float *bias_ptr;
+  float a_scale;
+};
+
+// Moduli constants of Epi from a moduli block (kernel arguments or a
+// by-value copy).
+template <int RCAP, typename Mods>
+__device__ __forceinline__ void fill_moduli(Epi<RCAP> &e, const Mods &mods, int c_act) {
+  static_for<RCAP>([&](auto C) {
+    constexpr int c = decltype(C)::value;
+    const uint32_t m = static_cast<uint32_t>(mods.moduli[c]), magic = mods.magic[c];
+    e.m[c] = m;
+    e.qinv[c] = mods.qinv[c];
+    static_for<c>([&](auto J) { e.u[decltype(J)::value][c] = mods.ucoef[decltype(J)::value][c]; });
+    // the 24-bit reduction constants (see canon_fast); channels past the
+    // set's size have m = 0 and are never used
+    e.m24[c] = magic >> 8;
+    e.c16[c] = 65536u - (magic >> 16) * m;
+    e.bias[c] = m * (magic >> 9);
+  });
+  static_for<RCAP + 1>([&](auto C) { e.prefix[decltype(C)::value] = mods.prefix[decltype(C)::value]; });
+  e.p_act = prefix_at<RCAP>(mods, c_act);
+}
+
+template <int RCAP>
+__device__ __forceinline__ void load_epi(KGemmArgs &g, Epi<RCAP> &e, int c_act) {
+  fill_moduli<RCAP>(e, g.mods, c_act);
+  e.lut_channels = g.lut_channels;
+  e.out_dtype = g.out_dtype;
+  e.out_ld = g.out_ld;
+  e.out = g.out;
+  e.w_scale = g.w_scale;
+  e.bias_ptr = g.bias;
+  e.a_scale = g.out_dtype != RNSMX_INT64 ? *g.a_scale : 0.0f;
+}
+
+template <typename T>
+__device__ __forceinline__ void pin_sgpr(T &v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values only");
+  if constexpr (sizeof(T) == 4) {
+    uint32_t w = __builtin_bit_cast(uint32_t, v);
+    w = __builtin_amdgcn_readfirstlane(w);
+    asm volatile("" : "+s"(w));
+    v = __builtin_bit_cast(T, w);
+  } else {
+    uint64_t w = __builtin_bit_cast(uint64_t, v);
+    uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(w));
+    uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(w >> 32));
+    asm volatile("" : "+s"(lo), "+s"(hi));
+    v = __builtin_bit_cast(T, (static_cast<uint64_t>(hi) << 32) | lo);
+  }
+}
+
+template <int RCAP>
+__device__ __forceinline__ void pin_epi(Epi<RCAP> &e) {
+  static_for<RCAP>([&](auto C) {
+    constexpr int c = decltype(C)::value;
+    pin_sgpr(e.m[c]);
+    pin_sgpr(e.m24[c]);
+    pin_sgpr(e.c16[c]);
+    pin_sgpr(e.bias[c]);
+    pin_sgpr(e.qinv[c]);
+    static_for<c>([&](auto J) { pin_sgpr(e.u[decltype(J)::value][c]); });
+  });
+  static_for<RCAP + 1>([&](auto C) { pin_sgpr(e.prefix[decltype(C)::value]); });
+  pin_sgpr(e.p_act);
+  pin_sgpr(e.out_ld);
+  pin_sgpr(e.out);
+  pin_sgpr(e.lut_channels);
+  pin_sgpr(e.out_dtype);
+  pin_sgpr(e.a_scale);
+  pin_sgpr(e.w_scale);
+  pin_sgpr(e.bias_ptr);
+}
+
+// Canonical residue of one int32 accumulator of channel c: the byte table
+// for the first lut_channels channels (reference semantics, the same
+// residue), the 24-bit reduction otherwise.
+template <int RCAP>
+__device__ __forceinline__ uint32_t reduce_acc(KGemmArgs &g, const Epi<RCAP> &e, int c, int32_t v) {
+  if (c < e.lut_channels) return canon_i32_lut(v, g.lut + c * 1024, e.m[c], g.mods.c31[c]);
+  return canon_fast(v, FastMod{e.m[c], e.m24[c], e.c16[c], e.bias[c]});
+}
+
+// Signed integer from the canonical residues r[0..c_act) of the first c_act
+// channels.  Mixed-radix digits d_c = (r_c * q_c + sum_{j<c} d_j * u_{j,c})
+// mod m_c with q_c = P_c^-1 mod m_c and u_{j,c} = -P_j q_c mod m_c
+// (P_c = prod_{j<c} m_j): the same unique digits as the reference's
+// pairwise-inverse recurrence (csrc/rns_cuda.cu:389-400) with one reduction
+// per digit.  Every term is below 2^16 and there are at most 10, so each sum
+// is below 2^24 (24-bit multiplies, mod_small).  x = sum d_c P_c: for c < 4,
+// P_c <= 255^3 < 2^24 and the partial sums stay below P_4 <= 255^4 < 2^32,
+// so they accumulate in 32 bits; later digits in 64 bits.  x > P/2 maps to
+// x - P (P = P_{c_act}), the reference's signed correction.
+template <int RCAP>
+__device__ __forceinline__ int64_t garner_value(const Epi<RCAP> &e, const uint32_t (&r)[RCAP], int c_act) {
+  uint32_t d[RCAP];
+  uint32_t x32 = 0;
+  uint64_t x64 = 0;
+  static_for<RCAP>([&](auto C) {
+    constexpr int c = decltype(C)::value;
+    if (c >= c_act) {
+      d[c] = 0;
+      return;
+    }
+    if constexpr (c == 0) {
+      d[0] = r[0];  // q_0 = 1 and r_0 < m_0
+    } else {
+      uint32_t s = __umul24(r[c], e.qinv[c]);
+      static_for<c>([&](auto J) { s += __umul24(d[decltype(J)::value], e.u[decltype(J)::value][c]); });
+      d[c] = mod_small(s, e.m[c], e.m24[c]);
+    }
+    if constexpr (c < 4) {
+      x32 += __umul24(d[c], static_cast<uint32_t>(e.prefix[c]));
+    } else {
+      x64 += static_cast<uint64_t>(d[c]) * static_cast<uint64_t>(e.prefix[c]);
+    }
+  });
+  const int64_t p = e.p_act;
+  int64_t y = static_cast<int64_t>(static_cast<uint64_t>(x32) + x64);
+  if (y > (p >> 1)) y -= p;
+  return y;
+}
+
+// Writes one output element in the requested type.  The float chain is
+// ((float)y * a_scale) * w_scale[col] + bias[col], each step rounded to
+// nearest even with no contraction: the op order of rns_linear.py:272-275.
+template <int RCAP>
+__device__ __forceinline__ void store_value(const Epi<RCAP> &e, int64_t y, int row, int col) {
+  const int64_t idx = static_cast<int64_t>(row) * e.out_ld + col;
+  if (e.out_dtype == RNSMX_INT64) {
+    static_cast<int64_t *>(e.out)[idx] = y;
+    return;
+  }
+  float f = __ll2float_rn(y);
+  f = __fmul_rn(f, e.a_scale);
+  f = __fmul_rn(f, e.w_scale[col]);
+  if (e.bias_ptr != nullptr) f = __fadd_rn(f, e.bias_ptr[col]);
+  if (e.out_dtype == RNSMX_FLOAT32) {
+    static_cast<float *>(e.out)[idx] = f;
+  } else if (e.out_dtype == RNSMX_FLOAT16) {
+    static_cast<__half *>(e.out)[idx] = __float2half_rn(f);
+  } else {
+    static_cast<uint16_t *>(e.out)[idx] = f32_to_bf16_rne(f);
+  }
+}
+
+// Reduction + reconstruction + store of one element from its channel sums.
+template <int RCAP>
+__device__ __forceinline__ void finish_element(KGemmArgs &g, const Epi<RCAP> &e, int c_act,
+                                               const int32_t (&v)[RCAP], int row, int col) {
+  uint32_t r[RCAP];
+  static_for<RCAP>([&](auto C) {
+    constexpr int c = decltype(C)::value;
+    r[c] = c < c_act ? reduce_acc<RCAP>(g, e, c, v[c]) : 0u;
+  });
+  store_value<RCAP>(e, garner_value<RCAP>(e, r, c_act), row, col);
+}
+
+// Byte offset of channel c's plane with the channel clamped to a valid one:
+// loads of channels at or past the active count read channel 0 again (their
+// products are never used), so every load in the main loops is
+// unconditional.  Loads under a branch or an execution mask make the
+// compiler wait for every outstanding load at the join, which empties the
+// prefetch pipeline.
+__device__ __forceinline__ int64_t plane_off(int c, int c_act, int64_t stride) {
+  return (c < c_act ? c : 0) * stride;
+}
+
+__device__ __forceinline__ i32x4 select16(bool keep, i32x4 v) {
+  const i32x4 zero = {0, 0, 0, 0};
+  return keep ? v : zero;
+}
+
+// Workgroup -> output tile.  Workgroups are handed to the 8 XCDs round-robin
+// (workgroup b runs on XCD b % 8), and each XCD has its own L2.  Tiles are
+// numbered M-block fastest, so giving every XCD one contiguous run of tile
+// numbers keeps the workgroups that read the same weight columns on the
+// same L2.  The map is a bijection on [0, tiles) for any tile count.
+__device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int &mt, int &nt) {
+  const int total = tiles_m * tiles_n;
+  const int b = blockIdx.x;
+  const int xcd = b & 7, local = b >> 3;
+  const int base = total >> 3, rem = total & 7;
+  const int t = xcd * base + min(xcd, rem) + local;
+  mt = t % tiles_m;
+  nt = t / tiles_m;
+}
+
+// ---------------------------------------------------------------------------
+// GEMV (M <= MR <= 8).  Each wave owns one output column: lane l reads the
+// 16-byte K chunks l, l + 64, ... of that column in every channel (a
+// contiguous run of kp bytes per channel, fully coalesced) and the matching
+// A chunks of every row, accumulating with v_dot4 (4 int8 products per lane
+// per instruction).  U batches of chunks are loaded before any arithmetic.
+// A butterfly sum gives every lane the full dot products; lane r then
+// reconstructs and stores row r.
+// ---------------------------------------------------------------------------
+constexpr int gemv_u_of(int rcap, int mr, bool araw) {
+  const int frags = rcap + (araw ? 1 : rcap) * mr;
+  const int u = 48 / frags;
+  return u < 1 ? 1 : (u > 4 ? 4 : u);
+}
+
+template <int RCAP, int MR, bool ARAW>
+__global__ __launch_bounds__(256) void gemv_kernel(const GemmArgs args) {
+  KGemmArgs &g = kernel_args<GemmArgs>();
+  constexpr int AP = ARAW ? 1 : RCAP;
+  constexpr int U = gemv_u_of(RCAP, MR, ARAW);
+  __shared__ int64_t red[4];
+  __shared__ int bcast;
+  const int c_act = active_channels<RCAP>(g, red, &bcast);
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = min(static_cast<int>(blockIdx.x) * 4 + wave, g.n - 1);  // clamped; stored only if in range
+  const bool col_ok = static_cast<int>(blockIdx.x) * 4 + wave < g.n;
+  const int nchunk = g.kp >> 4;
+  const int a_chunks = g.a_k >> 4;
+  const int8_t *bcol = g.b + static_cast<int64_t>(col) * g.b_ld;
+  int64_t boff[RCAP], aoff[AP];
+  static_for<RCAP>([&](auto C) { boff[decltype(C)::value] = plane_off(decltype(C)::value, c_act, g.b_cs); });
+  static_for<AP>([&](auto PP) { aoff[decltype(PP)::value] = plane_off(decltype(PP)::value, c_act, g.a_cs); });
+  const int8_t *arow[MR];
+  static_for<MR>([&](auto R) {
+    constexpr int r = decltype(R)::value;
+    arow[r] = g.a + static_cast<int64_t>(min(r, g.m - 1)) * g.a_ld;
+  });
+  int32_t acc[RCAP][MR];
+  static_for<RCAP>([&](auto C) { static_for<MR>([&](auto R) { acc[C][R] = 0; }); });
+
+  Epi<RCAP> e;
+  load_epi<RCAP>(g, e, c_act);
+  pin_epi<RCAP>(e);
+  for (int q0 = 0; q0 < nchunk; q0 += 64 * U) {
+    i32x4 fb[U][RCAP], fa[U][AP][MR];
+    static_for<U>([&](auto UU) {
+      constexpr int u = decltype(UU)::value;
+      const int q = q0 + lane + 64 * u;
+      const int qb = min(q, nchunk - 1), qa = min(q, a_chunks - 1);
+      const bool av = q < a_chunks;  // a_chunks <= nchunk
+      static_for<RCAP>([&](auto C) {
+        constexpr int c = decltype(C)::value;
+        fb[u][c] = load16(bcol + boff[c] + qb * 16);
+      });
+      static_for<AP>([&](auto PP) {
+        constexpr int p = decltype(PP)::value;
+        static_for<MR>([&](auto R) {
+          constexpr int r = decltype(R)::value;
+          fa[u][p][r] = select16(av, load16(arow[r] + aoff[p] + qa * 16));
+        });
+      });
+    });
+    static_for<U>([&](auto UU) {
+      constexpr int u = decltype(UU)::value;
+      static_for<RCAP>([&](auto C) {
+        constexpr int c = decltype(C)::value;
+        if (c >= c_act) return;
+        static_for<MR>([&](auto R) {
+          constexpr int r = decltype(R)::value;
+          const i32x4 a = fa[u][ARAW ? 0 : c][r], b = fb[u][c];
+          int32_t s = acc[c][r];
+          s = __builtin_amdgcn_sdot4(a.x, b.x, s, false);
+          s = __builtin_amdgcn_sdot4(a.y, b.y, s, false);
+          s = __builtin_amdgcn_sdot4(a.z, b.z, s, false);
+          s = __builtin_amdgcn_sdot4(a.w, b.w, s, false);
+          acc[c][r] = s;
+        });
+      });
+    });
+  }
+
+  static_for<RCAP>([&](auto C) {
+    constexpr int c = decltype(C)::value;
+    if (c >= c_act) return;
+    static_for<MR>([&](auto R) { acc[c][decltype(R)::value] = wave_sum_i32(acc[c][decltype(R)::value]); });
+  });
+  if (col_ok && lane < MR && lane < g.m) {
+    int32_t v[RCAP];
+    static_for<RCAP>([&](auto C) {
+      constexpr int c = decltype(C)::value;
+      v[c] = acc[c][0];
+      static_for<MR>([&](auto R) {
+        if (lane == decltype(R)::value) v[c] = acc[c][decltype(R)::value];
+      });
+    });
+    finish_element<RCAP>(g, e, c_act, v, lane, col);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Stream GEMM (M <= 256: continuous batches and the C2 shapes).  The weight
+// residues are read once and the problem is a few MB, so latency rules:
+// every wave issues all the loads of a chunk of U K steps before its first
+// MFMA.  A workgroup owns a (16*MB) x (16*NB) output tile; its KS waves
+// split K (wave w takes chunks w, w + KS, ... of U steps) and each wave
+// accumulates every channel.  With KS > 1 the int32 partial sums meet in LDS
+// (atomic adds: a sum of partial sums over disjoint K ranges is the full
+// accumulator, which fits int32); each element is then reduced once.  With
+// KS = 1 the epilogue runs straight from the MFMA registers.
+// ---------------------------------------------------------------------------
+// K steps per chunk: as many as fit next to the accumulators in 240
+// registers (two waves per SIMD), at most 4.
+constexpr int stream_u_of(int rcap, bool araw, int mb, int nb) {
+  const int frags = (araw ? 1 : rcap) * mb + rcap * nb;  // 16-byte loads per K step
+  const int u = (240 - 4 * rcap * mb * nb) / (4 * frags);
+  return u < 1 ? 1 : (u > 4 ? 4 : u);
+}
+
+template <int RCAP, int MB, int NB, bool ARAW>
+__global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
+  KGemmArgs &g = kernel_args<GemmArgs>();
+  constexpr int BM = 16 * MB, BN = 16 * NB, TILE = BM * BN;
+  constexpr int AP = ARAW ? 1 : RCAP;
+  constexpr int U = stream_u_of(RCAP, ARAW, MB, NB);
+  extern __shared__ __attribute__((aligned(16))) int32_t sacc[];  // [RCAP][TILE] when KS > 1
+  __shared__ int64_t red[4];
+  __shared__ int bcast;
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ks_n = blockDim.x >> 6;
+  const int c_act = active_channels<RCAP>(g, red, &bcast);
+  int mt, nt;
+  tile_of(g.tiles_m, g.tiles_n, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int nk = g.kp >> 6;
+  const int kofs = (lane >> 4) * 16;
+
+  const int8_t *ap[MB];
+  const int8_t *bp[NB];
+  static_for<MB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    const int row = min(m0 + i * 16 + (lane & 15), g.m - 1);
+    ap[i] = g.a + static_cast<int64_t>(row) * g.a_ld;
+  });
+  static_for<NB>([&](auto J) {
+    constexpr int j = decltype(J)::value;
+    const int col = min(n0 + j * 16 + (lane & 15), g.n - 1);
+    bp[j] = g.b + static_cast<int64_t>(col) * g.b_ld + kofs;
+  });
+  int64_t boff[RCAP], aoff[AP];
+  static_for<RCAP>([&](auto C) { boff[decltype(C)::value] = plane_off(decltype(C)::value, c_act, g.b_cs); });
+  static_for<AP>([&](auto PP) { aoff[decltype(PP)::value] = plane_off(decltype(PP)::value, c_act, g.a_cs); });
+
+  const i32x4 zero = {0, 0, 0, 0};
+  i32x4 acc[RCAP][MB][NB];
+  static_for<RCAP>([&](auto C) {
+    static_for<MB>([&](auto I) { static_for<NB>([&](auto J) { acc[C][I][J] = zero; }); });
+  });
+
+  Epi<RCAP> e;
+  load_epi<RCAP>(g, e, c_act);
+  pin_epi<RCAP>(e);
+  for (int q = wave * U; q < nk; q += ks_n * U) {
+    i32x4 fa[U][AP][MB], fb[U][RCAP][NB];
+    static_for<U>([&](auto UU) {
+      constexpr int u = decltype(UU)::value;
+      const int ks = min(q + u, nk - 1);
+      const int ka = ks * 64 + kofs;
+      const bool av = (q + u < nk) && (ka < g.a_k);
+      const int kac = min(ka, g.a_k - 16);
+      static_for<AP>([&](auto PP) {
+        constexpr int p = decltype(PP)::value;
+        static_for<MB>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          fa[u][p][i] = select16(av, load16(ap[i] + aoff[p] + kac));
+        });
+      });
+      static_for<RCAP>([&](auto C) {
+        constexpr int c = decltype(C)::value;
+        static_for<NB>([&](auto J) {
+          constexpr int j = decltype(J)::value;
+          fb[u][c][j] = load16(bp[j] + boff[c] + ks * 64);
+        });
+      });
+    });
+    static_for<U>([&](auto UU) {
+      constexpr int u = decltype(UU)::value;
+      static_for<RCAP>([&](auto C) {
+        constexpr int c = decltype(C)::value;
+        if (c >= c_act) return;
+        static_for<MB>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          static_for<NB>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][ARAW ? 0 : c][i], fb[u][c][j],
+                                                                 acc[c][i][j], 0, 0, 0);
+          });
+        });
+      });
+    });
+  }
+
+  if (ks_n == 1) {
+    static_for<MB>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      static_for<NB>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        const int col = n0 + j * 16 + (lane & 15);
+        static_for<4>([&](auto T) {
+          constexpr int t = decltype(T)::value;
+          const int row = m0 + i * 16 + 4 * (lane >> 4) + t;
+          if (row < g.m && col < g.n) {
+            int32_t v[RCAP];
+            static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
+            finish_element<RCAP>(g, e, c_act, v, row, col);
+          }
+        });
+      });
+    });
+    return;
+  }
+
+  for (int i = threadIdx.x; i < RCAP * TILE; i += blockDim.x) sacc[i] = 0;
+  __syncthreads();
+  static_for<RCAP>([&](auto C) {
+    constexpr int c = decltype(C)::value;
+    if (c >= c_act) return;
+    static_for<MB>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      static_for<NB>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        static_for<4>([&](auto T) {
+          constexpr int t = decltype(T)::value;
+          atomicAdd(&sacc[c * TILE + (i * 16 + 4 * (lane >> 4) + t) * BN + j * 16 + (lane & 15)],
+                    acc[c][i][j][t]);
+        });
+      });
+    });
+  });
+  __syncthreads();
+
+  // each thread finishes 4 adjacent columns of one row
+  const int rows_here = min(BM, g.m - m0);
+  for (int x = threadIdx.x * 4; x < rows_here * BN; x += blockDim.x * 4) {
+    const int row = x / BN, col = x % BN;
+    i32x4 sv[RCAP];
+    static_for<RCAP>([&](auto C) {
+      constexpr int c = decltype(C)::value;
+      sv[c] = *reinterpret_cast<const i32x4 *>(&sacc[c * TILE + x]);
+    });
+    static_for<4>([&](auto V) {
+      constexpr int v4 = decltype(V)::value;
+      if (n0 + col + v4 < g.n) {
+        int32_t v[RCAP];
+        static_for<RCAP>([&](auto C) { v[decltype(C)::value] = sv[decltype(C)::value][v4]; });
+        finish_element<RCAP>(g, e, c_act, v, m0 + row, n0 + col + v4);
+      }
+    });
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA GEMM (M > 256: prefill, C4/C5 shapes), bound by MFMA throughput.  A
+// workgroup of 4 waves owns a (16*MB) x (4*16*NB) tile: the A rows (shared by
+// all waves, and in raw mode by all channels) pass through a P-deep register
+// ring into double-buffered LDS with rows padded to 80 bytes (the 16-byte
+// fragment reads of 16 lanes hit disjoint banks); each wave owns 16*NB
+// columns and streams their weight residues straight from global memory into
+// a P-deep register ring.  Loads of K step ks + P are issued while step ks
+// computes; the loop runs a multiple of P steps with the steps past K fed
+// zero A rows, so it has no branch around a load.  Every K step feeds all
+// channels, so all channel accumulators finish together and the reduction +
+// Garner + store run from registers.
+// ---------------------------------------------------------------------------
+constexpr int kLdsRow = 80;
+
+constexpr int mfma_ac_of(int rcap, int mb, bool araw) {
+  const int chunks = (araw ? 1 : rcap) * 16 * mb * 4;
+  return (chunks + 255) / 256;
+}
+
+// Ring depth: as many K steps of A and B loads as fit in ~220 VGPRs beside
+// the A fragments and addressing, between 2 and 4.
+constexpr int mfma_p_of(int rcap, int mb, int nb, bool araw) {
+  const int per_step = 4 * (rcap * nb + mfma_ac_of(rcap, mb, araw));
+  const int p = (220 - 40 - 4 * mb) / per_step;
+  return p < 2 ? 2 : (p > 4 ? 4 : p);
+}
+
+template <int RCAP, int MB, int NB, bool ARAW>
+__global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
+  KGemmArgs &g = kernel_args<GemmArgs>();
+  constexpr int BM = 16 * MB, BNW = 16 * NB;
+  constexpr int AP = ARAW ? 1 : RCAP;
+  constexpr int PLANE = BM * kLdsRow;
+  constexpr int ACH = AP * BM * 4;  // 16-byte A chunks per K step
+  constexpr int AC = mfma_ac_of(RCAP, MB, ARAW);
+  constexpr int P = mfma_p_of(RCAP, MB, NB, ARAW);
+  // one spare 16-byte slot takes the stores of threads without an A chunk
+  __shared__ __attribute__((aligned(16))) int8_t As[2][AP * PLANE + 16];
+  __shared__ int64_t red[4];
+  __shared__ int bcast;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c_act = active_channels<RCAP>(g, red, &bcast);
+  int mt, nt;
+  tile_of(g.tiles_m, g.tiles_n, mt, nt);
+  const int m0 = mt * BM, n0 = nt * (4 * BNW) + wave * BNW;
+  const int nk = g.kp >> 6;
+  const int kofs = (lane >> 4) * 16;
+
+  // A staging: chunk q -> plane p, row, 16-byte part
+  const int8_t *asrc[AC];
+  int alds[AC], apart[AC];
+  bool aon[AC];
+  static_for<AC>([&](auto II) {
+    constexpr int i = decltype(II)::value;
+    const int q = tid + 256 * i;
+    const bool inside = q < ACH;
+    const int qq = inside ? q : 0;
+    const int p = qq / (BM * 4), w = qq % (BM * 4), row = w >> 2, part = w & 3;
+    const int grow = min(m0 + row, g.m - 1);
+    asrc[i] = g.a + plane_off(p, c_act, g.a_cs) + static_cast<int64_t>(grow) * g.a_ld;
+    alds[i] = inside ? p * PLANE + row * kLdsRow + part * 16 : AP * PLANE;
+    apart[i] = part * 16;
+    aon[i] = inside && (ARAW || p < c_act);
+  });
+  const int8_t *bp[NB];
+  static_for<NB>([&](auto J) {
+    constexpr int j = decltype(J)::value;
+    const int col = min(n0 + j * 16 + (lane & 15), g.n - 1);
+    bp[j] = g.b + static_cast<int64_t>(col) * g.b_ld + kofs;
+  });
+  int64_t boff[RCAP];
+  static_for<RCAP>([&](auto C) { boff[decltype(C)::value] = plane_off(decltype(C)::value, c_act, g.b_cs); });
+
+  const i32x4 zero = {0, 0, 0, 0};
+  i32x4 ra[P][AC];
+  i32x4 fb[P][RCAP][NB];
+  // loads of K step ks (clamped to the last one; A of steps past K is zero)
+  auto gload = [&](auto SLOT, int ks) {
+    constexpr int s = decltype(SLOT)::value;
+    const int kc = min(ks, nk - 1);
+    static_for<AC>([&](auto II) {
+      constexpr int i = decltype(II)::value;
+      const int ka = kc * 64 + apart[i];
+      const bool keep = aon[i] && ks < nk && ka < g.a_k;
+      ra[s][i] = select16(keep, load16(asrc[i] + min(ka, g.a_k - 16)));
+    });
+    static_for<RCAP>([&](auto C) {
+      constexpr int c = decltype(C)::value;
+      static_for<NB>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        fb[s][c][j] = load16(bp[j] + boff[c] + kc * 64);
+      });
+    });
+  };
+  auto lstore = [&](auto SLOT, int buf) {
+    constexpr int s = decltype(SLOT)::value;
+    static_for<AC>([&](auto II) {
+      constexpr int i = decltype(II)::value;
+      *reinterpret_cast<i32x4 *>(&As[buf][alds[i]]) = ra[s][i];
+    });
+  };
+
+  i32x4 acc[RCAP][MB][NB];
+  static_for<RCAP>([&](auto C) {
+    static_for<MB>([&](auto I) { static_for<NB>([&](auto J) { acc[C][I][J] = zero; }); });
+  });
+
+  Epi<RCAP> e;
+  load_epi<RCAP>(g, e, c_act);
+  static_for<P>([&](auto SS) { gload(SS, decltype(SS)::value); });
+  pin_epi<RCAP>(e);
+  lstore(std::integral_constant<int, 0>{}, 0);
+  __syncthreads();
+
+  const int steps = (nk + P - 1) / P * P;
+  const int a_frag = (lane & 15) * kLdsRow + kofs;
+  for (int ks0 = 0; ks0 < steps; ks0 += P) {
+    static_for<P>([&](auto SS) {
+      constexpr int s = decltype(SS)::value;
+      const int ks = ks0 + s;
+      const int buf = ks & 1;
+      i32x4 fa[MB];
+      static_for<RCAP>([&](auto C) {
+        constexpr int c = decltype(C)::value;
+        if (c >= c_act) return;
+        if (!ARAW || c == 0) {
+          static_for<MB>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            fa[i] = *reinterpret_cast<const i32x4 *>(&As[buf][(ARAW ? 0 : c) * PLANE + a_frag + i * 16 * kLdsRow]);
+          });
+        }
+        static_for<MB>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          static_for<NB>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[s][c][j], acc[c][i][j], 0, 0, 0);
+          });
+        });
+      });
+      gload(SS, ks + P);
+      lstore(std::integral_constant<int, (s + 1) % P>{}, buf ^ 1);
+      __syncthreads();
+    });
+  }
+
+  // epilogue from registers: lane holds rows 4*(lane>>4)+t of column lane&15
+  static_for<MB>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    static_for<NB>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      const int col = n0 + j * 16 + (lane & 15);
+      static_for<4>([&](auto T) {
+        constexpr int t = decltype(T)::value;
+        const int row = m0 + i * 16 + 4 * (lane >> 4) + t;
+        if (row < g.m && col < g.n) {
+          int32_t v[RCAP];
+          static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
+          finish_element<RCAP>(g, e, c_act, v, row, col);
+        }
+      });
+    });
+  });
+}
+
+// ---------------------------------------------------------------------------
+// Launchers for one channel capacity (instantiated per translation unit).
+// ---------------------------------------------------------------------------
+template <int RCAP, bool ARAW>
+bool launch_gemv(GemmArgs g, int mr, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((g.n + 3) / 4));
+#define RNSMX_GEMV(MR_)                                                                  \
+  if (mr == MR_) {                                                                       \
+    hipLaunchKernelGGL((gemv_kernel<RCAP, MR_, ARAW>), grid, dim3(256), 0, st, g);        \
+    return true;                                                                         \
+  }
+  RNSMX_GEMV(1)
+  RNSMX_GEMV(2)
+  RNSMX_GEMV(4)
+  RNSMX_GEMV(8)
+#undef RNSMX_GEMV
+  return false;
+}
+
+template <int RCAP, bool ARAW>
+bool launch_stream(GemmArgs g, int mb, int nb, int ks, hipStream_t st) {
+#define RNSMX_STREAM(MB_, NB_)                                                              \
+  if (mb == MB_ && nb == NB_) {                                                             \
+    g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                                          \
+    g.tiles_n = (g.n + 16 * NB_ - 1) / (16 * NB_);                                          \
+    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));                          \
+    const size_t lds = ks > 1 ? static_cast<size_t>(RCAP) * 256 * MB_ * NB_ * 4 : 0;         \
+    hipLaunchKernelGGL((stream_kernel<RCAP, MB_, NB_, ARAW>), grid, dim3(64 * ks), lds, st, g); \
+    return true;                                                                            \
+  }
+  RNSMX_STREAM(1, 1)
+  RNSMX_STREAM(2, 1)
+  RNSMX_STREAM(4, 1)
+  if constexpr (RCAP <= 4) {
+    RNSMX_STREAM(1, 2)
+    RNSMX_STREAM(2, 2)
+    RNSMX_STREAM(4, 2)
+  }
+#undef RNSMX_STREAM
+  return false;
+}
+
+template <int RCAP, bool ARAW>
+bool launch_mfma(GemmArgs g, int mb, int nb, hipStream_t st) {
+#define RNSMX_MFMA(MB_, NB_)                                                          \
+  if (mb == MB_ && nb == NB_) {                                                       \
+    g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                                    \
+    g.tiles_n = (g.n + 64 * NB_ - 1) / (64 * NB_);                                    \
+    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));                    \
+    hipLaunchKernelGGL((mfma_kernel<RCAP, MB_, NB_, ARAW>), grid, dim3(256), 0, st, g); \
+    return true;                                                                      \
+  }
+  if constexpr (RCAP <= 4) {
+    RNSMX_MFMA(8, 2)
+    RNSMX_MFMA(4, 2)
+    RNSMX_MFMA(4, 4)
+  } else if constexpr (RCAP == 6) {
+    RNSMX_MFMA(4, 2)
+  } else {
+    RNSMX_MFMA(2, 2)
+  }
+#undef RNSMX_MFMA
+  return false;
+}
+
+template <int RCAP>
+bool launch_gemm_rcap(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st) {
+  switch (c.kind) {
+    case kGemv:
+      return araw ? launch_gemv<RCAP, true>(g, c.mb, st) : launch_gemv<RCAP, false>(g, c.mb, st);
+    case kStream:
+      return araw ? launch_stream<RCAP, true>(g, c.mb, c.nb, c.ks, st)
+                  : launch_stream<RCAP, false>(g, c.mb, c.nb, c.ks, st);
+    case kMfma:
+      return araw ? launch_mfma<RCAP, true>(g, c.mb, c.nb, st) : launch_mfma<RCAP, false>(g, c.mb, c.nb, st);
+    default:
+      return false;
+  }
+}
+
+}  // namespace rnsmx

@@ -1,6 +1,7 @@
-// rnsmx device code for gfx950 (MI355X): residue encode, per-channel int8
-// MFMA GEMM with the fused modular-reduction + Garner (+ dequant) epilogue,
-// device-side adaptive channel prefix, Garner decode and operand repacking.
+// rnsmx device code for gfx950 (MI355X) outside the GEMM: residue
+// encoders, Garner decode of residue planes, operand repacking for the
+// drop-in fused op, the GEMM kernel choice and the C ABI.  The GEMM kernels
+// themselves live in rnsmx_gemm.hpp (instantiated in rnsmx_gemm_r*.hip).
 //
 // Data layout in HBM
 //   residue planes   [R][rows][ld] int8, K contiguous, ld a multiple of 64
@@ -10,51 +11,18 @@
 //                    orientation); the reference keeps [R][K][N]
 //                    (cuda_backend.py:68-76, rns_linear.py:185).
 //   output           [M][N] int64 (exact) or float32/float16/bfloat16.
-//
-// MFMA: v_mfma_i32_16x16x64_i8.  Lane l of a wave feeds A row (l & 15) and B
-// column (l & 15), both with K bytes [16 * (l >> 4), +16) of a 64-byte step,
-// and receives D rows 4 * (l >> 4) + t (t = 0..3) of column (l & 15).
-#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <climits>
 
-#include "rnsmx_arith.hpp"
-#include "rnsmx_common.hpp"
+#include "rnsmx_gemm.hpp"
 
 namespace rnsmx {
-
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
 // Argument blocks (passed by value; kernarg memory)
 // ---------------------------------------------------------------------------
-struct GemmArgs {
-  const int8_t *a;  // [R][M][a_ld] residue planes, or [M][a_ld] int8 (a_cs = 0)
-  int64_t a_ld, a_cs;
-  const int8_t *b;  // [R][N][b_ld]
-  int64_t b_ld, b_cs;
-  int32_t m, n, kp;  // kp: multiple of 64, <= b_ld
-  int32_t a_k;       // A bytes per row that are read; 16-byte chunks at or past it load as 0
-  int32_t tiles_m, tiles_n;  // output tile grid (set at launch)
-  int32_t lut_channels;
-  const int16_t *lut;  // [R][4][256]
-  // adaptive prefix
-  int32_t min_channels;  // 0: all channels
-  const int64_t *row_l1;
-  const int32_t *w_absmax;
-  int64_t *meta;
-  // epilogue
-  void *out;
-  int64_t out_ld;
-  int32_t out_dtype;
-  const float *a_scale;
-  const float *w_scale;
-  const float *bias;
-  rnsmx_moduli_t mods;
-};
-
 struct EncodeArgs {
   const void *values;
   int64_t rows, cols, out_ld, plane;
@@ -67,489 +35,10 @@ struct EncodeArgs {
 // ---------------------------------------------------------------------------
 // Helpers
 // ---------------------------------------------------------------------------
-// Kernel arguments read in place from the kernarg segment (constant address
-// space, scalar loads).  A by-value struct parameter used as an ordinary
-// object can be copied whole into per-lane scratch memory by the compiler
-// (it does so for the larger GEMM instances); a reference to the segment
-// never is.  Valid for kernels whose only parameter is the struct, which
-// then sits at offset 0 of the segment.
-#define RNSMX_KARG(T) const __attribute__((address_space(4))) T
-template <typename T>
-__device__ __forceinline__ RNSMX_KARG(T) & kernel_args() {
-  return *(RNSMX_KARG(T) *)(__builtin_amdgcn_kernarg_segment_ptr());
-}
-typedef RNSMX_KARG(GemmArgs) KGemmArgs;
-
-__device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const int64_t o = __shfl_xor(v, off, 64);
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
 __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
-}
-
-// prefix[idx] for a runtime idx <= RCAP, as a select chain over constant
-// indices: a runtime index into the kernel-argument block would make the
-// compiler copy the whole block to scratch memory.
-template <int RCAP, typename Mods>
-__device__ __forceinline__ int64_t prefix_at(const Mods &mods, int idx) {
-  int64_t p = mods.prefix[0];
-  static_for<RCAP + 1>([&](auto I) {
-    if (idx == decltype(I)::value) p = mods.prefix[decltype(I)::value];
-  });
-  return p;
-}
-
-// Number of moduli channels to use.  Without the adaptive prefix this is the
-// full set.  With it, every workgroup derives the same answer from the row
-// L1 norms written by the encoder and max|B| written at weight preparation:
-// bound = max_i sum_k |a_ik| * max|B| (adaptive.py:44-52); the answer is the
-// smallest c >= min_channels with 2 * bound < prod_{i<c} m_i
-// (adaptive.py:15-41), i.e. bound <= (P_c - 1) / 2.  When no prefix fits,
-// the full set is used and meta[3] flags the overflow (the reference raises
-// OverflowError on the host, which a device-side selector cannot).
-template <int RCAP>
-__device__ __forceinline__ int active_channels(KGemmArgs &g, int64_t *red, int *bcast) {
-  const int full = g.mods.channels;
-  if (g.min_channels <= 0) return full;
-  int64_t mx = 0;
-  for (int r = threadIdx.x; r < g.m; r += blockDim.x) {
-    const int64_t v = g.row_l1[r];
-    mx = v > mx ? v : mx;
-  }
-  mx = wave_max_i64(mx);
-  const int nw = blockDim.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int64_t best = 0;
-    for (int w = 0; w < nw; ++w) best = red[w] > best ? red[w] : best;
-    const int64_t wmax = *g.w_absmax;
-    const int64_t bound =
-        (wmax != 0 && best > LLONG_MAX / wmax) ? LLONG_MAX : best * wmax;
-    int c = full, overflow = 1;
-    static_for<RCAP + 1>([&](auto I) {
-      constexpr int i = decltype(I)::value;
-      if (overflow && i >= g.min_channels && i <= full && bound <= (g.mods.prefix[i] - 1) / 2) {
-        c = i;
-        overflow = 0;
-      }
-    });
-    *bcast = c;
-    if (g.meta != nullptr && blockIdx.x == 0) {
-      g.meta[0] = c;
-      g.meta[1] = bound;
-      g.meta[2] = (prefix_at<RCAP>(g.mods, c) - 1) / 2;
-      g.meta[3] = overflow;
-    }
-  }
-  __syncthreads();
-  return *bcast;
-}
-
-// Final value of one output element from its mixed-radix digits, centered
-// about P_c / 2, written in the requested output type.  The float chain is
-// ((float)x * a_scale) * w_scale[col] + bias[col], each step rounded to
-// nearest even with no contraction: the op order of rns_linear.py:272-275.
-template <int RCAP>
-__device__ __forceinline__ void store_element(KGemmArgs &g, int c_act,
-                                              const uint32_t (&d)[RCAP], int row,
-                                              int col) {
-  uint64_t x = 0;
-#pragma unroll
-  for (int c = 0; c < RCAP; ++c)
-    if (c < c_act) x += static_cast<uint64_t>(d[c]) * static_cast<uint64_t>(g.mods.prefix[c]);
-  const int64_t p = prefix_at<RCAP>(g.mods, c_act);
-  int64_t y = static_cast<int64_t>(x);
-  if (y > (p >> 1)) y -= p;
-  const int64_t idx = static_cast<int64_t>(row) * g.out_ld + col;
-  if (g.out_dtype == RNSMX_INT64) {
-    static_cast<int64_t *>(g.out)[idx] = y;
-    return;
-  }
-  float f = __ll2float_rn(y);
-  f = __fmul_rn(f, *g.a_scale);
-  f = __fmul_rn(f, g.w_scale[col]);
-  if (g.bias != nullptr) f = __fadd_rn(f, g.bias[col]);
-  if (g.out_dtype == RNSMX_FLOAT32) {
-    static_cast<float *>(g.out)[idx] = f;
-  } else if (g.out_dtype == RNSMX_FLOAT16) {
-    static_cast<__half *>(g.out)[idx] = __float2half_rn(f);
-  } else {
-    static_cast<uint16_t *>(g.out)[idx] = f32_to_bf16_rne(f);
-  }
-}
-
-// Mixed-radix digit of channel C from its canonical residue r and the lower
-// digits: d_C = (r * q_C + sum_{j<C} d_j * u_{j,C}) mod m_C, where
-// q_C = P_C^-1 mod m_C and u_{j,C} = -P_j q_C mod m_C.  Every term is below
-// 2^16 and there are at most 10, so one Barrett reduction suffices.
-template <int C, typename Mods, typename DigitAt>
-__device__ __forceinline__ uint32_t garner_digit(const Mods &mods, uint32_t r, DigitAt &&digit_at) {
-  uint32_t s = r * mods.qinv[C];
-#pragma unroll
-  for (int j = 0; j < C; ++j) s += digit_at(j) * mods.ucoef[j][C];
-  return mod_u32(s, static_cast<uint32_t>(mods.moduli[C]), mods.magic[C]);
-}
-
-// ---------------------------------------------------------------------------
-// Workgroup -> output tile.  Workgroups are handed to the 8 XCDs round-robin
-// (workgroup b runs on XCD b % 8), and each XCD has its own L2.  Tiles are
-// numbered M-block fastest, so giving every XCD one contiguous run of tile
-// numbers keeps the workgroups that read the same weight columns on the
-// same L2.  The map is a bijection on [0, tiles) for any tile count.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int &mt, int &nt) {
-  const int total = tiles_m * tiles_n;
-  const int b = blockIdx.x;
-  const int xcd = b & 7, local = b >> 3;
-  const int base = total >> 3, rem = total & 7;
-  const int t = xcd * base + min(xcd, rem) + local;
-  mt = t % tiles_m;
-  nt = t / tiles_m;
-}
-
-__device__ __forceinline__ i32x4 load16(const int8_t *p) {
-  return *reinterpret_cast<const i32x4 *>(p);
-}
-
-// Canonical residue of one int32 accumulator of channel c (LUT or Barrett).
-__device__ __forceinline__ uint32_t reduce_acc(KGemmArgs &g, int c, int32_t v) {
-  const uint32_t m = static_cast<uint32_t>(g.mods.moduli[c]);
-  return c < g.lut_channels ? canon_i32_lut(v, g.lut + c * 1024, m, g.mods.c31[c])
-                            : canon_i32(v, m, g.mods.magic[c], g.mods.c31[c]);
-}
-
-// ---------------------------------------------------------------------------
-// Stream GEMM (small and medium M: decode, continuous batches, C2 shapes).
-// The bound is HBM latency: the weight residues are read once and the
-// problem is a few MB, so every wave issues all the loads of its K slice
-// before its first MFMA.  A workgroup owns a (16*MB) x (16*NB) output tile;
-// its waves split K (wave w takes K-step chunks w, w + KS, ... of U steps)
-// and each wave accumulates every channel.  Channel partial sums are reduced
-// mod m_c to canonical bytes in LDS ((sum of partials) mod m = (sum of
-// (partial mod m)) mod m), then each thread combines the slices of four
-// adjacent outputs, runs Garner and stores them.
-//
-// ARAW: A is one int8 matrix shared by every channel (an int8 activation is
-// its own representative mod every m_c, so the channel-c product of the raw
-// activations has the same residue as the product of the centered residues);
-// otherwise A holds one centered residue plane per channel.
-// ---------------------------------------------------------------------------
-// K steps per chunk of the stream kernel: as many as fit next to the
-// accumulators in 240 registers (two waves per SIMD), at most 4.
-constexpr int stream_u_of(int rcap, bool araw, int mb, int nb) {
-  const int frags = (araw ? 1 : rcap) * mb + rcap * nb;  // 16-byte loads per K step
-  const int u = (240 - 4 * rcap * mb * nb) / (4 * frags);
-  return u < 1 ? 1 : (u > 4 ? 4 : u);
-}
-
-template <int RCAP, int MB, int NB, bool ARAW>
-struct StreamCfg {
-  static constexpr int AP = ARAW ? 1 : RCAP;
-  static constexpr int U = stream_u_of(RCAP, ARAW, MB, NB);
-  static constexpr int TILE = 16 * MB * 16 * NB;
-};
-
-template <int RCAP, int MB, int NB, bool ARAW>
-__global__ __launch_bounds__(256) void gemm_stream_kernel(const GemmArgs args) {
-  KGemmArgs &g = kernel_args<GemmArgs>();
-  using Cfg = StreamCfg<RCAP, MB, NB, ARAW>;
-  constexpr int BM = 16 * MB, BN = 16 * NB, TILE = Cfg::TILE, AP = Cfg::AP, U = Cfg::U;
-  extern __shared__ __attribute__((aligned(16))) uint8_t sres[];  // [KS][RCAP][TILE]
-  __shared__ int64_t red[4];
-  __shared__ int bcast;
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int ks_n = blockDim.x >> 6;
-  const int c_act = active_channels<RCAP>(g, red, &bcast);
-  int mt, nt;
-  tile_of(g.tiles_m, g.tiles_n, mt, nt);
-  const int m0 = mt * BM, n0 = nt * BN;
-  const int nk = g.kp >> 6;
-  const int kofs = (lane >> 4) * 16;
-
-  const int8_t *ap[MB];
-  const int8_t *bp[NB];
-  static_for<MB>([&](auto I) {
-    constexpr int i = decltype(I)::value;
-    const int row = min(m0 + i * 16 + (lane & 15), g.m - 1);
-    ap[i] = g.a + static_cast<int64_t>(row) * g.a_ld + kofs;
-  });
-  static_for<NB>([&](auto J) {
-    constexpr int j = decltype(J)::value;
-    const int col = min(n0 + j * 16 + (lane & 15), g.n - 1);
-    bp[j] = g.b + static_cast<int64_t>(col) * g.b_ld + kofs;
-  });
-
-  const i32x4 zero = {0, 0, 0, 0};
-  i32x4 acc[RCAP][MB][NB];
-  static_for<RCAP>([&](auto C) {
-    static_for<MB>([&](auto I) {
-      static_for<NB>([&](auto J) { acc[C][I][J] = zero; });
-    });
-  });
-
-  for (int q = wave * U; q < nk; q += ks_n * U) {
-    i32x4 fa[U][AP][MB], fb[U][RCAP][NB];
-    static_for<U>([&](auto UU) {
-      constexpr int u = decltype(UU)::value;
-      const int ks = q + u;
-      const bool kv = ks < nk;
-      const int ko = ks * 64;
-      const bool av = kv && (ko + kofs < g.a_k);
-      static_for<AP>([&](auto PP) {
-        constexpr int p = decltype(PP)::value;
-        static_for<MB>([&](auto I) {
-          constexpr int i = decltype(I)::value;
-          fa[u][p][i] = (av && p < c_act) ? load16(ap[i] + p * g.a_cs + ko) : zero;
-        });
-      });
-      static_for<RCAP>([&](auto C) {
-        constexpr int c = decltype(C)::value;
-        static_for<NB>([&](auto J) {
-          constexpr int j = decltype(J)::value;
-          fb[u][c][j] = (kv && c < c_act) ? load16(bp[j] + c * g.b_cs + ko) : zero;
-        });
-      });
-    });
-    static_for<U>([&](auto UU) {
-      constexpr int u = decltype(UU)::value;
-      static_for<RCAP>([&](auto C) {
-        constexpr int c = decltype(C)::value;
-        if (c >= c_act) return;
-        static_for<MB>([&](auto I) {
-          constexpr int i = decltype(I)::value;
-          static_for<NB>([&](auto J) {
-            constexpr int j = decltype(J)::value;
-            acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][ARAW ? 0 : c][i], fb[u][c][j],
-                                                                 acc[c][i][j], 0, 0, 0);
-          });
-        });
-      });
-    });
-  }
-
-  // this wave's K slice: canonical residues, one byte per (channel, element)
-  uint8_t *mine = sres + wave * (RCAP * TILE);
-  static_for<RCAP>([&](auto C) {
-    constexpr int c = decltype(C)::value;
-    if (c >= c_act) return;
-    static_for<MB>([&](auto I) {
-      constexpr int i = decltype(I)::value;
-      static_for<NB>([&](auto J) {
-        constexpr int j = decltype(J)::value;
-        static_for<4>([&](auto T) {
-          constexpr int t = decltype(T)::value;
-          mine[c * TILE + (i * 16 + 4 * (lane >> 4) + t) * BN + j * 16 + (lane & 15)] =
-              static_cast<uint8_t>(reduce_acc(g, c, acc[c][i][j][t]));
-        });
-      });
-    });
-  });
-  __syncthreads();
-
-  // combine slices, Garner, store: each thread takes 4 adjacent columns
-  const int rows_here = min(BM, g.m - m0);
-  for (int e = threadIdx.x * 4; e < rows_here * BN; e += blockDim.x * 4) {
-    const int row = e / BN, col = e % BN;
-    uint32_t d[4][RCAP];
-    static_for<RCAP>([&](auto CC) {
-      constexpr int cc = decltype(CC)::value;
-      if (cc >= c_act) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) d[v][cc] = 0;
-        return;
-      }
-      // byte sums in 16-bit lanes: even bytes and odd bytes of the 4 outputs
-      uint32_t lo = 0, hi = 0;
-      for (int s = 0; s < ks_n; ++s) {
-        const uint32_t w = *reinterpret_cast<const uint32_t *>(sres + s * (RCAP * TILE) + cc * TILE + e);
-        lo += w & 0x00FF00FFu;
-        hi += (w >> 8) & 0x00FF00FFu;
-      }
-      const uint32_t sums[4] = {lo & 0xFFFFu, hi & 0xFFFFu, lo >> 16, hi >> 16};
-      const uint32_t m = static_cast<uint32_t>(g.mods.moduli[cc]);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const uint32_t r = mod_u32(sums[v], m, g.mods.magic[cc]);
-        d[v][cc] = garner_digit<cc>(g.mods, r, [&](int jj) { return d[v][jj]; });
-      }
-    });
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-      if (n0 + col + v < g.n) store_element<RCAP>(g, c_act, d[v], m0 + row, n0 + col + v);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// MFMA GEMM (large M: prefill, C4/C5 shapes).  Bound by MFMA throughput, so
-// operands are reused from registers and LDS.  A workgroup of 4 waves owns a
-// (16*MB) x (4*16*NB) tile: the A rows (shared by all waves, and in ARAW
-// mode by all channels) are staged through double-buffered LDS with rows
-// padded to 80 bytes (the 16-byte fragment reads of 16 lanes hit disjoint
-// banks); each wave owns 16*NB columns and streams their weight residues
-// straight from global memory into a P-deep register ring.  Every K step
-// feeds all channels, so all channel accumulators finish together and the
-// reduction + Garner + store run from registers.
-// ---------------------------------------------------------------------------
-constexpr int kLdsRow = 80;
-
-template <int RCAP, int MB, int NB, int P, bool ARAW>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(const GemmArgs args) {
-  KGemmArgs &g = kernel_args<GemmArgs>();
-  constexpr int BM = 16 * MB, BNW = 16 * NB;
-  constexpr int AP = ARAW ? 1 : RCAP;
-  constexpr int PLANE = BM * kLdsRow;
-  constexpr int ACH = AP * BM * 4;  // 16-byte A chunks per K step
-  constexpr int AC = (ACH + 255) / 256;
-  __shared__ __attribute__((aligned(16))) int8_t As[2][AP * PLANE];
-  __shared__ int64_t red[4];
-  __shared__ int bcast;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c_act = active_channels<RCAP>(g, red, &bcast);
-  int mt, nt;
-  tile_of(g.tiles_m, g.tiles_n, mt, nt);
-  const int m0 = mt * BM, n0 = nt * (4 * BNW) + wave * BNW;
-  const int nk = g.kp >> 6;
-  const int kofs = (lane >> 4) * 16;
-
-  // A staging: chunk q -> plane p, row, 16-byte part
-  const int8_t *asrc[AC];
-  int alds[AC], apart[AC];
-  bool aon[AC];
-  static_for<AC>([&](auto II) {
-    constexpr int i = decltype(II)::value;
-    const int q = tid + 256 * i;
-    aon[i] = q < ACH;
-    const int qq = aon[i] ? q : 0;
-    const int p = qq / (BM * 4), w = qq % (BM * 4), row = w >> 2, part = w & 3;
-    const int grow = min(m0 + row, g.m - 1);
-    asrc[i] = g.a + p * g.a_cs + static_cast<int64_t>(grow) * g.a_ld + part * 16;
-    alds[i] = p * PLANE + row * kLdsRow + part * 16;
-    apart[i] = part * 16;
-    aon[i] = aon[i] && (ARAW || p < c_act);
-  });
-  const int8_t *bp[NB];
-  static_for<NB>([&](auto J) {
-    constexpr int j = decltype(J)::value;
-    const int col = min(n0 + j * 16 + (lane & 15), g.n - 1);
-    bp[j] = g.b + static_cast<int64_t>(col) * g.b_ld + kofs;
-  });
-
-  const i32x4 zero = {0, 0, 0, 0};
-  i32x4 ra[AC];
-  i32x4 fb[P][RCAP][NB];
-  auto gload_a = [&](int ks) {
-    const int ko = ks * 64;
-    static_for<AC>([&](auto II) {
-      constexpr int i = decltype(II)::value;
-      ra[i] = (aon[i] && ko + apart[i] < g.a_k) ? load16(asrc[i] + ko) : zero;
-    });
-  };
-  auto lstore_a = [&](int buf) {
-    static_for<AC>([&](auto II) {
-      constexpr int i = decltype(II)::value;
-      if (aon[i]) *reinterpret_cast<i32x4 *>(&As[buf][alds[i]]) = ra[i];
-    });
-  };
-
-  i32x4 acc[RCAP][MB][NB];
-  static_for<RCAP>([&](auto C) {
-    static_for<MB>([&](auto I) {
-      static_for<NB>([&](auto J) { acc[C][I][J] = zero; });
-    });
-  });
-
-  gload_a(0);
-  lstore_a(0);
-  static_for<P>([&](auto SS) {
-    constexpr int s = decltype(SS)::value;
-    if (s < nk) {
-      static_for<RCAP>([&](auto C) {
-        constexpr int c = decltype(C)::value;
-        static_for<NB>([&](auto J) {
-          constexpr int j = decltype(J)::value;
-          fb[s][c][j] = c < c_act ? load16(bp[j] + c * g.b_cs + s * 64) : zero;
-        });
-      });
-    }
-  });
-  __syncthreads();
-
-  const int a_frag = (lane & 15) * kLdsRow + kofs;
-  for (int ks0 = 0; ks0 < nk; ks0 += P) {
-    static_for<P>([&](auto SS) {
-      constexpr int s = decltype(SS)::value;
-      const int ks = ks0 + s;
-      if (ks >= nk) return;
-      const int buf = ks & 1;
-      const bool more = ks + 1 < nk;
-      if (more) gload_a(ks + 1);
-      i32x4 fa[MB];
-      static_for<RCAP>([&](auto C) {
-        constexpr int c = decltype(C)::value;
-        if (c >= c_act) return;
-        if (!ARAW || c == 0) {
-          static_for<MB>([&](auto I) {
-            constexpr int i = decltype(I)::value;
-            fa[i] = *reinterpret_cast<const i32x4 *>(
-                &As[buf][(ARAW ? 0 : c) * PLANE + a_frag + i * 16 * kLdsRow]);
-          });
-        }
-        static_for<MB>([&](auto I) {
-          constexpr int i = decltype(I)::value;
-          static_for<NB>([&](auto J) {
-            constexpr int j = decltype(J)::value;
-            acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[s][c][j], acc[c][i][j], 0, 0, 0);
-          });
-        });
-      });
-      if (ks + P < nk) {
-        static_for<RCAP>([&](auto C) {
-          constexpr int c = decltype(C)::value;
-          static_for<NB>([&](auto J) {
-            constexpr int j = decltype(J)::value;
-            fb[s][c][j] = c < c_act ? load16(bp[j] + c * g.b_cs + (ks + P) * 64) : zero;
-          });
-        });
-      }
-      if (more) lstore_a(buf ^ 1);
-      __syncthreads();
-    });
-  }
-
-  // epilogue from registers: lane holds rows 4*(lane>>4)+t of column lane&15
-  static_for<MB>([&](auto I) {
-    constexpr int i = decltype(I)::value;
-    static_for<NB>([&](auto J) {
-      constexpr int j = decltype(J)::value;
-      const int col = n0 + j * 16 + (lane & 15);
-      static_for<4>([&](auto T) {
-        constexpr int t = decltype(T)::value;
-        const int row = m0 + i * 16 + 4 * (lane >> 4) + t;
-        uint32_t d[RCAP];
-        static_for<RCAP>([&](auto CC) {
-          constexpr int cc = decltype(CC)::value;
-          if (cc >= c_act) {
-            d[cc] = 0;
-            return;
-          }
-          const uint32_t r = reduce_acc(g, cc, acc[cc][i][j][t]);
-          d[cc] = garner_digit<cc>(g.mods, r, [&](int jj) { return d[jj]; });
-        });
-        if (row < g.m && col < g.n) store_element<RCAP>(g, c_act, d, row, col);
-      });
-    });
-  });
 }
 
 // ---------------------------------------------------------------------------
@@ -697,28 +186,22 @@ struct DecodeArgs {
 template <int RCAP>
 __global__ __launch_bounds__(256) void decode_garner_kernel(const DecodeArgs a) {
   const int R = a.mods.channels;
+  Epi<RCAP> k;
+  fill_moduli<RCAP>(k, a.mods, R);
   for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < a.count;
        e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    uint32_t d[RCAP];
+    uint32_t r[RCAP];
     static_for<RCAP>([&](auto CC) {
       constexpr int c = decltype(CC)::value;
       if (c >= R) {
-        d[c] = 0;
+        r[c] = 0;
         return;
       }
       const int32_t m = a.mods.moduli[c];
-      const int32_t v = a.res[c * a.count + e];
-      const uint32_t r = static_cast<uint32_t>(v < 0 ? v + m : v) % static_cast<uint32_t>(m);
-      d[c] = garner_digit<c>(a.mods, r, [&](int jj) { return d[jj]; });
+      const int32_t v = a.res[c * a.count + e];  // centered residue, |v| <= m/2
+      r[c] = static_cast<uint32_t>(v < 0 ? v + m : v);
     });
-    uint64_t x = 0;
-#pragma unroll
-    for (int c = 0; c < RCAP; ++c)
-      if (c < R) x += static_cast<uint64_t>(d[c]) * static_cast<uint64_t>(a.mods.prefix[c]);
-    const int64_t p = prefix_at<RCAP>(a.mods, R);
-    int64_t y = static_cast<int64_t>(x);
-    if (y > (p >> 1)) y -= p;
-    a.out[e] = y;
+    a.out[e] = garner_value<RCAP>(k, r, R);
   }
 }
 
@@ -777,31 +260,29 @@ static int32_t check_launch(const char *what) {
   return RNSMX_OK;
 }
 
-enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2 };
-
-struct GemmChoice {
-  int kind, mb, nb, ks;
-};
-
 // Process-wide override of the kernel choice (rnsmx_set_gemm_override).
 static GemmChoice g_override = {kAuto, 0, 0, 0};
 
 static constexpr int kStreamLdsMax = 65536;
 
 static int stream_ks_cap(int rcap, int mb, int nb) {
-  const int per_wave = rcap * 256 * mb * nb;
-  return std::max(1, std::min(4, kStreamLdsMax / per_wave));
+  const int per_ws = rcap * 256 * mb * nb * 4;  // int32 partial sums in LDS
+  return per_ws > kStreamLdsMax ? 1 : 4;
 }
 
-// Kernel family and tile for an M x N x kp problem.  Small M streams the
-// weights (stream kernel, K split over waves); large M is MFMA-bound (mfma
-// kernel, 128-row tiles for up to 4 channels).
+// Kernel family and tile for an M x N x kp problem: dot4 GEMV for up to 8
+// rows (weight streaming), the stream kernel (K split over waves) up to 256
+// rows, the MFMA kernel (128-row tiles for up to 4 channels) beyond.
 static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   const int rcap = rcap_for(g.mods.channels);
   const int nk = g.kp / 64;
   GemmChoice c{};
+  if (g.m <= 8) {
+    c.kind = kGemv;
+    c.mb = g.m <= 1 ? 1 : (g.m <= 2 ? 2 : (g.m <= 4 ? 4 : 8));
+    return c;
+  }
   if (g.m <= 256) {
-    // 16- or 32-row tiles of 16 columns: the most workgroups in flight
     c.kind = kStream;
     c.mb = g.m <= 16 ? 1 : 2;
     c.nb = 1;
@@ -824,65 +305,14 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   return c;
 }
 
-template <int RCAP, bool ARAW>
-static bool launch_stream(GemmArgs g, int mb, int nb, int ks, hipStream_t st) {
-#define RNSMX_STREAM(MB_, NB_)                                                             \
-  if (mb == MB_ && nb == NB_) {                                                            \
-    g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                                         \
-    g.tiles_n = (g.n + 16 * NB_ - 1) / (16 * NB_);                                         \
-    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));                         \
-    const size_t lds = static_cast<size_t>(ks) * RCAP * StreamCfg<RCAP, MB_, NB_, ARAW>::TILE; \
-    hipLaunchKernelGGL((gemm_stream_kernel<RCAP, MB_, NB_, ARAW>), grid, dim3(64 * ks), lds, st, g); \
-    return true;                                                                           \
-  }
-  RNSMX_STREAM(1, 1)
-  RNSMX_STREAM(2, 1)
-  RNSMX_STREAM(4, 1)
-  if constexpr (RCAP <= 4) {
-    RNSMX_STREAM(1, 2)
-    RNSMX_STREAM(1, 4)
-    RNSMX_STREAM(2, 2)
-    RNSMX_STREAM(4, 2)
-  }
-#undef RNSMX_STREAM
-  return false;
-}
-
-template <int RCAP, bool ARAW>
-static bool launch_mfma(GemmArgs g, int mb, int nb, hipStream_t st) {
-#define RNSMX_MFMA(MB_, NB_)                                                         \
-  if (mb == MB_ && nb == NB_) {                                                      \
-    g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                                   \
-    g.tiles_n = (g.n + 64 * NB_ - 1) / (64 * NB_);                                   \
-    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));                   \
-    hipLaunchKernelGGL((gemm_mfma_kernel<RCAP, MB_, NB_, 2, ARAW>), grid, dim3(256), 0, st, g); \
-    return true;                                                                     \
-  }
-  if constexpr (RCAP <= 4) {
-    RNSMX_MFMA(8, 2)
-    RNSMX_MFMA(4, 2)
-    RNSMX_MFMA(4, 4)
-  } else if constexpr (RCAP == 6) {
-    RNSMX_MFMA(4, 2)
-  } else {
-    RNSMX_MFMA(2, 2)
-  }
-#undef RNSMX_MFMA
-  return false;
-}
-
-template <int RCAP>
-static bool launch_rcap(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st) {
-  if (c.kind == kStream)
-    return araw ? launch_stream<RCAP, true>(g, c.mb, c.nb, c.ks, st)
-                : launch_stream<RCAP, false>(g, c.mb, c.nb, c.ks, st);
-  return araw ? launch_mfma<RCAP, true>(g, c.mb, c.nb, st) : launch_mfma<RCAP, false>(g, c.mb, c.nb, st);
-}
-
 // Launches the GEMM for `g`.  araw: A is one int8 matrix for all channels.
 static int32_t launch_gemm(const GemmArgs &g, bool araw, hipStream_t st) {
   const int rcap = rcap_for(g.mods.channels);
   GemmChoice c = g_override.kind != kAuto ? g_override : choose_gemm(g, araw);
+  if (c.kind == kGemv && g.m > c.mb) {
+    set_error("GEMV kernel for %d rows cannot take M = %d", c.mb, g.m);
+    return RNSMX_EINVAL;
+  }
   if (c.kind == kStream) {
     const int cap = stream_ks_cap(rcap, c.mb, c.nb);
     if (c.ks < 1 || c.ks > cap) {
@@ -892,17 +322,17 @@ static int32_t launch_gemm(const GemmArgs &g, bool araw, hipStream_t st) {
   }
   bool ok = false;
   switch (rcap) {
-    case 3: ok = launch_rcap<3>(g, araw, c, st); break;
-    case 4: ok = launch_rcap<4>(g, araw, c, st); break;
-    case 6: ok = launch_rcap<6>(g, araw, c, st); break;
-    default: ok = launch_rcap<10>(g, araw, c, st); break;
+    case 3: ok = launch_gemm_r3(g, araw, c, st); break;
+    case 4: ok = launch_gemm_r4(g, araw, c, st); break;
+    case 6: ok = launch_gemm_r6(g, araw, c, st); break;
+    default: ok = launch_gemm_r10(g, araw, c, st); break;
   }
   if (!ok) {
     set_error("no GEMM kernel for kind %d, tile %d x %d, %d channels", c.kind, c.mb, c.nb,
               g.mods.channels);
     return RNSMX_EINVAL;
   }
-  return check_launch(c.kind == kStream ? "gemm_stream" : "gemm_mfma");
+  return check_launch(c.kind == kStream ? "gemm_stream" : (c.kind == kMfma ? "gemm_mfma" : "gemm_gemv"));
 }
 
 static int32_t launch_encode_rows(int32_t dtype, const EncodeArgs &e, hipStream_t st) {
@@ -1233,7 +663,8 @@ int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb, int32_t ks
     g_override = GemmChoice{kAuto, 0, 0, 0};
     return RNSMX_OK;
   }
-  if (kind != kStream && kind != kMfma) return fail(RNSMX_EINVAL, "kind must be 0 (auto), 1 (stream) or 2 (mfma)");
+  if (kind != kStream && kind != kMfma && kind != kGemv)
+    return fail(RNSMX_EINVAL, "kind must be 0 (auto), 1 (stream), 2 (mfma) or 3 (gemv)");
   if (mb < 1 || nb < 1) return fail(RNSMX_EINVAL, "tile blocks must be positive");
   g_override = GemmChoice{kind, mb, nb, ks};
   return RNSMX_OK;

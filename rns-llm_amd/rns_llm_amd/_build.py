@@ -1,18 +1,25 @@
-"""Builds librnsmx.so (gfx950) in this package directory with hipcc."""
+"""Builds librnsmx.so (gfx950) in this package directory with hipcc.
+
+Every translation unit is compiled to an object in parallel (the GEMM
+kernels are split by channel capacity for this), then linked."""
 from __future__ import annotations
 
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)                 # rns-llm_amd/
 REPO = os.path.dirname(ROOT)
 CSRC = os.path.join(ROOT, "csrc")
 INCLUDE = os.path.join(REPO, "include")
+OBJDIR = os.path.join(ROOT, "_build")
 OUT = os.path.join(PKG, "librnsmx.so")
-SOURCES = ("rnsmx_kernels.hip", "rnsmx_host.cpp")
+SOURCES = ("rnsmx_kernels.hip", "rnsmx_gemm_r3.hip", "rnsmx_gemm_r4.hip", "rnsmx_gemm_r6.hip",
+           "rnsmx_gemm_r10.hip", "rnsmx_host.cpp")
 ARCH = os.environ.get("RNSMX_OFFLOAD_ARCH", "gfx950")
+NOISE = "packed-fp32-ops"
 
 
 def hipcc() -> str:
@@ -20,30 +27,48 @@ def hipcc() -> str:
     return os.path.join(rocm, "bin", "hipcc")
 
 
-def command(out: str = OUT) -> list[str]:
+def flags() -> list[str]:
     return [
-        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+        f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
         # packed fp32 VALU ops stay off for all device code
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wall", "-Wno-unused-variable", "-Wno-unused-but-set-variable",
         "-I", INCLUDE, "-I", CSRC,
-        *[os.path.join(CSRC, s) for s in SOURCES],
-        "-Wl,-rpath,/opt/rocm/lib",
-        "-o", out,
     ]
 
 
-def build(verbose: bool = False) -> str:
-    tmp = OUT + ".tmp"
-    cmd = command(tmp)
+def compile_command(source: str, obj: str) -> list[str]:
+    return [hipcc(), *flags(), "-c", os.path.join(CSRC, source), "-o", obj]
+
+
+def link_command(objs: list[str], out: str) -> list[str]:
+    return [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs,
+            "-Wl,-rpath,/opt/rocm/lib", "-o", out]
+
+
+def _run(cmd: list[str]) -> tuple[int, str, list[str]]:
     proc = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "packed-fp32-ops"
-    msgs = [ln for ln in (proc.stdout + proc.stderr).splitlines() if noise not in ln]
-    if proc.returncode != 0:
-        sys.stderr.write("\n".join(msgs) + "\n")
-        raise RuntimeError(f"hipcc failed ({proc.returncode}): {' '.join(cmd)}")
-    if verbose and msgs:
-        sys.stderr.write("\n".join(msgs) + "\n")
+    msgs = [ln for ln in (proc.stdout + proc.stderr).splitlines() if NOISE not in ln]
+    return proc.returncode, "\n".join(msgs), cmd
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(OBJDIR, exist_ok=True)
+    objs = [os.path.join(OBJDIR, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    jobs = min(len(SOURCES), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        results = list(pool.map(_run, [compile_command(s, o) for s, o in zip(SOURCES, objs)]))
+    for rc, msgs, cmd in results:
+        if rc != 0:
+            sys.stderr.write(msgs + "\n")
+            raise RuntimeError(f"hipcc failed ({rc}): {' '.join(cmd)}")
+        if verbose and msgs:
+            sys.stderr.write(msgs + "\n")
+    tmp = OUT + ".tmp"
+    rc, msgs, cmd = _run(link_command(objs, tmp))
+    if rc != 0:
+        sys.stderr.write(msgs + "\n")
+        raise RuntimeError(f"hipcc link failed ({rc}): {' '.join(cmd)}")
     os.replace(tmp, OUT)
     return OUT
 

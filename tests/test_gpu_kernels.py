@@ -17,7 +17,7 @@ DENSE4 = (255, 253, 251, 247)
 SETS = {3: (254, 253, 251), 4: DENSE4, 6: (255, 253, 251, 247, 241, 239),
         10: (3, 5, 7, 11, 13, 17, 19, 23, 29, 31)}
 RCAP = {3: 3, 4: 4, 6: 6, 10: 10}
-STREAM_TILES = [(1, 1), (2, 1), (4, 1), (1, 2), (1, 4), (2, 2), (4, 2)]
+STREAM_TILES = [(1, 1), (2, 1), (4, 1), (1, 2), (2, 2), (4, 2)]
 MFMA_TILES = {3: [(8, 2), (4, 2), (4, 4)], 4: [(8, 2), (4, 2), (4, 4)], 6: [(4, 2)], 10: [(2, 2)]}
 
 
@@ -30,7 +30,7 @@ def stream_cases():
             if r == 10 and mb > 2:
                 continue
             for ks in (1, 2, 4):
-                if r * 256 * mb * nb * ks > 65536:
+                if ks > 1 and r * 256 * mb * nb * 4 > 65536:
                     continue
                 out.append((r, mb, nb, ks))
     return out
@@ -100,6 +100,17 @@ def test_stream_kernel_instances(backend, override, r, mb, nb, ks):
     run_case(backend, mods, 7, 150, 37, dtype=torch.int16, seed=ks + 1)
 
 
+@pytest.mark.parametrize("r", [3, 4, 6, 10])
+@pytest.mark.parametrize("mr", [1, 2, 4, 8])
+def test_gemv_kernel_instances(backend, override, r, mr):
+    override(3, mr, 1, 0)
+    mods = SETS[r]
+    for m in sorted({1, max(1, mr // 2 + 1), mr}):
+        run_case(backend, mods, m, 208, 37, seed=r * 10 + mr + m)          # raw int8 A
+        run_case(backend, mods, m, 100, 21, seed=r + mr + m)               # residue planes, K % 16 != 0
+        run_case(backend, mods, m, 1100, 9, dtype=torch.int16, seed=r + m)  # int16 sources, several chunks per lane
+
+
 @pytest.mark.parametrize("r,mb,nb", mfma_cases())
 def test_mfma_kernel_instances(backend, override, r, mb, nb):
     override(2, mb, nb, 0)
@@ -110,17 +121,24 @@ def test_mfma_kernel_instances(backend, override, r, mb, nb):
 
 
 @pytest.mark.parametrize("kind,mb,nb,ks", [(1, 1, 1, 4), (1, 4, 2, 2), (1, 2, 2, 1), (2, 8, 2, 0),
-                                           (2, 4, 4, 0)])
+                                           (2, 4, 4, 0), (3, 8, 1, 0)])
 def test_kernel_adaptive_prefix(backend, override, kind, mb, nb, ks):
     override(kind, mb, nb, ks)
-    run_case(backend, DENSE4, 50, 320, 90, seed=5, adaptive=True)
+    run_case(backend, DENSE4, 7 if kind == 3 else 50, 320, 90, seed=5, adaptive=True)
 
 
-@pytest.mark.parametrize("kind,mb,nb,ks", [(1, 1, 2, 2), (1, 4, 1, 4), (2, 8, 2, 0)])
+@pytest.mark.parametrize("kind,mb,nb,ks", [(1, 1, 2, 2), (1, 4, 1, 4), (1, 2, 1, 1), (2, 8, 2, 0), (3, 8, 1, 0)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_kernel_float_epilogue(backend, override, kind, mb, nb, ks, out_dtype):
     override(kind, mb, nb, ks)
-    run_case(backend, DENSE4, 45, 256, 77, seed=9, out_dtype=out_dtype)
+    run_case(backend, DENSE4, 6 if kind == 3 else 45, 256, 77, seed=9, out_dtype=out_dtype)
+
+
+def test_override_rejects_gemv_with_too_many_rows(backend, override):
+    override(3, 4, 1, 0)
+    prepared = backend.prepare_weight(torch.ones((64, 16), dtype=torch.int8, device=DEV), DENSE4)
+    with pytest.raises(ValueError, match="GEMV"):
+        backend.matmul_prepared_fused(torch.ones((5, 64), dtype=torch.int8, device=DEV), prepared)
 
 
 def test_override_rejects_unbuilt_tile(backend, override):
