@@ -5,26 +5,42 @@ Workload (the metric's config): fused OPT-125m QKV,
 K=768, N=3x768=2304, R=4 channels (255, 253, 251, 247), M=256 tokens.
 Weights: per-output-channel symmetric int8 of seeded N(0, 0.02) matrices;
 activations: per-token int8 of seeded N(0, 1).  One step = one
-``matmul_prepared_fused`` call (residue encode + MFMA GEMM + reduction +
-Garner + signed correction, exact int64 output) with inputs resident in HBM.
-The prepared weights rotate over copies totalling more than 512 MB so the
-256 MB MALL cannot serve repeats.
+``matmul_prepared_fused`` call (MFMA GEMM over the residue channels +
+modular reduction + Garner + signed correction, exact int64 output) with
+inputs resident in HBM.  The prepared weights rotate over copies totalling
+more than 512 MB so the 256 MB MALL cannot serve repeats.
 
-Printed JSON (one line): value = effective int8 TOPS = 2*R*M*K*N / t_step;
-roofline of the dominant kernel (the GEMM) timed alone with HIP events;
-cpu_baseline = the NumPy restatement of the reference CPU path on a bounded
-sample, 1 core.  Extra rows cover the other C2 token counts, C3 decode and
-a C5 (OPT-6.7B QKV) shape.
+Timing: W untimed eager warmup steps, then the K timed steps are captured in
+one HIP graph (the launch cost of Python + ctypes per call is host time, not
+device throughput); the graph is replayed once untimed (upload), then once
+between synchronizations with HIP events on the launching stream.  The
+eager per-call latency (event pair around each call, host overhead
+included) is reported beside it as us_per_call_p50/p95.
+
+Printed JSON (one line): value = effective int8 TOPS = 2*R*M*K*N / t_step.
+roofline: the step is one GEMM kernel launch, so its duration is the
+graph-timed step; achieved = algorithmic bytes (A + residue weights + int64
+output) per launch / that duration.  traffic: HBM bytes per launch from two
+rocprofv3 --pmc child runs (FETCH_SIZE, WRITE_SIZE), each scaled by what
+the counter reads for a 64 MiB device copy in the same run (null when
+rocprofv3 is unavailable or fails).  cpu_baseline = the NumPy restatement
+of the reference CPU path on a bounded sample, 1 core.  Extra rows cover
+the other C2 token counts, C3 decode and C5 (OPT-6.7B QKV) shapes.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import math
 import os
 import platform
+import shutil
 import statistics
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -34,6 +50,9 @@ sys.path.insert(0, ROOT)
 DENSE4 = (255, 253, 251, 247)
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
+CALIB_BYTES = 64 << 20   # device copy used to scale the PMC byte counters
+GEMM_KERNELS = ("mfma_kernel", "stream_kernel")
+METRIC = "effective int8 TOPS + us/call, fused-QKV RNS GEMM+reconstruct, bit-exact"
 
 
 def log(*a):
@@ -49,11 +68,11 @@ def quant_rows_int8(w):
 
 
 def make_weights(backend, k, n_each, parts, count, seed, device):
-    """`count` prepared fused weights (B^T = [parts*n_each, k]) and their int8."""
+    """`count` prepared fused weights (B^T = [parts*n_each, k]) and the first one's int8."""
     import torch
 
     gen = torch.Generator(device=device).manual_seed(seed)
-    prepared, raw = [], []
+    prepared, first = [], None
     for i in range(count):
         blocks = [quant_rows_int8(torch.randn((n_each, k), generator=gen, device=device,
                                               dtype=torch.float32).half().float() * 0.02)
@@ -61,8 +80,8 @@ def make_weights(backend, k, n_each, parts, count, seed, device):
         w = torch.cat(blocks, dim=0).contiguous()           # [N, K] int8
         prepared.append(backend.prepare_weight_nk(w, DENSE4))
         if i == 0:
-            raw.append(w)
-    return prepared, raw[0]
+            first = w
+    return prepared, first
 
 
 def make_tokens(m, k, seed, device):
@@ -87,22 +106,8 @@ def exact_check(out, a, w_nk, max_rows=256):
         raise SystemExit(f"parity failure: {bad} outputs differ from the exact int64 product")
 
 
-def time_loop(fn, steps, warmup):
-    import torch
-
-    for i in range(warmup):
-        fn(i)
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        fn(i)
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps  # ms
-
-
 def per_call(fn, iters):
+    """Eager latency: event pair around each call (host launch cost included)."""
     import torch
 
     samples = []
@@ -117,55 +122,149 @@ def per_call(fn, iters):
     return statistics.median(samples), samples[min(len(samples) - 1, math.ceil(0.95 * len(samples)) - 1)]
 
 
-def measure_shape(backend, name, m, k, n_each, parts, steps, warmup, rotate_bytes, seed, device,
-                  check=True):
+def graph_steps(fn, steps, warmup):
+    """W eager warmup steps, K steps captured in one graph, replayed once
+    untimed and once timed.  Returns (device ms per step, host ms per step)."""
+    import torch
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            fn(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            fn(warmup + i)
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        t0 = time.perf_counter()
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        host = (time.perf_counter() - t0) * 1000.0
+    del graph
+    return start.elapsed_time(end) / steps, host / steps
+
+
+def rotation_count(k, n, rotate_bytes):
+    res_bytes = len(DENSE4) * n * ((k + 63) // 64 * 64)
+    return max(2, math.ceil(rotate_bytes / res_bytes))
+
+
+def measure_shape(backend, name, m, k, n_each, parts, steps, warmup, rotate_bytes, seed, device):
     import torch
 
     n = n_each * parts
     r = len(DENSE4)
-    res_bytes = r * n * ((k + 63) // 64 * 64)
-    count = max(2, math.ceil(rotate_bytes / res_bytes))
+    count = rotation_count(k, n, rotate_bytes)
     prepared, w0 = make_weights(backend, k, n_each, parts, count, seed, device)
     a = make_tokens(m, k, seed + 1, device)
     ws = backend.create_workspace(device=device, channels=r, m=m, n=n, k=k)
     out0 = backend.matmul_prepared_fused(a, prepared[0], workspace=ws).clone()
-    if check:
-        exact_check(out0, a, w0, max_rows=256 if k * n < 4_000_000 else 16)
+    exact_check(out0, a, w0, max_rows=256 if k * n < 4_000_000 else 16)
 
     def step(i):
         backend.matmul_prepared_fused(a, prepared[i % count], workspace=ws)
 
-    ms = time_loop(step, steps, warmup)
+    ms, host_ms = graph_steps(step, steps, warmup)
     p50, p95 = per_call(step, min(200, max(50, steps)))
-
-    # dominant kernel alone: GEMM on pre-encoded residues, same rotation
-    a_res = backend.encode_activations(a, prepared[0])
-    out = torch.empty((m, n), dtype=torch.int64, device=device)
-
-    def gemm(i):
-        backend.matmul_residues_prepared(a_res, prepared[i % count], out=out)
-
-    gemm_ms = time_loop(gemm, steps, warmup)
-    if check and not torch.equal(backend.matmul_residues_prepared(a_res, prepared[0], out=out), out0):
-        raise SystemExit("parity failure: GEMM-only path differs from the fused call")
+    if not torch.equal(backend.matmul_prepared_fused(a, prepared[0], workspace=ws), out0):
+        raise SystemExit("parity failure: repeated call differs")
     ops = 2 * r * m * k * n
     bytes_alg = m * k + r * k * n + m * n * 8
-    t_roof = max(ops / (INT8_PEAK_TOPS * 1e12), bytes_alg / (HBM_PEAK_GBS * 1e9))
+    t_ops, t_bytes = ops / (INT8_PEAK_TOPS * 1e12), bytes_alg / (HBM_PEAK_GBS * 1e9)
+    bound = "hbm" if t_bytes >= t_ops else "mfma"
     row = {
         "config": name, "m": m, "k": k, "n": n, "channels": r, "weight_copies": count,
-        "ms_per_step": ms, "us_per_call_p50": p50, "us_per_call_p95": p95,
+        "ms_per_step": ms, "host_ms_per_step": host_ms,
+        "us_per_call_graph": ms * 1000.0, "us_per_call_p50": p50, "us_per_call_p95": p95,
         "eff_tops": ops / (ms * 1e-3) / 1e12, "useful_tops": ops / r / (ms * 1e-3) / 1e12,
-        "gemm_kernel_us": gemm_ms * 1000.0,
-        "gemm_hbm_gbs": bytes_alg / (gemm_ms * 1e-3) / 1e9,
-        "gemm_eff_tops": ops / (gemm_ms * 1e-3) / 1e12,
-        "roofline_frac_step": t_roof / (ms * 1e-3),
-        "roofline_frac_gemm": t_roof / (gemm_ms * 1e-3),
-        "bound": "hbm" if bytes_alg / (HBM_PEAK_GBS * 1e9) >= ops / (INT8_PEAK_TOPS * 1e12) else "mfma",
+        "gbs_alg": bytes_alg / (ms * 1e-3) / 1e9,
+        "bound": bound,
+        "roofline_frac": (t_bytes if bound == "hbm" else t_ops) / (ms * 1e-3),
         "ops_eff": ops, "bytes_alg": bytes_alg,
     }
-    del prepared, ws, a_res, out
+    del prepared, ws
     torch.cuda.empty_cache()
     return row
+
+
+# --- HBM traffic from PMC counters -----------------------------------------
+
+def pmc_child(args):
+    """Workload of one counter pass: a 64 MiB device copy (calibration) and
+    the headline GEMM calls."""
+    import torch
+
+    from rns_llm_amd import HipRNSBackend
+
+    device = torch.device("cuda:0")
+    backend = HipRNSBackend()
+    x = torch.empty(CALIB_BYTES, dtype=torch.uint8, device=device)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    k, n = 768, 2304
+    count = rotation_count(k, n, int(args.rotate_mb * 1e6))
+    prepared, _ = make_weights(backend, k, 768, 3, count, 17, device)
+    a = make_tokens(args.m, k, 18, device)
+    ws = backend.create_workspace(device=device, channels=4, m=args.m, n=n, k=k)
+    for i in range(12):
+        backend.matmul_prepared_fused(a, prepared[(i + 1) % count], workspace=ws)
+    torch.cuda.synchronize()
+    print("pmc child done", flush=True)
+
+
+def pmc_pass(counter, args):
+    """Median counter value (KiB) of the GEMM and of the calibration copy."""
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        raise RuntimeError("rocprofv3 not found")
+    out = tempfile.mkdtemp(prefix="rnsmx_pmc_")
+    try:
+        cmd = ["timeout", "-s", "KILL", "150", prof, "--pmc", counter, "--output-format", "csv",
+               "-d", out, "-o", "pmc", "--", sys.executable, os.path.abspath(__file__),
+               "--pmc-child", "--m", str(args.m), "--rotate-mb", str(args.rotate_mb)]
+        env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
+        proc = subprocess.run(cmd, cwd=ROOT, env=env, capture_output=True, text=True)
+        files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+        if "pmc child done" not in proc.stdout or not files:
+            raise RuntimeError(f"rocprofv3 pass {counter} failed (rc {proc.returncode}): "
+                               f"{(proc.stderr or proc.stdout)[-400:]}")
+        gemm, copy = [], []
+        with open(files[0], newline="") as fh:
+            for rec in csv.DictReader(fh):
+                if rec["Counter_Name"] != counter:
+                    continue
+                name, value = rec["Kernel_Name"], float(rec["Counter_Value"])
+                if "copyBuffer" in name:
+                    copy.append(value)
+                elif any(g in name for g in GEMM_KERNELS):
+                    gemm.append(value)
+        if not gemm or not copy:
+            raise RuntimeError(f"rocprofv3 pass {counter}: kernels not found")
+        return statistics.median(gemm), statistics.median(copy)
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
+
+
+def measure_traffic(args):
+    """HBM bytes per GEMM launch = sum over FETCH_SIZE and WRITE_SIZE of
+    counter x (known copy bytes / counter of the copy)."""
+    parts = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        gemm_kib, copy_kib = pmc_pass(counter, args)
+        factor = CALIB_BYTES / (copy_kib * 1024.0)
+        parts[counter] = {"gemm_kib": gemm_kib, "copy_kib": copy_kib, "factor": factor,
+                          "bytes": gemm_kib * 1024.0 * factor}
+        log(f"bench: {counter} gemm {gemm_kib:.0f} KiB, copy {copy_kib:.0f} KiB, factor {factor:.3f}")
+    return parts
 
 
 def cpu_baseline(seconds):
@@ -205,11 +304,24 @@ def main():
     parser.add_argument("--rotate-mb", type=float, default=600.0)
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-extra", action="store_true", help="headline shape only")
+    parser.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
+    parser.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = parser.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the RNS path has no "
-              "collective, see DESIGN.md for how it would shard", file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): the RNS GEMM path has "
+              "no collective; DESIGN.md describes how it would shard", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_child:
+        pmc_child(args)
+        return
+
+    # counter passes first, in child processes, before this one touches the GPU
+    traffic = None
+    if not args.no_traffic:
+        try:
+            traffic = measure_traffic(args)
+        except Exception as exc:  # reported as null traffic, never fatal
+            log(f"bench: traffic unavailable: {exc}")
 
     import torch
 
@@ -220,32 +332,36 @@ def main():
     backend = HipRNSBackend()
     rot = int(args.rotate_mb * 1e6)
     log(f"bench: C2 fused QKV M={args.m} K=768 N=2304 R=4, steps={args.steps} warmup={args.warmup}")
-    head = measure_shape(backend, "C2 fused QKV", args.m, 768, 768, 3, args.steps, args.warmup, rot,
-                         17, device)
-    log(f"bench: headline {head['us_per_call_p50']:.2f} us/call, {head['eff_tops']:.1f} eff TOPS, "
-        f"GEMM {head['gemm_kernel_us']:.2f} us")
+    head = measure_shape(backend, "C2 fused QKV", args.m, 768, 768, 3, args.steps, args.warmup,
+                         rot, 17, device)
+    log(f"bench: headline {head['us_per_call_graph']:.2f} us/step (graph), eager p50 "
+        f"{head['us_per_call_p50']:.2f} us, {head['eff_tops']:.1f} eff TOPS")
     rows = [head]
     if not args.no_extra:
-        for m in (1, 16, 128):
-            rows.append(measure_shape(backend, "C2 fused QKV", m, 768, 768, 3, args.steps,
-                                      args.warmup, rot, 17, device))
-            log(f"bench: C2 M={m} {rows[-1]['us_per_call_p50']:.2f} us/call")
-        for req in (1, 2, 4):
-            rows.append(measure_shape(backend, f"C3 decode {req} requests", req, 768, 768, 1,
-                                      args.steps, args.warmup, rot, 33, device))
-            log(f"bench: C3 {req} req {rows[-1]['us_per_call_p50']:.2f} us/call")
-        for m in (1, 512):
-            rows.append(measure_shape(backend, "C5 OPT-6.7B QKV", m, 4096, 4096, 3,
-                                      max(20, args.steps // 4), max(5, args.warmup // 4),
-                                      rot, 67, device))
-            log(f"bench: C5 M={m} {rows[-1]['us_per_call_p50']:.2f} us/call, "
-                f"{rows[-1]['eff_tops']:.1f} eff TOPS")
+        extra = [("C2 fused QKV", m, 768, 768, 3, 17) for m in (1, 16, 128)]
+        extra += [(f"C3 decode {q} requests", q, 768, 768, 1, 33) for q in (1, 2, 4)]
+        extra += [("C5 OPT-6.7B QKV", m, 4096, 4096, 3, 67) for m in (1, 512, 2048)]
+        for name, m, k, n_each, parts, seed in extra:
+            rows.append(measure_shape(backend, name, m, k, n_each, parts, args.steps, args.warmup,
+                                      rot, seed, device))
+            log(f"bench: {name} M={m}: {rows[-1]['us_per_call_graph']:.2f} us/step, "
+                f"{rows[-1]['eff_tops']:.1f} eff TOPS, {rows[-1]['gbs_alg']:.0f} GB/s alg, "
+                f"{rows[-1]['bound']} roofline {rows[-1]['roofline_frac']:.3f}")
 
     cpu = cpu_baseline(args.cpu_seconds)
-    gemm_s = head["gemm_kernel_us"] * 1e-6
-    achieved = head["bytes_alg"] / gemm_s / 1e9
+    achieved = head["bytes_alg"] / (head["ms_per_step"] * 1e-3) / 1e9
+    roofline = {
+        "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": achieved / HBM_PEAK_GBS,
+        "traffic": (traffic["FETCH_SIZE"]["bytes"] + traffic["WRITE_SIZE"]["bytes"]) if traffic else None,
+        "kernel": "GEMM (mfma_kernel / stream_kernel, one launch per step)",
+        "kernel_us": head["us_per_call_graph"],
+        "bytes_alg_per_launch": head["bytes_alg"],
+    }
+    if traffic:
+        roofline["traffic_parts"] = traffic
     line = {
-        "metric": "effective int8 TOPS + us/call, fused-QKV RNS GEMM+reconstruct, bit-exact",
+        "metric": METRIC,
         "value": head["eff_tops"],
         "unit": "effective int8 TOPS",
         "n_gpus": 1,
@@ -263,10 +379,7 @@ def main():
                                "(255,253,251,247), int64 exact output, weights rotated over "
                                f"{head['weight_copies']} copies (> 512 MB)",
                    "m": args.m, "k": 768, "n": 2304, "channels": 4},
-        "roofline": {"bound": head["bound"], "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "gemm (rnsmx_matmul_residues_prepared)",
-                     "kernel_us": head["gemm_kernel_us"]},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "rows": rows,
     }

@@ -112,7 +112,8 @@ int64_t rnsmx_fused_workspace_bytes(int64_t m, int64_t k, int64_t n,
  * Per-channel int8 GEMM on MFMA, modular reduction (Barrett, or the byte
  * LUT `lut_dev` [R][4][256] for channels < lut_channels), Garner mixed
  * radix and signed correction, all in one GEMM epilogue.  No K%4 / N%4
- * restriction.  `workspace_dev` holds the repacked operands.
+ * restriction.  `workspace_dev` holds the repacked operands (B in the
+ * fragment-major order of rnsmx_prepare_weight).
  * Replaces _C.matmul_centered_fused_out (csrc/rns_cuda.cu:887-980: cuBLAS
  * site 478-523 + fused_reduce_garner_kernel 442-476).
  */
@@ -124,12 +125,16 @@ int32_t rnsmx_matmul_centered_fused_out(
 
 /*
  * Weight preparation: b_nk_dev [N][K] (int8/16/32, i.e. the quantized
- * nn.Linear weight, or B transposed) -> packed_dev [R][N][kp] centered
- * residues, kp = round_up(K, RNSMX_K_ALIGN), zero padded.  absmax_dev
- * (nullable, zeroed by the caller) receives max |b| for the adaptive bound.
+ * nn.Linear weight, or B transposed) -> packed_dev, centered residues in
+ * fragment-major order [R][ceil(N/16)][kp/64][1024], kp = round_up(K,
+ * RNSMX_K_ALIGN): byte 16*l + b of the fragment of column block jb and K
+ * step ks is the residue of column 16*jb + (l % 16), K index
+ * 64*ks + 16*(l / 16) + b (zero past N and past K).  That is the B-operand
+ * layout of the gfx950 int8 MFMA, so each operand load is one contiguous
+ * 1 KB.  absmax_dev (nullable, zeroed by the caller) receives max |b| for
+ * the adaptive bound.
  * Replaces CudaRNSBackend.prepare_weight (cuda_backend.py:464-487), whose
- * storage is [R][K][N]; the K-contiguous layout feeds both MFMA operands
- * with 16-byte loads.
+ * storage is [R][K][N].
  */
 int32_t rnsmx_prepare_weight(const void *b_nk_dev, int32_t dtype, int32_t n,
                              int32_t k, const rnsmx_moduli_t *mods,
@@ -196,8 +201,9 @@ int32_t rnsmx_matmul_residues_prepared(
  * Process-wide override of the GEMM kernel choice, for tuning sweeps and
  * for tests that run every kernel family on the same inputs.  kind 0
  * restores the automatic choice; kind 1 = stream kernel (tile 16*mb x 16*nb,
- * ks waves splitting K), kind 2 = MFMA kernel (tile 16*mb x 64*nb).  A tile
- * that is not built makes the next GEMM call fail with RNSMX_EINVAL.  Not
+ * ks waves splitting K), kind 2 = MFMA kernel (tile 16*mb x 64*nb, ks =
+ * K steps of loads in flight, 0 = automatic).  A tile or depth that is not
+ * built makes the next GEMM call fail with RNSMX_EINVAL.  Not
  * thread-safe; results never depend on it.  No counterpart in the reference
  * (cuBLAS picks its own kernels there).
  */

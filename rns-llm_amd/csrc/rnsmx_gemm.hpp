@@ -2,22 +2,23 @@
 // modular reduction, Garner mixed-radix reconstruction, signed correction
 // and optional dequantization fused into the epilogue.
 //
-// Three families, chosen by the number of output rows M:
-//   gemv_kernel    M <= 8       one wave per output column, dot4 on VALU,
-//                               every channel's column read as one contiguous
-//                               run (weight streaming, HBM bound)
-//   stream_kernel  M <= 256     MFMA tiles of (16*MB) x (16*NB), K split over
-//                               the waves of a workgroup, every wave issuing
-//                               all loads of its K slice before its first MFMA
-//   mfma_kernel    M > 256      MFMA tiles of (16*MB) x (64*NB), A staged
-//                               through LDS, B streamed into a register ring,
-//                               P K steps of loads in flight (MFMA bound)
+// Two families, chosen by the number of output rows M and the tile count:
+//   stream_kernel  decode and small batches: MFMA tiles of (16*MB) x (16*NB),
+//                  K split over the waves of a workgroup, every wave issuing
+//                  all loads of its K slice before its first MFMA
+//   mfma_kernel    larger M: tiles of (16*MB) x (64*NB), A staged through
+//                  LDS with quad-contiguous loads, B streamed into a register
+//                  ring, P K steps of loads in flight
 //
 // Layouts: A is [M][a_ld] int8 activations shared by every channel (a_cs = 0;
 // an int8 value is its own representative mod every m_c, so the channel-c
 // product of raw activations has the residue of the product of centered
 // residues) or [R][M][a_ld] centered residue planes.  B is the prepared
-// weight [R][N][b_ld], K contiguous, zero padded to kp (a multiple of 64).
+// weight in fragment-major order [R][N16][kp/64][64 lanes x 16 bytes]: the
+// 1 KB fragment of column block jb and K step ks holds, at byte 16*l, column
+// 16*jb + (l & 15) and K bytes 64*ks + 16*(l >> 4) .. +16, the MFMA B-operand
+// layout, so every B load is one contiguous 1 KB (b_ld = bytes per column
+// block, b_cs = bytes per channel; columns past N and K past K are zero).
 //
 // MFMA v_mfma_i32_16x16x64_i8: lane l feeds A row (l & 15) and B column
 // (l & 15), both with K bytes [16 * (l >> 4), +16) of a 64-byte step, and
@@ -39,8 +40,8 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 struct GemmArgs {
   const int8_t *a;  // [R][M][a_ld] residue planes, or [M][a_ld] int8 (a_cs = 0)
   int64_t a_ld, a_cs;
-  const int8_t *b;  // [R][N][b_ld]
-  int64_t b_ld, b_cs;
+  const int8_t *b;  // [R][N16][kp/64][1024] fragment-major
+  int64_t b_ld, b_cs;  // bytes per column block, per channel
   int32_t m, n, kp;  // kp: multiple of 64, <= b_ld
   int32_t a_k;       // A bytes per row that are read; 16-byte chunks at or past it load as 0
   int32_t tiles_m, tiles_n;  // output tile grid (set at launch)
@@ -61,10 +62,11 @@ struct GemmArgs {
   rnsmx_moduli_t mods;
 };
 
-enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kGemv = 3 };
+enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2 };
 
+// ks: waves splitting K (stream kernel) or ring depth, 0 = automatic (MFMA kernel).
 struct GemmChoice {
-  int kind, mb, nb, ks;  // gemv: mb = rows per wave (1, 2, 4, 8)
+  int kind, mb, nb, ks;
 };
 
 // Per channel-capacity launchers, one translation unit each.
@@ -95,10 +97,19 @@ __device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
   return v;
 }
 
-__device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+// Sum over the 64 lanes of a wave, returned as a wave-uniform value.  DPP
+// row shifts build prefix sums inside each 16-lane row (lane 15 then holds
+// its row's total), two row broadcasts fold the rows into lane 63, and
+// readlane moves that total to a scalar register: 6 DPP adds instead of 6
+// LDS-latency shuffles.
+__device__ __forceinline__ int32_t wave_total(int32_t v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, true);  // row_bcast:15 -> rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, true);  // row_bcast:31 -> rows 2, 3
+  return __builtin_amdgcn_readlane(v, 63);
 }
 
 __device__ __forceinline__ i32x4 load16(const int8_t *p) { return *reinterpret_cast<const i32x4 *>(p); }
@@ -366,105 +377,6 @@ __device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int &mt, int &
 }
 
 // ---------------------------------------------------------------------------
-// GEMV (M <= MR <= 8).  Each wave owns one output column: lane l reads the
-// 16-byte K chunks l, l + 64, ... of that column in every channel (a
-// contiguous run of kp bytes per channel, fully coalesced) and the matching
-// A chunks of every row, accumulating with v_dot4 (4 int8 products per lane
-// per instruction).  U batches of chunks are loaded before any arithmetic.
-// A butterfly sum gives every lane the full dot products; lane r then
-// reconstructs and stores row r.
-// ---------------------------------------------------------------------------
-constexpr int gemv_u_of(int rcap, int mr, bool araw) {
-  const int frags = rcap + (araw ? 1 : rcap) * mr;
-  const int u = 48 / frags;
-  return u < 1 ? 1 : (u > 4 ? 4 : u);
-}
-
-template <int RCAP, int MR, bool ARAW>
-__global__ __launch_bounds__(256) void gemv_kernel(const GemmArgs args) {
-  KGemmArgs &g = kernel_args<GemmArgs>();
-  constexpr int AP = ARAW ? 1 : RCAP;
-  constexpr int U = gemv_u_of(RCAP, MR, ARAW);
-  __shared__ int64_t red[4];
-  __shared__ int bcast;
-  const int c_act = active_channels<RCAP>(g, red, &bcast);
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int col = min(static_cast<int>(blockIdx.x) * 4 + wave, g.n - 1);  // clamped; stored only if in range
-  const bool col_ok = static_cast<int>(blockIdx.x) * 4 + wave < g.n;
-  const int nchunk = g.kp >> 4;
-  const int a_chunks = g.a_k >> 4;
-  const int8_t *bcol = g.b + static_cast<int64_t>(col) * g.b_ld;
-  int64_t boff[RCAP], aoff[AP];
-  static_for<RCAP>([&](auto C) { boff[decltype(C)::value] = plane_off(decltype(C)::value, c_act, g.b_cs); });
-  static_for<AP>([&](auto PP) { aoff[decltype(PP)::value] = plane_off(decltype(PP)::value, c_act, g.a_cs); });
-  const int8_t *arow[MR];
-  static_for<MR>([&](auto R) {
-    constexpr int r = decltype(R)::value;
-    arow[r] = g.a + static_cast<int64_t>(min(r, g.m - 1)) * g.a_ld;
-  });
-  int32_t acc[RCAP][MR];
-  static_for<RCAP>([&](auto C) { static_for<MR>([&](auto R) { acc[C][R] = 0; }); });
-
-  Epi<RCAP> e;
-  load_epi<RCAP>(g, e, c_act);
-  pin_epi<RCAP>(e);
-  for (int q0 = 0; q0 < nchunk; q0 += 64 * U) {
-    i32x4 fb[U][RCAP], fa[U][AP][MR];
-    static_for<U>([&](auto UU) {
-      constexpr int u = decltype(UU)::value;
-      const int q = q0 + lane + 64 * u;
-      const int qb = min(q, nchunk - 1), qa = min(q, a_chunks - 1);
-      const bool av = q < a_chunks;  // a_chunks <= nchunk
-      static_for<RCAP>([&](auto C) {
-        constexpr int c = decltype(C)::value;
-        fb[u][c] = load16(bcol + boff[c] + qb * 16);
-      });
-      static_for<AP>([&](auto PP) {
-        constexpr int p = decltype(PP)::value;
-        static_for<MR>([&](auto R) {
-          constexpr int r = decltype(R)::value;
-          fa[u][p][r] = select16(av, load16(arow[r] + aoff[p] + qa * 16));
-        });
-      });
-    });
-    static_for<U>([&](auto UU) {
-      constexpr int u = decltype(UU)::value;
-      static_for<RCAP>([&](auto C) {
-        constexpr int c = decltype(C)::value;
-        if (c >= c_act) return;
-        static_for<MR>([&](auto R) {
-          constexpr int r = decltype(R)::value;
-          const i32x4 a = fa[u][ARAW ? 0 : c][r], b = fb[u][c];
-          int32_t s = acc[c][r];
-          s = __builtin_amdgcn_sdot4(a.x, b.x, s, false);
-          s = __builtin_amdgcn_sdot4(a.y, b.y, s, false);
-          s = __builtin_amdgcn_sdot4(a.z, b.z, s, false);
-          s = __builtin_amdgcn_sdot4(a.w, b.w, s, false);
-          acc[c][r] = s;
-        });
-      });
-    });
-  }
-
-  static_for<RCAP>([&](auto C) {
-    constexpr int c = decltype(C)::value;
-    if (c >= c_act) return;
-    static_for<MR>([&](auto R) { acc[c][decltype(R)::value] = wave_sum_i32(acc[c][decltype(R)::value]); });
-  });
-  if (col_ok && lane < MR && lane < g.m) {
-    int32_t v[RCAP];
-    static_for<RCAP>([&](auto C) {
-      constexpr int c = decltype(C)::value;
-      v[c] = acc[c][0];
-      static_for<MR>([&](auto R) {
-        if (lane == decltype(R)::value) v[c] = acc[c][decltype(R)::value];
-      });
-    });
-    finish_element<RCAP>(g, e, c_act, v, lane, col);
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Stream GEMM (M <= 256: continuous batches and the C2 shapes).  The weight
 // residues are read once and the problem is a few MB, so latency rules:
 // every wave issues all the loads of a chunk of U K steps before its first
@@ -509,10 +421,11 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
     const int row = min(m0 + i * 16 + (lane & 15), g.m - 1);
     ap[i] = g.a + static_cast<int64_t>(row) * g.a_ld;
   });
+  const int nblk = (g.n + 15) >> 4;
   static_for<NB>([&](auto J) {
     constexpr int j = decltype(J)::value;
-    const int col = min(n0 + j * 16 + (lane & 15), g.n - 1);
-    bp[j] = g.b + static_cast<int64_t>(col) * g.b_ld + kofs;
+    const int jb = min(nt * NB + j, nblk - 1);
+    bp[j] = g.b + static_cast<int64_t>(jb) * g.b_ld + lane * 16;
   });
   int64_t boff[RCAP], aoff[AP];
   static_for<RCAP>([&](auto C) { boff[decltype(C)::value] = plane_off(decltype(C)::value, c_act, g.b_cs); });
@@ -524,11 +437,8 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
     static_for<MB>([&](auto I) { static_for<NB>([&](auto J) { acc[C][I][J] = zero; }); });
   });
 
-  Epi<RCAP> e;
-  load_epi<RCAP>(g, e, c_act);
-  pin_epi<RCAP>(e);
-  for (int q = wave * U; q < nk; q += ks_n * U) {
-    i32x4 fa[U][AP][MB], fb[U][RCAP][NB];
+  i32x4 fa[U][AP][MB], fb[U][RCAP][NB];
+  auto load_chunk = [&](int q) {
     static_for<U>([&](auto UU) {
       constexpr int u = decltype(UU)::value;
       const int ks = min(q + u, nk - 1);
@@ -546,10 +456,12 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
         constexpr int c = decltype(C)::value;
         static_for<NB>([&](auto J) {
           constexpr int j = decltype(J)::value;
-          fb[u][c][j] = load16(bp[j] + boff[c] + ks * 64);
+          fb[u][c][j] = load16(bp[j] + boff[c] + ks * 1024);
         });
       });
     });
+  };
+  auto mfma_chunk = [&]() {
     static_for<U>([&](auto UU) {
       constexpr int u = decltype(UU)::value;
       static_for<RCAP>([&](auto C) {
@@ -565,6 +477,17 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
         });
       });
     });
+  };
+
+  // first chunk in flight before the epilogue constants are waited for
+  load_chunk(wave * U);
+  Epi<RCAP> e;
+  load_epi<RCAP>(g, e, c_act);
+  pin_epi<RCAP>(e);
+  if (wave * U < nk) mfma_chunk();
+  for (int q = wave * U + ks_n * U; q < nk; q += ks_n * U) {
+    load_chunk(q);
+    mfma_chunk();
   }
 
   if (ks_n == 1) {
@@ -646,15 +569,7 @@ constexpr int mfma_ac_of(int rcap, int mb, bool araw) {
   return (chunks + 255) / 256;
 }
 
-// Ring depth: as many K steps of A and B loads as fit in ~220 VGPRs beside
-// the A fragments and addressing, between 2 and 4.
-constexpr int mfma_p_of(int rcap, int mb, int nb, bool araw) {
-  const int per_step = 4 * (rcap * nb + mfma_ac_of(rcap, mb, araw));
-  const int p = (220 - 40 - 4 * mb) / per_step;
-  return p < 2 ? 2 : (p > 4 ? 4 : p);
-}
-
-template <int RCAP, int MB, int NB, bool ARAW>
+template <int RCAP, int MB, int NB, int P, bool ARAW>
 __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
   KGemmArgs &g = kernel_args<GemmArgs>();
   constexpr int BM = 16 * MB, BNW = 16 * NB;
@@ -662,7 +577,6 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
   constexpr int PLANE = BM * kLdsRow;
   constexpr int ACH = AP * BM * 4;  // 16-byte A chunks per K step
   constexpr int AC = mfma_ac_of(RCAP, MB, ARAW);
-  constexpr int P = mfma_p_of(RCAP, MB, NB, ARAW);
   // one spare 16-byte slot takes the stores of threads without an A chunk
   __shared__ __attribute__((aligned(16))) int8_t As[2][AP * PLANE + 16];
   __shared__ int64_t red[4];
@@ -693,10 +607,11 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
     aon[i] = inside && (ARAW || p < c_act);
   });
   const int8_t *bp[NB];
+  const int nblk = (g.n + 15) >> 4;
   static_for<NB>([&](auto J) {
     constexpr int j = decltype(J)::value;
-    const int col = min(n0 + j * 16 + (lane & 15), g.n - 1);
-    bp[j] = g.b + static_cast<int64_t>(col) * g.b_ld + kofs;
+    const int jb = min((n0 >> 4) + j, nblk - 1);
+    bp[j] = g.b + static_cast<int64_t>(jb) * g.b_ld + lane * 16;
   });
   int64_t boff[RCAP];
   static_for<RCAP>([&](auto C) { boff[decltype(C)::value] = plane_off(decltype(C)::value, c_act, g.b_cs); });
@@ -718,7 +633,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
       constexpr int c = decltype(C)::value;
       static_for<NB>([&](auto J) {
         constexpr int j = decltype(J)::value;
-        fb[s][c][j] = load16(bp[j] + boff[c] + kc * 64);
+        fb[s][c][j] = load16(bp[j] + boff[c] + kc * 1024);
       });
     });
   };
@@ -752,7 +667,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
       i32x4 fa[MB];
       static_for<RCAP>([&](auto C) {
         constexpr int c = decltype(C)::value;
-        if (c >= c_act) return;
+        if (c >= c_act || ks >= nk) return;
         if (!ARAW || c == 0) {
           static_for<MB>([&](auto I) {
             constexpr int i = decltype(I)::value;
@@ -796,22 +711,6 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
 // Launchers for one channel capacity (instantiated per translation unit).
 // ---------------------------------------------------------------------------
 template <int RCAP, bool ARAW>
-bool launch_gemv(GemmArgs g, int mr, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>((g.n + 3) / 4));
-#define RNSMX_GEMV(MR_)                                                                  \
-  if (mr == MR_) {                                                                       \
-    hipLaunchKernelGGL((gemv_kernel<RCAP, MR_, ARAW>), grid, dim3(256), 0, st, g);        \
-    return true;                                                                         \
-  }
-  RNSMX_GEMV(1)
-  RNSMX_GEMV(2)
-  RNSMX_GEMV(4)
-  RNSMX_GEMV(8)
-#undef RNSMX_GEMV
-  return false;
-}
-
-template <int RCAP, bool ARAW>
 bool launch_stream(GemmArgs g, int mb, int nb, int ks, hipStream_t st) {
 #define RNSMX_STREAM(MB_, NB_)                                                              \
   if (mb == MB_ && nb == NB_) {                                                             \
@@ -824,49 +723,62 @@ bool launch_stream(GemmArgs g, int mb, int nb, int ks, hipStream_t st) {
   }
   RNSMX_STREAM(1, 1)
   RNSMX_STREAM(2, 1)
-  RNSMX_STREAM(4, 1)
   if constexpr (RCAP <= 4) {
+    RNSMX_STREAM(4, 1)
     RNSMX_STREAM(1, 2)
-    RNSMX_STREAM(2, 2)
-    RNSMX_STREAM(4, 2)
   }
 #undef RNSMX_STREAM
   return false;
 }
 
+// p_req: ring depth (K steps of A and B loads in flight), 0 = the tile's
+// default.  Deeper rings than 3-4 steps cost occupancy (registers) and
+// measured slower on every shape tried.
 template <int RCAP, bool ARAW>
-bool launch_mfma(GemmArgs g, int mb, int nb, hipStream_t st) {
-#define RNSMX_MFMA(MB_, NB_)                                                          \
-  if (mb == MB_ && nb == NB_) {                                                       \
-    g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                                    \
-    g.tiles_n = (g.n + 64 * NB_ - 1) / (64 * NB_);                                    \
-    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));                    \
-    hipLaunchKernelGGL((mfma_kernel<RCAP, MB_, NB_, ARAW>), grid, dim3(256), 0, st, g); \
-    return true;                                                                      \
+bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, hipStream_t st) {
+#define RNSMX_MFMA_P(MB_, NB_, P_)                                                          \
+  if (p == P_) {                                                                            \
+    hipLaunchKernelGGL((mfma_kernel<RCAP, MB_, NB_, P_, ARAW>), grid, dim3(256), 0, st, g); \
+    return true;                                                                            \
+  }
+#define RNSMX_MFMA(MB_, NB_, PDEF, ...)                                    \
+  if (mb == MB_ && nb == NB_) {                                            \
+    g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                         \
+    g.tiles_n = (g.n + 64 * NB_ - 1) / (64 * NB_);                         \
+    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));         \
+    const int p = p_req > 0 ? p_req : PDEF;                                \
+    __VA_ARGS__                                                            \
+    return false;                                                          \
   }
   if constexpr (RCAP <= 4) {
-    RNSMX_MFMA(8, 2)
-    RNSMX_MFMA(4, 2)
-    RNSMX_MFMA(4, 4)
+    RNSMX_MFMA(2, 1, 3, RNSMX_MFMA_P(2, 1, 3) RNSMX_MFMA_P(2, 1, 4))
+    RNSMX_MFMA(4, 1, 4, RNSMX_MFMA_P(4, 1, 3) RNSMX_MFMA_P(4, 1, 4))
+    RNSMX_MFMA(2, 2, 3, RNSMX_MFMA_P(2, 2, 3) RNSMX_MFMA_P(2, 2, 4))
+    RNSMX_MFMA(4, 2, 3, RNSMX_MFMA_P(4, 2, 3) RNSMX_MFMA_P(4, 2, 4))
+    RNSMX_MFMA(8, 2, 3, RNSMX_MFMA_P(8, 2, 3) RNSMX_MFMA_P(8, 2, 4))
   } else if constexpr (RCAP == 6) {
-    RNSMX_MFMA(4, 2)
-  } else {
-    RNSMX_MFMA(2, 2)
+    RNSMX_MFMA(2, 1, 3, RNSMX_MFMA_P(2, 1, 3) RNSMX_MFMA_P(2, 1, 4))
+    RNSMX_MFMA(4, 1, 3, RNSMX_MFMA_P(4, 1, 3) RNSMX_MFMA_P(4, 1, 4))
+    RNSMX_MFMA(4, 2, 3, RNSMX_MFMA_P(4, 2, 3))
+  } else {  // registers allow no more
+    RNSMX_MFMA(2, 1, 3, RNSMX_MFMA_P(2, 1, 3))
+    RNSMX_MFMA(4, 1, 3, RNSMX_MFMA_P(4, 1, 3))
+    RNSMX_MFMA(2, 2, 2, RNSMX_MFMA_P(2, 2, 2))
   }
 #undef RNSMX_MFMA
+#undef RNSMX_MFMA_P
   return false;
 }
 
 template <int RCAP>
 bool launch_gemm_rcap(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st) {
   switch (c.kind) {
-    case kGemv:
-      return araw ? launch_gemv<RCAP, true>(g, c.mb, st) : launch_gemv<RCAP, false>(g, c.mb, st);
     case kStream:
       return araw ? launch_stream<RCAP, true>(g, c.mb, c.nb, c.ks, st)
                   : launch_stream<RCAP, false>(g, c.mb, c.nb, c.ks, st);
     case kMfma:
-      return araw ? launch_mfma<RCAP, true>(g, c.mb, c.nb, st) : launch_mfma<RCAP, false>(g, c.mb, c.nb, st);
+      return araw ? launch_mfma<RCAP, true>(g, c.mb, c.nb, c.ks, st)
+                  : launch_mfma<RCAP, false>(g, c.mb, c.nb, c.ks, st);
     default:
       return false;
   }

@@ -121,6 +121,64 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(const EncodeArgs e) {
   }
 }
 
+// Weight preparation into the fragment-major layout the GEMM kernels read:
+// [R][N16][nk][64 lanes x 16 bytes] (N16 = ceil(N/16), nk = kp/64).  Lane l
+// of fragment (column block jb, K step ks) holds column 16*jb + (l & 15),
+// K bytes 64*ks + 16*(l >> 4) .. +16: the v_mfma_i32_16x16x64_i8 B-operand
+// layout, so a fragment is one contiguous 1 KB load in which every group of
+// four lanes reads 64 consecutive bytes.  One wave per column block: lane l
+// reads 16 K values of source row n = 16*jb + (l & 15) per step and writes
+// 16 bytes at fragment offset 16*l for every channel.  Columns past N and K
+// values past K are zero; max |b| is folded into absmax.
+template <typename T>
+__global__ __launch_bounds__(256) void encode_frag_kernel(const EncodeArgs e) {
+  const int lane = threadIdx.x & 63;
+  const int64_t jb = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t n16 = (e.rows + 15) / 16;
+  if (jb >= n16) return;
+  const int64_t n = jb * 16 + (lane & 15);
+  const bool row_ok = n < e.rows;
+  const T *src = static_cast<const T *>(e.values) + (row_ok ? n : 0) * e.cols;
+  const bool vec = (e.cols % 16) == 0;
+  const int64_t nk = e.out_ld / 64;
+  int8_t *dst = e.out + jb * nk * 1024 + lane * 16;
+  int32_t amax = 0;
+  const int R = e.mods.channels;
+  for (int64_t ks = 0; ks < nk; ++ks) {
+    const int64_t k0 = ks * 64 + (lane >> 4) * 16;
+    int32_t v[16];
+    if (row_ok && vec && k0 + 16 <= e.cols) {
+      load16<T>(src + k0, v);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) v[q] = (row_ok && k0 + q < e.cols) ? static_cast<int32_t>(src[k0 + q]) : 0;
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int32_t a = v[q] < 0 ? -v[q] : v[q];  // |INT32_MIN| wraps to INT32_MIN: largest unsigned
+      amax = static_cast<uint32_t>(a) > static_cast<uint32_t>(amax) ? a : amax;
+    }
+    for (int c = 0; c < R; ++c) {
+      const uint32_t m = static_cast<uint32_t>(e.mods.moduli[c]);
+      const uint32_t magic = e.mods.magic[c], c31 = e.mods.c31[c];
+      i32x4 w;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          packed |= (static_cast<uint32_t>(centered_i32(v[4 * d + q], m, magic, c31)) & 0xFFu) << (8 * q);
+        w[d] = static_cast<int32_t>(packed);
+      }
+      *reinterpret_cast<i32x4 *>(dst + c * e.plane + ks * 1024) = w;
+    }
+  }
+  if (e.absmax != nullptr) {
+    int64_t am = wave_max_i64(static_cast<int64_t>(static_cast<uint32_t>(amax)));
+    if (lane == 0) atomicMax(e.absmax, static_cast<int32_t>(am > INT_MAX ? INT_MAX : am));
+  }
+}
+
 // Flat form of the reference encoder: values [numel] -> [R][numel].
 template <typename T>
 __global__ __launch_bounds__(256) void encode_flat_kernel(const EncodeArgs e) {
@@ -208,25 +266,32 @@ __global__ __launch_bounds__(256) void decode_garner_kernel(const DecodeArgs a) 
 // ---------------------------------------------------------------------------
 // Repacking for the drop-in op (reference layouts -> K-contiguous, padded)
 // ---------------------------------------------------------------------------
-// src [R][K][N] -> dst [R][N][ld], zero in [K, ld); 64 x 64 byte tiles via LDS.
-__global__ __launch_bounds__(256) void transpose_kn_kernel(const int8_t *__restrict__ src,
-                                                           int64_t k, int64_t n, int64_t ld,
-                                                           int8_t *__restrict__ dst) {
-  __shared__ int8_t tile[64][65];
-  const int64_t c = blockIdx.z;
-  const int64_t k0 = static_cast<int64_t>(blockIdx.y) * 64, n0 = static_cast<int64_t>(blockIdx.x) * 64;
-  const int8_t *s = src + c * k * n;
-  int8_t *d = dst + c * n * ld;
-  for (int q = threadIdx.x; q < 64 * 64; q += 256) {
-    const int r = q >> 6, col = q & 63;
-    const int64_t kk = k0 + r, nn = n0 + col;
-    tile[r][col] = (kk < k && nn < n) ? s[kk * n + nn] : static_cast<int8_t>(0);
-  }
-  __syncthreads();
-  for (int q = threadIdx.x; q < 64 * 64; q += 256) {
-    const int r = q >> 6, col = q & 63;  // r indexes n, col indexes k
-    const int64_t nn = n0 + r, kk = k0 + col;
-    if (nn < n && kk < ld) d[nn * ld + kk] = tile[col][r];
+// src [R][K][N] (the reference layout) -> the fragment-major layout of
+// encode_frag_kernel, zero padded: one thread per 16-byte fragment slot.
+__global__ __launch_bounds__(256) void transpose_frag_kernel(const int8_t *__restrict__ src, int64_t k,
+                                                             int64_t n, int64_t n16, int64_t nk,
+                                                             int64_t total, int8_t *__restrict__ dst) {
+  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < total;
+       q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int lane = static_cast<int>(q & 63);
+    int64_t t = q >> 6;
+    const int64_t ks = t % nk;
+    t /= nk;
+    const int64_t jb = t % n16, c = t / n16;
+    const int64_t nn = jb * 16 + (lane & 15), kb = ks * 64 + (lane >> 4) * 16;
+    uint32_t word[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+      const int64_t kk = kb + b;
+      const uint32_t v = (nn < n && kk < k) ? static_cast<uint8_t>(src[(c * k + kk) * n + nn]) : 0u;
+      word[b >> 2] |= v << (8 * (b & 3));
+    }
+    i32x4 w;
+    w[0] = static_cast<int32_t>(word[0]);
+    w[1] = static_cast<int32_t>(word[1]);
+    w[2] = static_cast<int32_t>(word[2]);
+    w[3] = static_cast<int32_t>(word[3]);
+    *reinterpret_cast<i32x4 *>(dst + q * 16) = w;
   }
 }
 
@@ -270,37 +335,40 @@ static int stream_ks_cap(int rcap, int mb, int nb) {
   return per_ws > kStreamLdsMax ? 1 : 4;
 }
 
-// Kernel family and tile for an M x N x kp problem: dot4 GEMV for up to 8
-// rows (weight streaming), the stream kernel (K split over waves) up to 256
-// rows, the MFMA kernel (128-row tiles for up to 4 channels) beyond.
+// Kernel family and tile for an M x N x kp problem, from sweeps on MI355X
+// (K = 768 and 4096, N = 2304 and 12288).  Up to 128 rows the stream kernel
+// (K split over 4 waves) keeps the most weight loads in flight.  Beyond
+// that the MFMA kernel: 128 x 128 tiles once they alone give >= 1024
+// workgroups (their weight reuse then pays for one wave per SIMD), else
+// 64 x 64 tiles (two waves per SIMD) while they give >= 256 workgroups,
+// else 32 x 64 tiles.
 static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   const int rcap = rcap_for(g.mods.channels);
   const int nk = g.kp / 64;
+  auto tiles = [&](int mb, int nbw) {
+    return static_cast<int64_t>((g.m + 16 * mb - 1) / (16 * mb)) * ((g.n + nbw - 1) / nbw);
+  };
   GemmChoice c{};
-  if (g.m <= 8) {
-    c.kind = kGemv;
-    c.mb = g.m <= 1 ? 1 : (g.m <= 2 ? 2 : (g.m <= 4 ? 4 : 8));
-    return c;
-  }
-  if (g.m <= 256) {
+  if (g.m <= 128) {
     c.kind = kStream;
-    c.mb = g.m <= 16 ? 1 : 2;
+    c.mb = g.m <= 64 ? 1 : 2;
     c.nb = 1;
+    if (rcap > 4 && c.mb > 2) c.mb = 2;
     const int u = stream_u_of(rcap, araw, c.mb, c.nb);
-    const int want = g.m <= 16 ? 4 : (g.m < 256 ? 2 : 1);
-    c.ks = std::min(std::min(want, stream_ks_cap(rcap, c.mb, c.nb)), std::max(1, (nk + u - 1) / u));
+    c.ks = std::min(stream_ks_cap(rcap, c.mb, c.nb), std::max(1, (nk + u - 1) / u));
     return c;
   }
   c.kind = kMfma;
-  if (rcap <= 4) {
+  c.ks = 0;  // the tile's default ring depth
+  if (rcap <= 4 && tiles(8, 128) >= 1024) {
     c.mb = 8;
     c.nb = 2;
-  } else if (rcap == 6) {
+  } else if (tiles(4, 64) >= 256) {
     c.mb = 4;
-    c.nb = 2;
+    c.nb = 1;
   } else {
     c.mb = 2;
-    c.nb = 2;
+    c.nb = 1;
   }
   return c;
 }
@@ -309,10 +377,6 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
 static int32_t launch_gemm(const GemmArgs &g, bool araw, hipStream_t st) {
   const int rcap = rcap_for(g.mods.channels);
   GemmChoice c = g_override.kind != kAuto ? g_override : choose_gemm(g, araw);
-  if (c.kind == kGemv && g.m > c.mb) {
-    set_error("GEMV kernel for %d rows cannot take M = %d", c.mb, g.m);
-    return RNSMX_EINVAL;
-  }
   if (c.kind == kStream) {
     const int cap = stream_ks_cap(rcap, c.mb, c.nb);
     if (c.ks < 1 || c.ks > cap) {
@@ -332,7 +396,7 @@ static int32_t launch_gemm(const GemmArgs &g, bool araw, hipStream_t st) {
               g.mods.channels);
     return RNSMX_EINVAL;
   }
-  return check_launch(c.kind == kStream ? "gemm_stream" : (c.kind == kMfma ? "gemm_mfma" : "gemm_gemv"));
+  return check_launch(c.kind == kStream ? "gemm_stream" : "gemm_mfma");
 }
 
 static int32_t launch_encode_rows(int32_t dtype, const EncodeArgs &e, hipStream_t st) {
@@ -414,7 +478,7 @@ int64_t rnsmx_fused_workspace_bytes(int64_t m, int64_t k, int64_t n, int32_t cha
   // room for a padded copy of A (used when K % 16 != 0 or A is not 16-byte
   // aligned) followed by B repacked to [R][N][kp]
   const int64_t a = round_up(channels * m * kp, 256);
-  const int64_t b = round_up(channels * n * kp, 256);
+  const int64_t b = round_up(channels * ((n + 15) / 16) * 16 * kp, 256);
   return a + b;
 }
 
@@ -458,11 +522,13 @@ int32_t rnsmx_matmul_centered_fused_out(const int8_t *a_dev, const int8_t *b_dev
     a_ld = kp;
     a_k = kp;
   }
+  const int64_t n16 = (n + 15) / 16, nk = kp / 64;
   {
-    const dim3 grid((n + 63) / 64, static_cast<unsigned>((kp + 63) / 64), R);
-    hipLaunchKernelGGL(transpose_kn_kernel, grid, dim3(256), 0, st, b_dev, static_cast<int64_t>(k),
-                       static_cast<int64_t>(n), kp, b_nk);
-    if (int32_t rc = check_launch("transpose_kn")) return rc;
+    const int64_t total = R * n16 * nk * 64;
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 16384));
+    hipLaunchKernelGGL(transpose_frag_kernel, dim3(blocks), dim3(256), 0, st, b_dev, static_cast<int64_t>(k),
+                       static_cast<int64_t>(n), n16, nk, total, b_nk);
+    if (int32_t rc = check_launch("transpose_frag")) return rc;
   }
   GemmArgs g{};
   g.a = a_use;
@@ -470,8 +536,8 @@ int32_t rnsmx_matmul_centered_fused_out(const int8_t *a_dev, const int8_t *b_dev
   g.a_cs = a_ld * m;
   g.a_k = static_cast<int32_t>(a_k);
   g.b = b_nk;
-  g.b_ld = kp;
-  g.b_cs = kp * n;
+  g.b_ld = kp * 16;
+  g.b_cs = kp * 16 * n16;
   g.m = m;
   g.n = n;
   g.kp = static_cast<int32_t>(kp);
@@ -497,17 +563,26 @@ int32_t rnsmx_prepare_weight(const void *b_nk_dev, int32_t dtype, int32_t n, int
   if (!aligned16(b_nk_dev) || !aligned16(packed_dev))
     return fail(RNSMX_EINVAL, "weight buffers must be 16-byte aligned");
   const int64_t kp = round_up(k, RNSMX_K_ALIGN);
+  const int64_t n16 = (static_cast<int64_t>(n) + 15) / 16;
   EncodeArgs e{};
   e.values = b_nk_dev;
   e.rows = n;
   e.cols = k;
   e.out_ld = kp;
-  e.plane = static_cast<int64_t>(n) * kp;
+  e.plane = n16 * kp * 16;
   e.out = packed_dev;
   e.row_l1 = nullptr;
   e.absmax = absmax_dev;
   e.mods = *mods;
-  return launch_encode_rows(dtype, e, static_cast<hipStream_t>(stream));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>((n16 + 3) / 4)), block(256);
+  switch (dtype) {
+    case RNSMX_INT8: hipLaunchKernelGGL(encode_frag_kernel<int8_t>, grid, block, 0, st, e); break;
+    case RNSMX_INT16: hipLaunchKernelGGL(encode_frag_kernel<int16_t>, grid, block, 0, st, e); break;
+    default: hipLaunchKernelGGL(encode_frag_kernel<int32_t>, grid, block, 0, st, e); break;
+  }
+  return check_launch("encode_frag");
+
 }
 
 int64_t rnsmx_prepared_workspace_bytes(int64_t m, int64_t k, int32_t channels) {
@@ -586,8 +661,8 @@ int32_t rnsmx_matmul_prepared_fused(const void *a_dev, int32_t a_dtype, int32_t 
     g.a_k = static_cast<int32_t>(kp);
   }
   g.b = packed_dev;
-  g.b_ld = kp;
-  g.b_cs = kp * n;
+  g.b_ld = kp * 16;
+  g.b_cs = kp * 16 * ((n + 15) / 16);
   g.m = m;
   g.n = n;
   g.kp = static_cast<int32_t>(kp);
@@ -639,8 +714,8 @@ int32_t rnsmx_matmul_residues_prepared(const int8_t *a_res_dev, int64_t a_ld, in
   g.a_cs = a_ld * m;
   g.a_k = static_cast<int32_t>(kp);
   g.b = packed_dev;
-  g.b_ld = kp;
-  g.b_cs = kp * n;
+  g.b_ld = kp * 16;
+  g.b_cs = kp * 16 * ((n + 15) / 16);
   g.m = m;
   g.n = n;
   g.kp = static_cast<int32_t>(kp);
@@ -663,8 +738,7 @@ int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb, int32_t ks
     g_override = GemmChoice{kAuto, 0, 0, 0};
     return RNSMX_OK;
   }
-  if (kind != kStream && kind != kMfma && kind != kGemv)
-    return fail(RNSMX_EINVAL, "kind must be 0 (auto), 1 (stream), 2 (mfma) or 3 (gemv)");
+  if (kind != kStream && kind != kMfma) return fail(RNSMX_EINVAL, "kind must be 0 (auto), 1 (stream) or 2 (mfma)");
   if (mb < 1 || nb < 1) return fail(RNSMX_EINVAL, "tile blocks must be positive");
   g_override = GemmChoice{kind, mb, nb, ks};
   return RNSMX_OK;

@@ -8,8 +8,9 @@ computation goes through ``librnsmx.so`` (``include/rnsmx.h``); there is no
 host or torch fallback for the integer path.
 
 Deliberate deviations (each keeps results bit-identical):
-  * prepared weights are stored K-contiguous ``[R, N, kp]`` (``packed``); the
-    public ``residues`` field is the reference-shaped ``[R, K, N]`` view of it;
+  * prepared weights are stored fragment-major ``[R, N/16, kp/64, 1024]``
+    (``packed``, the MFMA operand layout); the public ``residues`` field is
+    the reference-shaped ``[R, K, N]`` tensor, unpacked on first access;
   * ``kernel`` names are ``"mfma"``; ``RNSLinear`` asks ``supports_fused`` instead
     of comparing the kernel string with ``"cublas"``;
   * the workspace's ``accumulators`` tensor is byte scratch sized by the
@@ -21,6 +22,7 @@ Deliberate deviations (each keeps results bit-identical):
 from __future__ import annotations
 
 import ctypes
+import functools
 from collections import Counter
 from collections.abc import Mapping
 from dataclasses import dataclass, field
@@ -53,17 +55,30 @@ class _DeviceConstants:
 class PreparedRNSWeight:
     """Weight encoded once into centered residue planes.
 
-    ``residues`` has the reference shape ``[R, K, N]`` (a view); ``packed`` is
-    the K-contiguous ``[R, N, kp]`` storage the kernels read.
+    ``packed`` is the storage the kernels read, fragment-major
+    ``[R, ceil(N/16), kp/64, 1024]``: the 1 KB fragment of column block ``jb``
+    and K step ``ks`` holds, at byte ``16*l``, column ``16*jb + l % 16`` and K
+    bytes ``64*ks + 16*(l // 16)`` .. ``+16`` (zero past N and K).
+    ``residues`` is the reference-shaped ``[R, K, N]`` tensor, unpacked from
+    it on first access.
     """
 
-    residues: torch.Tensor
     moduli: tuple[int, ...]
     k: int
     n: int
     kernel: str
-    packed: torch.Tensor | None = None
+    packed: torch.Tensor
     absmax: torch.Tensor | None = None  # int32 [1], max |B| on the device
+
+    @functools.cached_property
+    def residues(self) -> torch.Tensor:
+        r, n16, nk, _ = self.packed.shape
+        planes = self.packed.view(r, n16, nk, 4, 16, 16).permute(0, 2, 3, 5, 1, 4)
+        return planes.reshape(r, nk * 64, n16 * 16)[:, :self.k, :self.n]
+
+    @property
+    def kp(self) -> int:
+        return int(self.packed.shape[2]) * _native.K_ALIGN
 
 
 @dataclass
@@ -422,16 +437,16 @@ class HipRNSBackend:
         consts = self._constants(b_nk.device, mods)
         r = len(mods)
         kp = (k + _native.K_ALIGN - 1) // _native.K_ALIGN * _native.K_ALIGN
-        packed = torch.empty((r, n, kp), dtype=torch.int8, device=b_nk.device)
+        packed = torch.empty((r, (n + 15) // 16, kp // _native.K_ALIGN, 1024), dtype=torch.int8,
+                             device=b_nk.device)
         absmax = torch.zeros((1,), dtype=torch.int32, device=b_nk.device)
         self._stats["encode_centered_calls"] += 1
         self._stats["encode_centered_values"] += int(b_nk.numel())
         _native.check(self._lib.rnsmx_prepare_weight(
             _aligned(b_nk).data_ptr(), _native.dtype_code(b_nk.dtype), n, k, consts.native_ref,
             packed.data_ptr(), absmax.data_ptr(), _stream_handle(b_nk.device)))
-        residues = packed[:, :, :k].transpose(1, 2)
-        return PreparedRNSWeight(residues=residues, moduli=mods, k=k, n=n, kernel=kernel,
-                                 packed=packed, absmax=absmax)
+        return PreparedRNSWeight(moduli=mods, k=k, n=n, kernel=kernel, packed=packed,
+                                 absmax=absmax)
 
     def prepare_weight(self, b: torch.Tensor, moduli: Iterable[int]) -> PreparedRNSWeight:
         """B [K, N] int8/int16/int32 -> prepared centered residues."""
@@ -462,7 +477,7 @@ class HipRNSBackend:
             raise ValueError("a must be int8/int16/int32")
         if int(a.shape[1]) != prepared.k:
             raise ValueError("K dimension does not match prepared weight")
-        if a.device != prepared.residues.device:
+        if a.device != prepared.packed.device:
             raise ValueError("activation and prepared weight must share device")
         if not self.supports_fused(prepared):
             raise ValueError("prepared weight was not built by this backend")
@@ -531,7 +546,7 @@ class HipRNSBackend:
         prepared weight's K alignment (the layout the GEMM reads)."""
         self._check_activation(a, prepared_weight)
         m, k = int(a.shape[0]), prepared_weight.k
-        kp = int(prepared_weight.packed.shape[2])
+        kp = prepared_weight.kp
         r = len(prepared_weight.moduli)
         if out is None:
             out = torch.empty((r, m, kp), dtype=torch.int8, device=a.device)
@@ -553,7 +568,7 @@ class HipRNSBackend:
         if a_residues.ndim != 3 or a_residues.dtype != torch.int8 or not a_residues.is_contiguous():
             raise ValueError("a_residues must be a contiguous int8 [R, M, kp] tensor")
         r, m, kp = map(int, a_residues.shape)
-        if r != len(prepared_weight.moduli) or kp != int(prepared_weight.packed.shape[2]):
+        if r != len(prepared_weight.moduli) or kp != prepared_weight.kp:
             raise ValueError("a_residues do not match the prepared weight")
         if lut_channels not in (0, 1, 2):
             raise ValueError("lut_channels must be 0, 1 or 2")
@@ -607,10 +622,9 @@ class HipRNSBackend:
         for c in range(min_channels, len(full.moduli) + 1):
             prefix = full.moduli[:c]
             kernel = self.select_centered_kernel(k=full.k, n=full.n, moduli=prefix,
-                                                 requested="auto", device=full.residues.device)
-            variants[c] = PreparedRNSWeight(
-                residues=full.residues[:c], moduli=prefix, k=full.k, n=full.n, kernel=kernel,
-                packed=full.packed[:c], absmax=full.absmax)
+                                                 requested="auto", device=full.packed.device)
+            variants[c] = PreparedRNSWeight(moduli=prefix, k=full.k, n=full.n, kernel=kernel,
+                                            packed=full.packed[:c], absmax=full.absmax)
         return PreparedAdaptiveRNSWeight(variants, full.moduli, full.absmax, min_channels)
 
     def select_adaptive_variant(self, a: torch.Tensor, prepared: PreparedAdaptiveRNSWeight):

@@ -154,7 +154,7 @@ class RNSLinear(nn.Module):
             prepared = self.backend.prepare_weight(quantized.transpose(0, 1).contiguous(),
                                                    self.moduli)
         self._weight_scale = scale.squeeze(1).to(self.weight.device).contiguous()
-        self._weight_residues = prepared.residues
+        self._weight_residues = prepared.packed
         self._prepared_weight = prepared
         self._adaptive_prepared_weight = adaptive_prepared
         self._prepared_weight_version = version
