@@ -40,12 +40,15 @@ __device__ __forceinline__ uint32_t mod_u32(uint32_t x, uint32_t m, uint32_t mag
 // 32-bit integer multiplies are quarter rate).  m24 = floor(2^24 / m).
 // Writing 2^24/m = m24 + f with 0 <= f < 1, x*m24/2^24 = x/m - x*f/2^24 and
 // x*f/2^24 < 1, so q = floor(x*m24/2^24) is floor(x/m) or floor(x/m) - 1 and
-// x - q*m lies in [0, 2m): one conditional subtraction finishes.
-__device__ __forceinline__ uint32_t mod_small(uint32_t x, uint32_t m, uint32_t m24) {
+// x - q*m lies in [0, 2m): one conditional subtraction finishes.  q <= m24
+// <= 2^23 - 1 for m >= 2 (x < 2^24), so x - q*m is one signed 24-bit
+// multiply-add (the unsigned form is selected as a 32-bit multiply).
+// negm = -m, precomputed by the caller.
+__device__ __forceinline__ uint32_t mod_small(uint32_t x, uint32_t m, uint32_t m24, int32_t negm) {
   const uint64_t p = static_cast<uint64_t>(x & 0xFFFFFFu) * static_cast<uint64_t>(m24 & 0xFFFFFFu);
-  const uint32_t q = static_cast<uint32_t>(p >> 24);
-  const uint32_t r = x - __umul24(q, m);
-  return r >= m ? r - m : r;
+  const int32_t q = static_cast<int32_t>(p >> 24);
+  const uint32_t r = static_cast<uint32_t>(static_cast<int32_t>(x) + __mul24(q, negm));
+  return min(r, r - m);  // r < m: r - m wraps above r
 }
 
 // Constants of the 24-bit reduction of one modulus, all derived from
@@ -55,10 +58,11 @@ struct FastMod {
   uint32_t m24;   // floor(2^24 / m)
   uint32_t c16;   // 2^16 mod m
   uint32_t bias;  // m * floor(2^23 / m), a multiple of m in (2^23 - m, 2^23]
+  int32_t negm;   // -m
 };
 
 __device__ __forceinline__ FastMod fast_mod_of(uint32_t m, uint32_t magic) {
-  return FastMod{m, magic >> 8, 65536u - (magic >> 16) * m, m * (magic >> 9)};
+  return FastMod{m, magic >> 8, 65536u - (magic >> 16) * m, m * (magic >> 9), -static_cast<int32_t>(m)};
 }
 
 // Canonical residue in [0, m) of any int32 v.  v = hi * 2^16 + lo with
@@ -71,7 +75,7 @@ __device__ __forceinline__ uint32_t canon_fast(int32_t v, const FastMod &f) {
   const int32_t hi = v >> 16;
   const uint32_t lo = static_cast<uint32_t>(v) & 0xFFFFu;
   const uint32_t t = static_cast<uint32_t>(__mul24(hi, static_cast<int32_t>(f.c16))) + lo + f.bias;
-  return mod_small(t, f.m, f.m24);
+  return mod_small(t, f.m, f.m24, f.negm);
 }
 
 // Canonical residue in [0, m) of a signed 32-bit value.

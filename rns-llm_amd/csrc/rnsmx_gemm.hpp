@@ -69,11 +69,27 @@ struct GemmChoice {
   int kind, mb, nb, ks;
 };
 
-// Per channel-capacity launchers, one translation unit each.
-bool launch_gemm_r3(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st);
-bool launch_gemm_r4(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st);
-bool launch_gemm_r6(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st);
-bool launch_gemm_r10(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st);
+// The kernels are instantiated in parts, one translation unit each
+// (rnsmx_gemm_part.hip built once per channel capacity R and part P) so the
+// library compiles in parallel:
+//   P0 stream kernels, P1 MFMA kernels with raw int8 A and 64-column tiles,
+//   P2 MFMA kernels with raw int8 A and 128-column tiles, P3 MFMA kernels
+//   with residue-plane A.
+// launch_gemm_rR_pP returns false when the part has no kernel for the choice.
+inline int gemm_part_of(const GemmChoice &c, bool araw) {
+  if (c.kind == kStream) return 0;
+  if (!araw) return 3;
+  return c.nb == 1 ? 1 : 2;
+}
+#define RNSMX_GEMM_PART_NAME(R, P) launch_gemm_r##R##_p##P
+#define RNSMX_GEMM_PART_DECL(R, P) \
+  bool RNSMX_GEMM_PART_NAME(R, P)(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st);
+#define RNSMX_GEMM_PARTS_DECL(R) \
+  RNSMX_GEMM_PART_DECL(R, 0) RNSMX_GEMM_PART_DECL(R, 1) RNSMX_GEMM_PART_DECL(R, 2) RNSMX_GEMM_PART_DECL(R, 3)
+RNSMX_GEMM_PARTS_DECL(3)
+RNSMX_GEMM_PARTS_DECL(4)
+RNSMX_GEMM_PARTS_DECL(6)
+RNSMX_GEMM_PARTS_DECL(10)
 
 // Kernel arguments read in place from the kernarg segment (constant address
 // space, scalar loads).  A by-value struct parameter used as an ordinary
@@ -113,6 +129,17 @@ __device__ __forceinline__ int32_t wave_total(int32_t v) {
 }
 
 __device__ __forceinline__ i32x4 load16(const int8_t *p) { return *reinterpret_cast<const i32x4 *>(p); }
+
+// Initial value of one MFMA accumulator: zero, hidden from the compiler.
+// With a plain constant every accumulator of a K loop starts from the same
+// folded zero, and the register allocator then keeps rotating accumulators
+// between registers inside the loop (accvgpr moves and copies around every
+// MFMA); a distinct opaque zero per accumulator avoids that.
+__device__ __forceinline__ i32x4 acc_zero() {
+  i32x4 z = {0, 0, 0, 0};
+  asm volatile("" : "+v"(z));
+  return z;
+}
 
 // prefix[idx] for a runtime idx <= RCAP, as a select chain over constant
 // indices: a runtime index into the kernel-argument block would make the
@@ -180,6 +207,7 @@ __device__ __forceinline__ int active_channels(KGemmArgs &g, int64_t *red, int *
 template <int RCAP>
 struct Epi {
   uint32_t m[RCAP], m24[RCAP], c16[RCAP], bias[RCAP], qinv[RCAP];
+  int32_t negm[RCAP];
   uint32_t u[RCAP][RCAP];  // u[j][c], j < c
   int64_t prefix[RCAP + 1];
   int64_t p_act;  // prefix[c_act], the modulus of the signed correction
@@ -206,6 +234,7 @@ __device__ __forceinline__ void fill_moduli(Epi<RCAP> &e, const Mods &mods, int 
     e.m24[c] = magic >> 8;
     e.c16[c] = 65536u - (magic >> 16) * m;
     e.bias[c] = m * (magic >> 9);
+    e.negm[c] = -static_cast<int32_t>(m);
   });
   static_for<RCAP + 1>([&](auto C) { e.prefix[decltype(C)::value] = mods.prefix[decltype(C)::value]; });
   e.p_act = prefix_at<RCAP>(mods, c_act);
@@ -248,6 +277,7 @@ __device__ __forceinline__ void pin_epi(Epi<RCAP> &e) {
     pin_sgpr(e.m24[c]);
     pin_sgpr(e.c16[c]);
     pin_sgpr(e.bias[c]);
+    pin_sgpr(e.negm[c]);
     pin_sgpr(e.qinv[c]);
     static_for<c>([&](auto J) { pin_sgpr(e.u[decltype(J)::value][c]); });
   });
@@ -268,7 +298,7 @@ __device__ __forceinline__ void pin_epi(Epi<RCAP> &e) {
 template <int RCAP>
 __device__ __forceinline__ uint32_t reduce_acc(KGemmArgs &g, const Epi<RCAP> &e, int c, int32_t v) {
   if (c < e.lut_channels) return canon_i32_lut(v, g.lut + c * 1024, e.m[c], g.mods.c31[c]);
-  return canon_fast(v, FastMod{e.m[c], e.m24[c], e.c16[c], e.bias[c]});
+  return canon_fast(v, FastMod{e.m[c], e.m24[c], e.c16[c], e.bias[c], e.negm[c]});
 }
 
 // Signed integer from the canonical residues r[0..c_act) of the first c_act
@@ -297,7 +327,7 @@ __device__ __forceinline__ int64_t garner_value(const Epi<RCAP> &e, const uint32
     } else {
       uint32_t s = __umul24(r[c], e.qinv[c]);
       static_for<c>([&](auto J) { s += __umul24(d[decltype(J)::value], e.u[decltype(J)::value][c]); });
-      d[c] = mod_small(s, e.m[c], e.m24[c]);
+      d[c] = mod_small(s, e.m[c], e.m24[c], e.negm[c]);
     }
     if constexpr (c < 4) {
       x32 += __umul24(d[c], static_cast<uint32_t>(e.prefix[c]));
@@ -305,45 +335,95 @@ __device__ __forceinline__ int64_t garner_value(const Epi<RCAP> &e, const uint32
       x64 += static_cast<uint64_t>(d[c]) * static_cast<uint64_t>(e.prefix[c]);
     }
   });
-  const int64_t p = e.p_act;
-  int64_t y = static_cast<int64_t>(static_cast<uint64_t>(x32) + x64);
-  if (y > (p >> 1)) y -= p;
-  return y;
+  if constexpr (RCAP <= 4) {
+    // x = x32 < P <= 255^4 < 2^32: the correction x - P lies in [-P/2, 0),
+    // so its high word is -1 and its low word is x - P mod 2^32.
+    const uint32_t p32 = static_cast<uint32_t>(e.p_act);
+    const bool neg = x32 > (p32 >> 1);
+    const uint32_t lo = neg ? x32 - p32 : x32;
+    const uint32_t hi = neg ? 0xFFFFFFFFu : 0u;
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+  } else {
+    const int64_t p = e.p_act;
+    int64_t y = static_cast<int64_t>(static_cast<uint64_t>(x32) + x64);
+    if (y > (p >> 1)) y -= p;
+    return y;
+  }
 }
 
-// Writes one output element in the requested type.  The float chain is
+// The output pointers arrive as generic pointers inside the argument block;
+// naming their address space lets the compiler emit global (not flat)
+// memory instructions.
+template <typename T>
+using gptr = __attribute__((address_space(1))) T *;
+template <typename T, typename U>
+__device__ __forceinline__ gptr<T> as_global(U *p) {
+  return (gptr<T>)(p);
+}
+
+// Output element kinds of the epilogue variants: int64, the float chain
+// (float32/float16/bfloat16 chosen per element), or any (generic path).
+enum EpiOut { kOutInt64 = 0, kOutFloat = 1, kOutAny = 2 };
+
+// Writes one output element.  The float chain is
 // ((float)y * a_scale) * w_scale[col] + bias[col], each step rounded to
 // nearest even with no contraction: the op order of rns_linear.py:272-275.
-template <int RCAP>
-__device__ __forceinline__ void store_value(const Epi<RCAP> &e, int64_t y, int row, int col) {
-  const int64_t idx = static_cast<int64_t>(row) * e.out_ld + col;
-  if (e.out_dtype == RNSMX_INT64) {
-    static_cast<int64_t *>(e.out)[idx] = y;
+template <int RCAP, int OUT>
+__device__ __forceinline__ void store_value(const Epi<RCAP> &e, int64_t y, int64_t idx, int col) {
+  if (OUT == kOutInt64 || (OUT == kOutAny && e.out_dtype == RNSMX_INT64)) {
+    as_global<int64_t>(e.out)[idx] = y;
     return;
   }
   float f = __ll2float_rn(y);
   f = __fmul_rn(f, e.a_scale);
-  f = __fmul_rn(f, e.w_scale[col]);
-  if (e.bias_ptr != nullptr) f = __fadd_rn(f, e.bias_ptr[col]);
+  f = __fmul_rn(f, as_global<const float>(e.w_scale)[col]);
+  if (e.bias_ptr != nullptr) f = __fadd_rn(f, as_global<const float>(e.bias_ptr)[col]);
   if (e.out_dtype == RNSMX_FLOAT32) {
-    static_cast<float *>(e.out)[idx] = f;
+    as_global<float>(e.out)[idx] = f;
   } else if (e.out_dtype == RNSMX_FLOAT16) {
-    static_cast<__half *>(e.out)[idx] = __float2half_rn(f);
+    as_global<uint16_t>(e.out)[idx] = __half_as_ushort(__float2half_rn(f));
   } else {
-    static_cast<uint16_t *>(e.out)[idx] = f32_to_bf16_rne(f);
+    as_global<uint16_t>(e.out)[idx] = f32_to_bf16_rne(f);
   }
 }
 
 // Reduction + reconstruction + store of one element from its channel sums.
-template <int RCAP>
+// FAST: every channel active and no byte table (the common case), so the
+// channel loop and Garner run with no per-element branch.
+// idx = row * out_ld + col, the element's offset in the output.
+template <int RCAP, bool FAST, int OUT>
 __device__ __forceinline__ void finish_element(KGemmArgs &g, const Epi<RCAP> &e, int c_act,
-                                               const int32_t (&v)[RCAP], int row, int col) {
+                                               const int32_t (&v)[RCAP], int64_t idx, int col) {
   uint32_t r[RCAP];
-  static_for<RCAP>([&](auto C) {
-    constexpr int c = decltype(C)::value;
-    r[c] = c < c_act ? reduce_acc<RCAP>(g, e, c, v[c]) : 0u;
-  });
-  store_value<RCAP>(e, garner_value<RCAP>(e, r, c_act), row, col);
+  int64_t y;
+  if constexpr (FAST) {
+    static_for<RCAP>([&](auto C) {
+      constexpr int c = decltype(C)::value;
+      r[c] = canon_fast(v[c], FastMod{e.m[c], e.m24[c], e.c16[c], e.bias[c], e.negm[c]});
+    });
+    y = garner_value<RCAP>(e, r, RCAP);
+  } else {
+    static_for<RCAP>([&](auto C) {
+      constexpr int c = decltype(C)::value;
+      r[c] = c < c_act ? reduce_acc<RCAP>(g, e, c, v[c]) : 0u;
+    });
+    y = garner_value<RCAP>(e, r, c_act);
+  }
+  store_value<RCAP, OUT>(e, y, idx, col);
+}
+
+// Calls f(FAST, OUT) with the epilogue variant for this call: a uniform
+// branch taken once per workgroup instead of once per element.
+template <int RCAP, typename F>
+__device__ __forceinline__ void with_epilogue(const Epi<RCAP> &e, int c_act, F &&f) {
+  if (c_act == RCAP && e.lut_channels == 0) {
+    if (e.out_dtype == RNSMX_INT64)
+      f(std::true_type{}, std::integral_constant<int, kOutInt64>{});
+    else
+      f(std::true_type{}, std::integral_constant<int, kOutFloat>{});
+  } else {
+    f(std::false_type{}, std::integral_constant<int, kOutAny>{});
+  }
 }
 
 // Byte offset of channel c's plane with the channel clamped to a valid one:
@@ -434,7 +514,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
   const i32x4 zero = {0, 0, 0, 0};
   i32x4 acc[RCAP][MB][NB];
   static_for<RCAP>([&](auto C) {
-    static_for<MB>([&](auto I) { static_for<NB>([&](auto J) { acc[C][I][J] = zero; }); });
+    static_for<MB>([&](auto I) { static_for<NB>([&](auto J) { acc[C][I][J] = acc_zero(); }); });
   });
 
   i32x4 fa[U][AP][MB], fb[U][RCAP][NB];
@@ -490,20 +570,28 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
     mfma_chunk();
   }
 
+  int m_lim = g.m, n_lim = g.n;
+  pin_sgpr(m_lim);
+  pin_sgpr(n_lim);
   if (ks_n == 1) {
-    static_for<MB>([&](auto I) {
-      constexpr int i = decltype(I)::value;
-      static_for<NB>([&](auto J) {
-        constexpr int j = decltype(J)::value;
-        const int col = n0 + j * 16 + (lane & 15);
-        static_for<4>([&](auto T) {
-          constexpr int t = decltype(T)::value;
-          const int row = m0 + i * 16 + 4 * (lane >> 4) + t;
-          if (row < g.m && col < g.n) {
-            int32_t v[RCAP];
-            static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
-            finish_element<RCAP>(g, e, c_act, v, row, col);
-          }
+    const int64_t idx0 = static_cast<int64_t>(m0 + 4 * (lane >> 4)) * e.out_ld + n0 + (lane & 15);
+    with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) {
+      static_for<MB>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        static_for<NB>([&](auto J) {
+          constexpr int j = decltype(J)::value;
+          const int col = n0 + j * 16 + (lane & 15);
+          static_for<4>([&](auto T) {
+            constexpr int t = decltype(T)::value;
+            const int row = m0 + i * 16 + 4 * (lane >> 4) + t;
+            if (row < m_lim && col < n_lim) {
+              int32_t v[RCAP];
+              static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
+              // the row step is uniform: only idx0 is per lane
+              const int64_t idx = idx0 + (i * 16 + t) * e.out_ld + j * 16;
+              finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(g, e, c_act, v, idx, col);
+            }
+          });
         });
       });
     });
@@ -530,23 +618,26 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
   __syncthreads();
 
   // each thread finishes 4 adjacent columns of one row
-  const int rows_here = min(BM, g.m - m0);
-  for (int x = threadIdx.x * 4; x < rows_here * BN; x += blockDim.x * 4) {
-    const int row = x / BN, col = x % BN;
-    i32x4 sv[RCAP];
-    static_for<RCAP>([&](auto C) {
-      constexpr int c = decltype(C)::value;
-      sv[c] = *reinterpret_cast<const i32x4 *>(&sacc[c * TILE + x]);
-    });
-    static_for<4>([&](auto V) {
-      constexpr int v4 = decltype(V)::value;
-      if (n0 + col + v4 < g.n) {
-        int32_t v[RCAP];
-        static_for<RCAP>([&](auto C) { v[decltype(C)::value] = sv[decltype(C)::value][v4]; });
-        finish_element<RCAP>(g, e, c_act, v, m0 + row, n0 + col + v4);
-      }
-    });
-  }
+  const int rows_here = min(BM, m_lim - m0);
+  with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) {
+    for (int x = threadIdx.x * 4; x < rows_here * BN; x += blockDim.x * 4) {
+      const int row = x / BN, col = x % BN;
+      i32x4 sv[RCAP];
+      static_for<RCAP>([&](auto C) {
+        constexpr int c = decltype(C)::value;
+        sv[c] = *reinterpret_cast<const i32x4 *>(&sacc[c * TILE + x]);
+      });
+      static_for<4>([&](auto V) {
+        constexpr int v4 = decltype(V)::value;
+        if (n0 + col + v4 < n_lim) {
+          int32_t v[RCAP];
+          static_for<RCAP>([&](auto C) { v[decltype(C)::value] = sv[decltype(C)::value][v4]; });
+          finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(
+              g, e, c_act, v, static_cast<int64_t>(m0 + row) * e.out_ld + n0 + col + v4, n0 + col + v4);
+        }
+      });
+    }
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -647,13 +738,16 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
 
   i32x4 acc[RCAP][MB][NB];
   static_for<RCAP>([&](auto C) {
-    static_for<MB>([&](auto I) { static_for<NB>([&](auto J) { acc[C][I][J] = zero; }); });
+    static_for<MB>([&](auto I) { static_for<NB>([&](auto J) { acc[C][I][J] = acc_zero(); }); });
   });
 
   Epi<RCAP> e;
   load_epi<RCAP>(g, e, c_act);
   static_for<P>([&](auto SS) { gload(SS, decltype(SS)::value); });
   pin_epi<RCAP>(e);
+  int m_lim = g.m, n_lim = g.n;
+  pin_sgpr(m_lim);
+  pin_sgpr(n_lim);
   lstore(std::integral_constant<int, 0>{}, 0);
   __syncthreads();
 
@@ -689,19 +783,215 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
   }
 
   // epilogue from registers: lane holds rows 4*(lane>>4)+t of column lane&15
-  static_for<MB>([&](auto I) {
-    constexpr int i = decltype(I)::value;
-    static_for<NB>([&](auto J) {
-      constexpr int j = decltype(J)::value;
-      const int col = n0 + j * 16 + (lane & 15);
-      static_for<4>([&](auto T) {
-        constexpr int t = decltype(T)::value;
-        const int row = m0 + i * 16 + 4 * (lane >> 4) + t;
-        if (row < g.m && col < g.n) {
-          int32_t v[RCAP];
-          static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
-          finish_element<RCAP>(g, e, c_act, v, row, col);
-        }
+  const int64_t idx0 = static_cast<int64_t>(m0 + 4 * (lane >> 4)) * e.out_ld + n0 + (lane & 15);
+  with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) {
+    static_for<MB>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      static_for<NB>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        const int col = n0 + j * 16 + (lane & 15);
+        static_for<4>([&](auto T) {
+          constexpr int t = decltype(T)::value;
+          const int row = m0 + i * 16 + 4 * (lane >> 4) + t;
+          if (row < m_lim && col < n_lim) {
+            int32_t v[RCAP];
+            static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
+            // the row step is uniform: only idx0 is per lane
+            const int64_t idx = idx0 + (i * 16 + t) * e.out_ld + j * 16;
+            finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(g, e, c_act, v, idx, col);
+          }
+        });
+      });
+    });
+  });
+}
+
+// ---------------------------------------------------------------------------
+// Large-M GEMM with LDS staging (raw int8 A, up to 4 channels).  A workgroup
+// of 4 waves owns a 256 x 64 output tile for every channel; per K step of 64
+// bytes it stages 16 A fragments (256 rows) and 4*R B fragments (64
+// columns x R channels), 1 KB each, in fragment order, with direct-to-LDS
+// loads (global_load_lds_dwordx4: no register staging, so S stages of loads
+// are in flight).  Waves split the tile 2 x 2 (128 rows x 32 columns each:
+// 8 x 2 fragments x R channels = 64 MFMAs per K step with R = 4); while a
+// wave runs the MFMAs of step ks it reads the fragments of step ks + 1 from
+// LDS into the other half of a register double buffer.  One barrier per K
+// step.  Rows past M and columns past N are clamped to the last valid ones
+// (their products are dropped); A bytes past K meet zero weight padding.
+// ---------------------------------------------------------------------------
+constexpr int kLdsBM = 256, kLdsBN = 64;
+
+// One direct-to-LDS load: lane l's 16 bytes at gbase + voff land at LDS
+// address sbase + OFF + 16 * l (gbase and sbase wave-uniform).  Written as
+// inline assembly so that the compiler does not track the LDS write: it
+// would otherwise wait for every such load in flight before each LDS read
+// it cannot prove disjoint, draining the pipeline.  The callers order these
+// loads and the reads of the same stage with explicit vmcnt waits and
+// barriers.  M0 holds the LDS address (the compiler keeps no value in M0
+// across this point on gfx9); one wait state separates its write from the
+// load.
+template <int OFF>
+__device__ __forceinline__ void lds_dma16(const int8_t *gbase, uint32_t voff, uint32_t sbase) {
+  asm volatile("s_add_u32 m0, %0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, %3"
+               :
+               : "s"(sbase), "i"(OFF), "v"(voff), "s"(gbase)
+               : "memory", "scc");
+}
+
+// s_waitcnt with only the vector-memory counter limited (to n <= 63).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int RCAP, int S>
+__global__ __launch_bounds__(256) void lds_kernel(const GemmArgs args) {
+  static_assert(RCAP <= 4, "the 256 x 64 x R tile holds R <= 4 channels");
+  static_assert(S == 4, "four stages (an even count keeps the register buffer of a stage fixed)");
+  KGemmArgs &g = kernel_args<GemmArgs>();
+  constexpr int AF = kLdsBM / 16;             // A fragments per stage
+  constexpr int BF = RCAP * (kLdsBN / 16);    // B fragments per stage
+  constexpr int STAGE = (AF + BF) * 1024;
+  constexpr int NL = AF / 4 + BF / 4;         // direct-to-LDS loads per wave per step
+  constexpr int MI = 8, NJ = 2;               // fragments of a wave's 128 x 32 tile
+  __shared__ __attribute__((aligned(1024))) int8_t smem[S * STAGE];
+  __shared__ int64_t red[4];
+  __shared__ int bcast;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int c_act = active_channels<RCAP>(g, red, &bcast);
+  int mt, nt;
+  tile_of(g.tiles_m, g.tiles_n, mt, nt);
+  const int m0 = mt * kLdsBM, n0 = nt * kLdsBN;
+  const int nk = g.kp >> 6;
+
+  // Direct-to-LDS sources.  A fragment wave + 4u: rows m0 + 16 (wave + 4u)
+  // + (lane & 15) (clamped to M - 1), bytes 16 (lane >> 4) of each 64-byte
+  // K step: a per-lane offset from A's base.  B fragment wave + 4u: channel
+  // q / 4, column block q % 4 (clamped to the last), one contiguous 1 KB
+  // block per K step: a per-wave base and offset 16 * lane.  Channels past
+  // c_act read channel 0 (their sums are not used).
+  uint32_t aoff[AF / 4];
+  static_for<AF / 4>([&](auto U) {
+    constexpr int u = decltype(U)::value;
+    const int row = min(m0 + (wave + 4 * u) * 16 + (lane & 15), g.m - 1);
+    aoff[u] = static_cast<uint32_t>(row * g.a_ld + (lane >> 4) * 16);
+  });
+  const int8_t *bbase[BF / 4];
+  const int nblk = (g.n + 15) >> 4;
+  static_for<BF / 4>([&](auto U) {
+    constexpr int u = decltype(U)::value;
+    const int q = wave + 4 * u, c = q / (kLdsBN / 16);
+    const int jb = min((n0 >> 4) + q % (kLdsBN / 16), nblk - 1);
+    bbase[u] = g.b + plane_off(c, c_act, g.b_cs) + static_cast<int64_t>(jb) * g.b_ld;
+  });
+  const uint32_t boff = static_cast<uint32_t>(lane * 16);
+  const int8_t *abase = g.a;
+  const uint32_t sbase = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t *)(smem))) +
+      wave * 1024);
+  // loads of K step ks into stage ST (steps past K, issued near the end,
+  // load the last step again; their stages are never read)
+  auto dma = [&](auto ST, int ks) {
+    constexpr int st = decltype(ST)::value;
+    const int kc = min(ks, nk - 1);
+    static_for<AF / 4>([&](auto U) {
+      constexpr int u = decltype(U)::value;
+      lds_dma16<st * STAGE + 4 * u * 1024>(abase + kc * 64, aoff[u], sbase);
+    });
+    static_for<BF / 4>([&](auto U) {
+      constexpr int u = decltype(U)::value;
+      lds_dma16<st * STAGE + (AF + 4 * u) * 1024>(bbase[u] + static_cast<int64_t>(kc) * 1024, boff, sbase);
+    });
+  };
+
+  // Rolling fragment registers: A fragment i of the next step is read as
+  // soon as the MFMAs of this step are done with it, B fragment (c, j)
+  // during the MFMAs of the last A fragment (eight MFMAs before its first
+  // use in the next step).
+  i32x4 fa[MI], fb[RCAP][NJ];
+  const int8_t *rbase = smem + lane * 16;
+  auto read_a = [&](auto ST, auto I) {
+    constexpr int st = decltype(ST)::value, i = decltype(I)::value;
+    fa[i] = *reinterpret_cast<const i32x4 *>(rbase + st * STAGE + (wm * MI + i) * 1024);
+  };
+  auto read_b = [&](auto ST, auto C, auto J) {
+    constexpr int st = decltype(ST)::value, c = decltype(C)::value, j = decltype(J)::value;
+    fb[c][j] = *reinterpret_cast<const i32x4 *>(rbase + st * STAGE + (AF + c * 4 + wn * NJ + j) * 1024);
+  };
+  i32x4 acc[RCAP][MI][NJ];
+  static_for<RCAP>([&](auto C) {
+    static_for<MI>([&](auto I) { static_for<NJ>([&](auto J) { acc[C][I][J] = acc_zero(); }); });
+  });
+  // one K step k at stage h: wait until step k + 1 landed (own loads, then
+  // everyone's, which also frees the stage of k - 1), refill that stage
+  // with step k + S - 1, then the MFMAs of step k (every channel: no branch
+  // in the loop, inactive channels' sums are dropped by the epilogue) with
+  // the reads of step k + 1's fragments behind them.
+  auto step = [&](auto H, int k) {
+    constexpr int h = decltype(H)::value;
+    constexpr int nxt = (h + 1) % S;
+    wait_vmcnt<(S - 3) * NL>();
+    __builtin_amdgcn_s_barrier();
+    dma(std::integral_constant<int, (h + S - 1) % S>{}, k + S - 1);
+    static_for<MI>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      static_for<RCAP>([&](auto C) {
+        constexpr int c = decltype(C)::value;
+        static_for<NJ>([&](auto J) {
+          constexpr int j = decltype(J)::value;
+          acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[c][j], acc[c][i][j], 0, 0, 0);
+          if constexpr (i == MI - 1) read_b(std::integral_constant<int, nxt>{}, C, J);
+        });
+      });
+      read_a(std::integral_constant<int, nxt>{}, I);
+    });
+  };
+
+  // prologue: steps 0 .. S-2 in flight in stages 0 .. S-2
+  static_for<S - 1>([&](auto T) { dma(T, static_cast<int>(decltype(T)::value)); });
+  Epi<RCAP> e;
+  load_epi<RCAP>(g, e, c_act);
+  pin_epi<RCAP>(e);
+  int m_lim = g.m, n_lim = g.n;
+  pin_sgpr(m_lim);
+  pin_sgpr(n_lim);
+  wait_vmcnt<(S - 2) * NL>();
+  __builtin_amdgcn_s_barrier();
+  static_for<RCAP>([&](auto C) {
+    static_for<NJ>([&](auto J) { read_b(std::integral_constant<int, 0>{}, C, J); });
+  });
+  static_for<MI>([&](auto I) { read_a(std::integral_constant<int, 0>{}, I); });
+
+  // S steps per trip (the stage of each step is a constant); the launcher
+  // guarantees nk % S == 0 and K % 64 == 0
+  for (int ks0 = 0; ks0 < nk; ks0 += S) {
+    static_for<S>([&](auto H) { step(H, ks0 + decltype(H)::value); });
+  }
+  // the loads issued for steps past K land before the workgroup ends
+  wait_vmcnt<0>();
+
+  // epilogue from registers: lane holds rows 4*(lane>>4)+t of column lane&15
+  const int rw0 = m0 + wm * (MI * 16), cw0 = n0 + wn * (NJ * 16);
+  const int64_t idx0 = static_cast<int64_t>(rw0 + 4 * (lane >> 4)) * e.out_ld + cw0 + (lane & 15);
+  with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) {
+    static_for<MI>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      static_for<NJ>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        const int col = cw0 + j * 16 + (lane & 15);
+        static_for<4>([&](auto T) {
+          constexpr int t = decltype(T)::value;
+          const int row = rw0 + i * 16 + 4 * (lane >> 4) + t;
+          if (row < m_lim && col < n_lim) {
+            int32_t v[RCAP];
+            static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
+            const int64_t idx = idx0 + (i * 16 + t) * e.out_ld + j * 16;
+            finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(g, e, c_act, v, idx, col);
+          }
+        });
       });
     });
   });
@@ -733,8 +1023,9 @@ bool launch_stream(GemmArgs g, int mb, int nb, int ks, hipStream_t st) {
 
 // p_req: ring depth (K steps of A and B loads in flight), 0 = the tile's
 // default.  Deeper rings than 3-4 steps cost occupancy (registers) and
-// measured slower on every shape tried.
-template <int RCAP, bool ARAW>
+// measured slower on every shape tried.  NBSEL: the tile widths this
+// instantiation covers (0 all, 1 or 2 only NB = NBSEL).
+template <int RCAP, bool ARAW, int NBSEL>
 bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, hipStream_t st) {
 #define RNSMX_MFMA_P(MB_, NB_, P_)                                                          \
   if (p == P_) {                                                                            \
@@ -742,13 +1033,15 @@ bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, hipStream_t st) {
     return true;                                                                            \
   }
 #define RNSMX_MFMA(MB_, NB_, PDEF, ...)                                    \
-  if (mb == MB_ && nb == NB_) {                                            \
-    g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                         \
-    g.tiles_n = (g.n + 64 * NB_ - 1) / (64 * NB_);                         \
-    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));         \
-    const int p = p_req > 0 ? p_req : PDEF;                                \
-    __VA_ARGS__                                                            \
-    return false;                                                          \
+  if constexpr (NBSEL == 0 || NBSEL == NB_) {                              \
+    if (mb == MB_ && nb == NB_) {                                          \
+      g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                       \
+      g.tiles_n = (g.n + 64 * NB_ - 1) / (64 * NB_);                       \
+      const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));       \
+      const int p = p_req > 0 ? p_req : PDEF;                              \
+      __VA_ARGS__                                                          \
+      return false;                                                        \
+    }                                                                      \
   }
   if constexpr (RCAP <= 4) {
     RNSMX_MFMA(2, 1, 3, RNSMX_MFMA_P(2, 1, 3) RNSMX_MFMA_P(2, 1, 4))
@@ -770,17 +1063,17 @@ bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, hipStream_t st) {
   return false;
 }
 
-template <int RCAP>
-bool launch_gemm_rcap(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st) {
-  switch (c.kind) {
-    case kStream:
-      return araw ? launch_stream<RCAP, true>(g, c.mb, c.nb, c.ks, st)
-                  : launch_stream<RCAP, false>(g, c.mb, c.nb, c.ks, st);
-    case kMfma:
-      return araw ? launch_mfma<RCAP, true>(g, c.mb, c.nb, c.ks, st)
-                  : launch_mfma<RCAP, false>(g, c.mb, c.nb, c.ks, st);
-    default:
-      return false;
+// Body of one part launcher (rnsmx_gemm_part.hip).
+template <int RCAP, int PART>
+bool launch_gemm_part(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st) {
+  if (gemm_part_of(c, araw) != PART) return false;
+  if constexpr (PART == 0) {
+    return araw ? launch_stream<RCAP, true>(g, c.mb, c.nb, c.ks, st)
+                : launch_stream<RCAP, false>(g, c.mb, c.nb, c.ks, st);
+  } else if constexpr (PART == 1 || PART == 2) {
+    return launch_mfma<RCAP, true, PART>(g, c.mb, c.nb, c.ks, st);
+  } else {
+    return launch_mfma<RCAP, false, 0>(g, c.mb, c.nb, c.ks, st);
   }
 }
 

@@ -385,12 +385,13 @@ static int32_t launch_gemm(const GemmArgs &g, bool araw, hipStream_t st) {
     }
   }
   bool ok = false;
-  switch (rcap) {
-    case 3: ok = launch_gemm_r3(g, araw, c, st); break;
-    case 4: ok = launch_gemm_r4(g, araw, c, st); break;
-    case 6: ok = launch_gemm_r6(g, araw, c, st); break;
-    default: ok = launch_gemm_r10(g, araw, c, st); break;
-  }
+  using PartFn = bool (*)(const GemmArgs &, bool, const GemmChoice &, hipStream_t);
+#define RNSMX_PARTS(R) \
+  { RNSMX_GEMM_PART_NAME(R, 0), RNSMX_GEMM_PART_NAME(R, 1), RNSMX_GEMM_PART_NAME(R, 2), RNSMX_GEMM_PART_NAME(R, 3) }
+  static const PartFn parts[4][4] = {RNSMX_PARTS(3), RNSMX_PARTS(4), RNSMX_PARTS(6), RNSMX_PARTS(10)};
+#undef RNSMX_PARTS
+  const int ri = rcap == 3 ? 0 : rcap == 4 ? 1 : rcap == 6 ? 2 : 3;
+  ok = parts[ri][gemm_part_of(c, araw)](g, araw, c, st);
   if (!ok) {
     set_error("no GEMM kernel for kind %d, tile %d x %d, %d channels", c.kind, c.mb, c.nb,
               g.mods.channels);

@@ -1,7 +1,8 @@
 """Builds librnsmx.so (gfx950) in this package directory with hipcc.
 
-Every translation unit is compiled to an object in parallel (the GEMM
-kernels are split by channel capacity for this), then linked."""
+Every translation unit is compiled to an object in parallel, then linked.
+The GEMM kernels are split into parts (rnsmx_gemm_part.hip, built once per
+channel capacity and part) so no single object dominates the build."""
 from __future__ import annotations
 
 import os
@@ -16,8 +17,12 @@ CSRC = os.path.join(ROOT, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 OBJDIR = os.path.join(ROOT, "_build")
 OUT = os.path.join(PKG, "librnsmx.so")
-SOURCES = ("rnsmx_kernels.hip", "rnsmx_gemm_r3.hip", "rnsmx_gemm_r4.hip", "rnsmx_gemm_r6.hip",
-           "rnsmx_gemm_r10.hip", "rnsmx_host.cpp")
+GEMM_CAPACITIES = (3, 4, 6, 10)
+GEMM_PARTS = 4
+# (source, object name, extra flags)
+UNITS = [("rnsmx_kernels.hip", "rnsmx_kernels", []), ("rnsmx_host.cpp", "rnsmx_host", [])] + [
+    ("rnsmx_gemm_part.hip", f"rnsmx_gemm_r{r}_p{p}", [f"-DRNSMX_RCAP={r}", f"-DRNSMX_PART={p}"])
+    for r in GEMM_CAPACITIES for p in range(GEMM_PARTS)]
 ARCH = os.environ.get("RNSMX_OFFLOAD_ARCH", "gfx950")
 NOISE = "packed-fp32-ops"
 
@@ -37,8 +42,8 @@ def flags() -> list[str]:
     ]
 
 
-def compile_command(source: str, obj: str) -> list[str]:
-    return [hipcc(), *flags(), "-c", os.path.join(CSRC, source), "-o", obj]
+def compile_command(source: str, obj: str, extra: list[str]) -> list[str]:
+    return [hipcc(), *flags(), *extra, "-c", os.path.join(CSRC, source), "-o", obj]
 
 
 def link_command(objs: list[str], out: str) -> list[str]:
@@ -54,10 +59,12 @@ def _run(cmd: list[str]) -> tuple[int, str, list[str]]:
 
 def build(verbose: bool = False) -> str:
     os.makedirs(OBJDIR, exist_ok=True)
-    objs = [os.path.join(OBJDIR, os.path.splitext(s)[0] + ".o") for s in SOURCES]
-    jobs = min(len(SOURCES), max(1, min(16, os.cpu_count() or 1)))
+    objs = [os.path.join(OBJDIR, name + ".o") for _, name, _ in UNITS]
+    jobs = min(len(UNITS), max(1, min(16, os.cpu_count() or 1)))
+    # the longest units first, so the tail of the build stays short
+    order = sorted(range(len(UNITS)), key=lambda i: UNITS[i][0] != "rnsmx_gemm_part.hip")
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        results = list(pool.map(_run, [compile_command(s, o) for s, o in zip(SOURCES, objs)]))
+        results = list(pool.map(_run, [compile_command(UNITS[i][0], objs[i], UNITS[i][2]) for i in order]))
     for rc, msgs, cmd in results:
         if rc != 0:
             sys.stderr.write(msgs + "\n")
