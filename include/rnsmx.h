@@ -202,8 +202,10 @@ int32_t rnsmx_matmul_residues_prepared(
  * for tests that run every kernel family on the same inputs.  kind 0
  * restores the automatic choice; kind 1 = stream kernel (tile 16*mb x 16*nb,
  * ks waves splitting K), kind 2 = MFMA kernel (tile 16*mb x 64*nb, ks =
- * K steps of loads in flight, 0 = automatic).  A tile or depth that is not
- * built makes the next GEMM call fail with RNSMX_EINVAL.  Not
+ * K steps of loads in flight, 0 = automatic), kind 3 = LDS-staged kernel
+ * (256 x 64 tiles; int8 activations, 4-channel capacity, K a multiple of
+ * 256; mb, nb, ks ignored).  A kernel that is not built, or does not fit the
+ * call, makes the next GEMM call fail with RNSMX_EINVAL.  Not
  * thread-safe; results never depend on it.  No counterpart in the reference
  * (cuBLAS picks its own kernels there).
  */

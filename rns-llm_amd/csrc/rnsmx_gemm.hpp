@@ -62,7 +62,7 @@ struct GemmArgs {
   rnsmx_moduli_t mods;
 };
 
-enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2 };
+enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kLds = 3 };
 
 // ks: waves splitting K (stream kernel) or ring depth, 0 = automatic (MFMA kernel).
 struct GemmChoice {
@@ -74,18 +74,21 @@ struct GemmChoice {
 // library compiles in parallel:
 //   P0 stream kernels, P1 MFMA kernels with raw int8 A and 64-column tiles,
 //   P2 MFMA kernels with raw int8 A and 128-column tiles, P3 MFMA kernels
-//   with residue-plane A.
+//   with residue-plane A, P4 the LDS-staged kernel.
 // launch_gemm_rR_pP returns false when the part has no kernel for the choice.
+constexpr int kGemmParts = 5;
 inline int gemm_part_of(const GemmChoice &c, bool araw) {
   if (c.kind == kStream) return 0;
+  if (c.kind == kLds) return 4;
   if (!araw) return 3;
   return c.nb == 1 ? 1 : 2;
 }
 #define RNSMX_GEMM_PART_NAME(R, P) launch_gemm_r##R##_p##P
 #define RNSMX_GEMM_PART_DECL(R, P) \
   bool RNSMX_GEMM_PART_NAME(R, P)(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st);
-#define RNSMX_GEMM_PARTS_DECL(R) \
-  RNSMX_GEMM_PART_DECL(R, 0) RNSMX_GEMM_PART_DECL(R, 1) RNSMX_GEMM_PART_DECL(R, 2) RNSMX_GEMM_PART_DECL(R, 3)
+#define RNSMX_GEMM_PARTS_DECL(R)                                                             \
+  RNSMX_GEMM_PART_DECL(R, 0) RNSMX_GEMM_PART_DECL(R, 1) RNSMX_GEMM_PART_DECL(R, 2) \
+  RNSMX_GEMM_PART_DECL(R, 3) RNSMX_GEMM_PART_DECL(R, 4)
 RNSMX_GEMM_PARTS_DECL(3)
 RNSMX_GEMM_PARTS_DECL(4)
 RNSMX_GEMM_PARTS_DECL(6)
@@ -808,18 +811,19 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
 
 // ---------------------------------------------------------------------------
 // Large-M GEMM with LDS staging (raw int8 A, up to 4 channels).  A workgroup
-// of 4 waves owns a 256 x 64 output tile for every channel; per K step of 64
-// bytes it stages 16 A fragments (256 rows) and 4*R B fragments (64
-// columns x R channels), 1 KB each, in fragment order, with direct-to-LDS
-// loads (global_load_lds_dwordx4: no register staging, so S stages of loads
-// are in flight).  Waves split the tile 2 x 2 (128 rows x 32 columns each:
-// 8 x 2 fragments x R channels = 64 MFMAs per K step with R = 4); while a
-// wave runs the MFMAs of step ks it reads the fragments of step ks + 1 from
-// LDS into the other half of a register double buffer.  One barrier per K
-// step.  Rows past M and columns past N are clamped to the last valid ones
-// (their products are dropped); A bytes past K meet zero weight padding.
+// of NW waves owns a 256 x 64 output tile for every channel; per K step of
+// 64 bytes it stages 16 A fragments (256 rows) and 4*R B fragments (64
+// columns x R channels), 1 KB each in MFMA fragment order, with
+// direct-to-LDS loads (global_load_lds_dwordx4: no register staging, so
+// S - 1 steps of loads are in flight).  The waves split the tile
+// (NW / 2) x 2; while a wave runs the MFMAs of step k it reads the
+// fragments of step k + 1 from LDS into the registers the MFMAs have just
+// released.  One barrier per K step.  Rows past M and columns past N are
+// clamped to the last valid ones (their products are dropped).  With
+// NW = 8 the accumulators (128 registers for R = 4) fit two waves per SIMD
+// with VGPR-form MFMAs, which hide each other's LDS latency.
 // ---------------------------------------------------------------------------
-constexpr int kLdsBM = 256, kLdsBN = 64;
+constexpr int kLdsBM = 256, kLdsBN = 64, kLdsStages = 4;
 
 // One direct-to-LDS load: lane l's 16 bytes at gbase + voff land at LDS
 // address sbase + OFF + 16 * l (gbase and sbase wave-uniform).  Written as
@@ -845,45 +849,49 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-template <int RCAP, int S>
-__global__ __launch_bounds__(256) void lds_kernel(const GemmArgs args) {
+template <int RCAP, int NW>
+__global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
   static_assert(RCAP <= 4, "the 256 x 64 x R tile holds R <= 4 channels");
-  static_assert(S == 4, "four stages (an even count keeps the register buffer of a stage fixed)");
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  constexpr int S = kLdsStages;               // even: each step's stage is a constant in a trip
   KGemmArgs &g = kernel_args<GemmArgs>();
   constexpr int AF = kLdsBM / 16;             // A fragments per stage
   constexpr int BF = RCAP * (kLdsBN / 16);    // B fragments per stage
   constexpr int STAGE = (AF + BF) * 1024;
-  constexpr int NL = AF / 4 + BF / 4;         // direct-to-LDS loads per wave per step
-  constexpr int MI = 8, NJ = 2;               // fragments of a wave's 128 x 32 tile
+  constexpr int WM = NW / 2, WN = 2;          // wave grid
+  constexpr int MI = AF / WM, NJ = kLdsBN / 16 / WN;  // fragments of a wave's tile
+  constexpr int AU = AF / NW, BU = BF / NW;   // direct-to-LDS loads per wave per step
+  constexpr int NL = AU + BU;
+  static_assert(AF % NW == 0 && BF % NW == 0, "fragments split evenly over the waves");
   __shared__ __attribute__((aligned(1024))) int8_t smem[S * STAGE];
-  __shared__ int64_t red[4];
+  __shared__ int64_t red[NW];
   __shared__ int bcast;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int c_act = active_channels<RCAP>(g, red, &bcast);
   int mt, nt;
   tile_of(g.tiles_m, g.tiles_n, mt, nt);
   const int m0 = mt * kLdsBM, n0 = nt * kLdsBN;
   const int nk = g.kp >> 6;
 
-  // Direct-to-LDS sources.  A fragment wave + 4u: rows m0 + 16 (wave + 4u)
-  // + (lane & 15) (clamped to M - 1), bytes 16 (lane >> 4) of each 64-byte
-  // K step: a per-lane offset from A's base.  B fragment wave + 4u: channel
-  // q / 4, column block q % 4 (clamped to the last), one contiguous 1 KB
-  // block per K step: a per-wave base and offset 16 * lane.  Channels past
-  // c_act read channel 0 (their sums are not used).
-  uint32_t aoff[AF / 4];
-  static_for<AF / 4>([&](auto U) {
+  // Direct-to-LDS sources.  A fragment f = wave + NW u: rows m0 + 16 f +
+  // (lane & 15) (clamped to M - 1), bytes 16 (lane >> 4) of each 64-byte K
+  // step: a per-lane offset from A's base.  B fragment q = wave + NW u:
+  // channel q / 4, column block q % 4 (clamped to the last), one contiguous
+  // 1 KB block per K step: a per-wave base and offset 16 * lane.  Channels
+  // past c_act read channel 0 (their sums are not used).
+  uint32_t aoff[AU];
+  static_for<AU>([&](auto U) {
     constexpr int u = decltype(U)::value;
-    const int row = min(m0 + (wave + 4 * u) * 16 + (lane & 15), g.m - 1);
+    const int row = min(m0 + (wave + NW * u) * 16 + (lane & 15), g.m - 1);
     aoff[u] = static_cast<uint32_t>(row * g.a_ld + (lane >> 4) * 16);
   });
-  const int8_t *bbase[BF / 4];
+  const int8_t *bbase[BU];
   const int nblk = (g.n + 15) >> 4;
-  static_for<BF / 4>([&](auto U) {
+  static_for<BU>([&](auto U) {
     constexpr int u = decltype(U)::value;
-    const int q = wave + 4 * u, c = q / (kLdsBN / 16);
+    const int q = wave + NW * u, c = q / (kLdsBN / 16);
     const int jb = min((n0 >> 4) + q % (kLdsBN / 16), nblk - 1);
     bbase[u] = g.b + plane_off(c, c_act, g.b_cs) + static_cast<int64_t>(jb) * g.b_ld;
   });
@@ -897,20 +905,19 @@ __global__ __launch_bounds__(256) void lds_kernel(const GemmArgs args) {
   auto dma = [&](auto ST, int ks) {
     constexpr int st = decltype(ST)::value;
     const int kc = min(ks, nk - 1);
-    static_for<AF / 4>([&](auto U) {
+    static_for<AU>([&](auto U) {
       constexpr int u = decltype(U)::value;
-      lds_dma16<st * STAGE + 4 * u * 1024>(abase + kc * 64, aoff[u], sbase);
+      lds_dma16<st * STAGE + NW * u * 1024>(abase + kc * 64, aoff[u], sbase);
     });
-    static_for<BF / 4>([&](auto U) {
+    static_for<BU>([&](auto U) {
       constexpr int u = decltype(U)::value;
-      lds_dma16<st * STAGE + (AF + 4 * u) * 1024>(bbase[u] + static_cast<int64_t>(kc) * 1024, boff, sbase);
+      lds_dma16<st * STAGE + (AF + NW * u) * 1024>(bbase[u] + static_cast<int64_t>(kc) * 1024, boff, sbase);
     });
   };
 
   // Rolling fragment registers: A fragment i of the next step is read as
   // soon as the MFMAs of this step are done with it, B fragment (c, j)
-  // during the MFMAs of the last A fragment (eight MFMAs before its first
-  // use in the next step).
+  // during the MFMAs of the last A fragment.
   i32x4 fa[MI], fb[RCAP][NJ];
   const int8_t *rbase = smem + lane * 16;
   auto read_a = [&](auto ST, auto I) {
@@ -1045,7 +1052,7 @@ bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, hipStream_t st) {
   }
   if constexpr (RCAP <= 4) {
     RNSMX_MFMA(2, 1, 3, RNSMX_MFMA_P(2, 1, 3) RNSMX_MFMA_P(2, 1, 4))
-    RNSMX_MFMA(4, 1, 4, RNSMX_MFMA_P(4, 1, 3) RNSMX_MFMA_P(4, 1, 4))
+    RNSMX_MFMA(4, 1, 3, RNSMX_MFMA_P(4, 1, 3) RNSMX_MFMA_P(4, 1, 4))
     RNSMX_MFMA(2, 2, 3, RNSMX_MFMA_P(2, 2, 3) RNSMX_MFMA_P(2, 2, 4))
     RNSMX_MFMA(4, 2, 3, RNSMX_MFMA_P(4, 2, 3) RNSMX_MFMA_P(4, 2, 4))
     RNSMX_MFMA(8, 2, 3, RNSMX_MFMA_P(8, 2, 3) RNSMX_MFMA_P(8, 2, 4))
@@ -1063,11 +1070,34 @@ bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, hipStream_t st) {
   return false;
 }
 
+// The LDS-staged kernel: raw int8 A, K a multiple of 256 (whole trips of
+// four 64-byte steps), 4-channel capacity (16 B fragments per stage split
+// over 8 waves).
+inline bool lds_kernel_fits(const GemmArgs &g, bool araw, int rcap) {
+  return araw && rcap == 4 && g.a_k == g.kp && g.kp % (64 * kLdsStages) == 0;
+}
+
+template <int RCAP>
+bool launch_lds(GemmArgs g, bool araw, hipStream_t st) {
+  if constexpr (RCAP != 4) {
+    return false;
+  } else {
+    if (!lds_kernel_fits(g, araw, RCAP)) return false;
+    g.tiles_m = (g.m + kLdsBM - 1) / kLdsBM;
+    g.tiles_n = (g.n + kLdsBN - 1) / kLdsBN;
+    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));
+    hipLaunchKernelGGL((lds_kernel<RCAP, 8>), grid, dim3(512), 0, st, g);
+    return true;
+  }
+}
+
 // Body of one part launcher (rnsmx_gemm_part.hip).
 template <int RCAP, int PART>
 bool launch_gemm_part(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st) {
   if (gemm_part_of(c, araw) != PART) return false;
-  if constexpr (PART == 0) {
+  if constexpr (PART == 4) {
+    return launch_lds<RCAP>(g, araw, st);
+  } else if constexpr (PART == 0) {
     return araw ? launch_stream<RCAP, true>(g, c.mb, c.nb, c.ks, st)
                 : launch_stream<RCAP, false>(g, c.mb, c.nb, c.ks, st);
   } else if constexpr (PART == 1 || PART == 2) {

@@ -338,32 +338,36 @@ static int stream_ks_cap(int rcap, int mb, int nb) {
 // Kernel family and tile for an M x N x kp problem, from sweeps on MI355X
 // (K = 768 and 4096, N = 2304 and 12288).  Up to 128 rows the stream kernel
 // (K split over 4 waves) keeps the most weight loads in flight.  Beyond
-// that the MFMA kernel: 128 x 128 tiles once they alone give >= 1024
-// workgroups (their weight reuse then pays for one wave per SIMD), else
-// 64 x 64 tiles (two waves per SIMD) while they give >= 256 workgroups,
-// else 32 x 64 tiles.
+// that the LDS-staged kernel (256 x 64 tiles) wherever it applies and its
+// tiles alone give every CU a workgroup; otherwise the MFMA kernel:
+// 128 x 128 tiles once they give >= 1024 workgroups (their weight reuse then
+// pays for one wave per SIMD), else 64 x 64 tiles (two waves per SIMD)
+// while they give >= 256 workgroups, else 32 x 64 tiles.
 static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   const int rcap = rcap_for(g.mods.channels);
   const int nk = g.kp / 64;
-  auto tiles = [&](int mb, int nbw) {
-    return static_cast<int64_t>((g.m + 16 * mb - 1) / (16 * mb)) * ((g.n + nbw - 1) / nbw);
+  auto tiles = [&](int bm, int bn) {
+    return static_cast<int64_t>((g.m + bm - 1) / bm) * ((g.n + bn - 1) / bn);
   };
   GemmChoice c{};
   if (g.m <= 128) {
     c.kind = kStream;
     c.mb = g.m <= 64 ? 1 : 2;
     c.nb = 1;
-    if (rcap > 4 && c.mb > 2) c.mb = 2;
     const int u = stream_u_of(rcap, araw, c.mb, c.nb);
     c.ks = std::min(stream_ks_cap(rcap, c.mb, c.nb), std::max(1, (nk + u - 1) / u));
     return c;
   }
+  if (lds_kernel_fits(g, araw, rcap) && tiles(kLdsBM, kLdsBN) >= 256) {
+    c.kind = kLds;
+    return c;
+  }
   c.kind = kMfma;
   c.ks = 0;  // the tile's default ring depth
-  if (rcap <= 4 && tiles(8, 128) >= 1024) {
+  if (rcap <= 4 && tiles(128, 128) >= 1024) {
     c.mb = 8;
     c.nb = 2;
-  } else if (tiles(4, 64) >= 256) {
+  } else if (tiles(64, 64) >= 256) {
     c.mb = 4;
     c.nb = 1;
   } else {
@@ -386,9 +390,13 @@ static int32_t launch_gemm(const GemmArgs &g, bool araw, hipStream_t st) {
   }
   bool ok = false;
   using PartFn = bool (*)(const GemmArgs &, bool, const GemmChoice &, hipStream_t);
-#define RNSMX_PARTS(R) \
-  { RNSMX_GEMM_PART_NAME(R, 0), RNSMX_GEMM_PART_NAME(R, 1), RNSMX_GEMM_PART_NAME(R, 2), RNSMX_GEMM_PART_NAME(R, 3) }
-  static const PartFn parts[4][4] = {RNSMX_PARTS(3), RNSMX_PARTS(4), RNSMX_PARTS(6), RNSMX_PARTS(10)};
+#define RNSMX_PARTS(R)                                                                      \
+  {                                                                                         \
+    RNSMX_GEMM_PART_NAME(R, 0), RNSMX_GEMM_PART_NAME(R, 1), RNSMX_GEMM_PART_NAME(R, 2),     \
+        RNSMX_GEMM_PART_NAME(R, 3), RNSMX_GEMM_PART_NAME(R, 4)                              \
+  }
+  static const PartFn parts[4][kGemmParts] = {RNSMX_PARTS(3), RNSMX_PARTS(4), RNSMX_PARTS(6),
+                                              RNSMX_PARTS(10)};
 #undef RNSMX_PARTS
   const int ri = rcap == 3 ? 0 : rcap == 4 ? 1 : rcap == 6 ? 2 : 3;
   ok = parts[ri][gemm_part_of(c, araw)](g, araw, c, st);
@@ -397,7 +405,7 @@ static int32_t launch_gemm(const GemmArgs &g, bool araw, hipStream_t st) {
               g.mods.channels);
     return RNSMX_EINVAL;
   }
-  return check_launch(c.kind == kStream ? "gemm_stream" : "gemm_mfma");
+  return check_launch(c.kind == kStream ? "gemm_stream" : c.kind == kLds ? "gemm_lds" : "gemm_mfma");
 }
 
 static int32_t launch_encode_rows(int32_t dtype, const EncodeArgs &e, hipStream_t st) {
@@ -739,8 +747,9 @@ int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb, int32_t ks
     g_override = GemmChoice{kAuto, 0, 0, 0};
     return RNSMX_OK;
   }
-  if (kind != kStream && kind != kMfma) return fail(RNSMX_EINVAL, "kind must be 0 (auto), 1 (stream) or 2 (mfma)");
-  if (mb < 1 || nb < 1) return fail(RNSMX_EINVAL, "tile blocks must be positive");
+  if (kind != kStream && kind != kMfma && kind != kLds)
+    return fail(RNSMX_EINVAL, "kind must be 0 (auto), 1 (stream), 2 (mfma) or 3 (lds)");
+  if (kind != kLds && (mb < 1 || nb < 1)) return fail(RNSMX_EINVAL, "tile blocks must be positive");
   g_override = GemmChoice{kind, mb, nb, ks};
   return RNSMX_OK;
 }

@@ -113,14 +113,34 @@ def test_mfma_kernel_instances(backend, override, r, mb, nb, p):
     run_case(backend, mods, 40, 150, 70, dtype=torch.int16, seed=r + 1)
 
 
-@pytest.mark.parametrize("kind,mb,nb,ks", [(1, 1, 1, 4), (1, 1, 2, 2), (1, 2, 1, 1), (2, 8, 2, 0),
-                                           (2, 2, 1, 0)])
-def test_kernel_adaptive_prefix(backend, override, kind, mb, nb, ks):
+@pytest.mark.parametrize("m,k,n", [(256 * 2 + 37, 256, 64 * 3 + 5), (300, 512, 100), (17, 1024, 64),
+                                   (256, 768, 2304)])
+def test_lds_kernel(backend, override, m, k, n):
+    # 256 x 64 tiles, four stages of direct-to-LDS loads: ragged M and N,
+    # one and several trips round the stages
+    override(3)
+    run_case(backend, DENSE4, m, k, n, seed=m + k)
+
+
+def test_lds_kernel_rejects_unfit_shapes(backend, override):
+    override(3)
+    prepared = backend.prepare_weight(torch.ones((320, 16), dtype=torch.int8, device=DEV), DENSE4)
+    with pytest.raises(ValueError, match="no GEMM kernel"):  # K not a multiple of 256
+        backend.matmul_prepared_fused(torch.ones((4, 320), dtype=torch.int8, device=DEV), prepared)
+    prepared = backend.prepare_weight(torch.ones((256, 16), dtype=torch.int8, device=DEV), SETS[3])
+    with pytest.raises(ValueError, match="no GEMM kernel"):  # 3-channel capacity
+        backend.matmul_prepared_fused(torch.ones((4, 256), dtype=torch.int8, device=DEV), prepared)
+
+
+@pytest.mark.parametrize("kind,mb,nb,ks,k", [(1, 1, 1, 4, 320), (1, 1, 2, 2, 320), (1, 2, 1, 1, 320),
+                                             (2, 8, 2, 0, 320), (2, 2, 1, 0, 320), (3, 0, 0, 0, 512)])
+def test_kernel_adaptive_prefix(backend, override, kind, mb, nb, ks, k):
     override(kind, mb, nb, ks)
-    run_case(backend, DENSE4, 50, 320, 90, seed=5, adaptive=True)
+    run_case(backend, DENSE4, 50, k, 90, seed=5, adaptive=True)
 
 
-@pytest.mark.parametrize("kind,mb,nb,ks", [(1, 1, 2, 2), (1, 4, 1, 4), (1, 2, 1, 1), (2, 8, 2, 0), (2, 2, 1, 0)])
+@pytest.mark.parametrize("kind,mb,nb,ks", [(1, 1, 2, 2), (1, 4, 1, 4), (1, 2, 1, 1), (2, 8, 2, 0), (2, 2, 1, 0),
+                                           (3, 0, 0, 0)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_kernel_float_epilogue(backend, override, kind, mb, nb, ks, out_dtype):
     override(kind, mb, nb, ks)
