@@ -24,8 +24,11 @@ output) per launch / that duration.  traffic: HBM bytes per launch from two
 rocprofv3 --pmc child runs (FETCH_SIZE, WRITE_SIZE), each scaled by what
 the counter reads for a 64 MiB device copy in the same run (null when
 rocprofv3 is unavailable or fails).  cpu_baseline = the NumPy restatement
-of the reference CPU path on a bounded sample, 1 core.  Extra rows cover
-the other C2 token counts, C3 decode and C5 (OPT-6.7B QKV) shapes.
+of the reference CPU path on a bounded sample, 1 core; cpu_baseline_all_cores
+= the OpenMP C restatement on the full headline shape.  Extra rows cover the
+other C2 token counts, C3 decode, C5 (OPT-6.7B QKV) shapes and C4 (a
+random-init OPT-125m forward with 4 RNS attention blocks: time, logit error,
+call counts).
 """
 from __future__ import annotations
 
@@ -51,7 +54,7 @@ DENSE4 = (255, 253, 251, 247)
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
 CALIB_BYTES = 64 << 20   # device copy used to scale the PMC byte counters
-GEMM_KERNELS = ("mfma_kernel", "stream_kernel")
+GEMM_KERNELS = ("mfma_kernel", "stream_kernel", "lds_kernel")
 METRIC = "effective int8 TOPS + us/call, fused-QKV RNS GEMM+reconstruct, bit-exact"
 
 
@@ -295,6 +298,90 @@ def cpu_baseline(seconds):
     }
 
 
+def cpu_baseline_all_cores(seconds):
+    """The OpenMP C restatement (oracle/rns_oracle.c) of the same centered
+    pipeline on the full headline shape, all host threads."""
+    import numpy as np
+
+    from oracle import c_oracle
+
+    rng = np.random.default_rng(6)
+    m, k, n = 256, 768, 2304
+    a = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    c_oracle.rns_matmul_centered(a, b, DENSE4)  # warmup (and build check)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        c_oracle.rns_matmul_centered(a, b, DENSE4)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    return {
+        "value": 2 * len(DENSE4) * m * k * n / t / 1e12, "unit": "effective int8 TOPS",
+        "cores": threads, "kind": "port",
+        "sample": (f"C2 M={m}, K={k}, N={n}, R=4: C restatement with OpenMP (oracle/rns_oracle.c), "
+                   f"median of {len(times)} calls, {t * 1e3:.1f} ms/call"),
+    }
+
+
+def measure_c4(backend, device, steps, warmup):
+    """random-init OPT-125m (fp16), batch 8 x 512 tokens,
+    fused RNS QKV + RNS out_proj in the first 4 attention blocks; one step =
+    one forward.  Reports the logit error against the fp16 model and the
+    backend call counts of one forward."""
+    import torch
+    import transformers
+
+    from rns_llm_amd import replace_opt_attention_blocks
+
+    config = transformers.OPTConfig()
+    config._attn_implementation = "sdpa"
+    torch.manual_seed(41)
+    model = transformers.OPTForCausalLM(config).to(device=device, dtype=torch.float16).eval()
+    gen = torch.Generator().manual_seed(42)
+    ids = torch.randint(0, config.vocab_size, (8, 512), generator=gen).to(device)
+
+    def timed():
+        with torch.no_grad():
+            for _ in range(warmup):
+                model(ids)
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(steps):
+                model(ids)
+            end.record()
+            torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
+
+    with torch.no_grad():
+        ref = model(ids).logits.float()
+    ms_fp16 = timed()
+    replaced, coordinators = replace_opt_attention_blocks(model, backend=backend, blocks=4)
+    with torch.no_grad():
+        model(ids)  # weight preparation
+        backend.reset_stats()
+        out = model(ids).logits.float()
+    stats = backend.stats_snapshot()
+    err = (out - ref).abs()
+    ms_rns = timed()
+    row = {
+        "config": "C4 OPT-125m random-init fp16, 8 x 512 tokens, 4 blocks fused RNS QKV + out_proj",
+        "ms_per_forward_rns": ms_rns, "ms_per_forward_fp16": ms_fp16,
+        "logit_max_err": err.max().item(), "logit_mean_err": err.mean().item(),
+        "logit_mean_abs": ref.abs().mean().item(),
+        "calls_per_forward": {k: v for k, v in stats.items() if k in (
+            "fused_gemm_calls", "encode_centered_calls", "fused_gemm_channels_4")},
+        "qkv_compute_count_per_block": [c.projection.compute_count for c in coordinators],
+        "replaced": replaced,
+    }
+    del model, ref, out
+    torch.cuda.empty_cache()
+    return row
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -347,8 +434,17 @@ def main():
             log(f"bench: {name} M={m}: {rows[-1]['us_per_call_graph']:.2f} us/step, "
                 f"{rows[-1]['eff_tops']:.1f} eff TOPS, {rows[-1]['gbs_alg']:.0f} GB/s alg, "
                 f"{rows[-1]['bound']} roofline {rows[-1]['roofline_frac']:.3f}")
+        try:
+            c4 = measure_c4(backend, device, steps=5, warmup=2)
+            rows.append(c4)
+            log(f"bench: C4 forward {c4['ms_per_forward_rns']:.2f} ms (fp16 {c4['ms_per_forward_fp16']:.2f} ms), "
+                f"logit max/mean err {c4['logit_max_err']:.4g}/{c4['logit_mean_err']:.4g}, "
+                f"calls {c4['calls_per_forward']}")
+        except ImportError as exc:
+            log(f"bench: C4 skipped ({exc})")
 
     cpu = cpu_baseline(args.cpu_seconds)
+    cpu_all = cpu_baseline_all_cores(min(args.cpu_seconds, 5.0))
     achieved = head["bytes_alg"] / (head["ms_per_step"] * 1e-3) / 1e9
     roofline = {
         "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -381,6 +477,7 @@ def main():
                    "m": args.m, "k": 768, "n": 2304, "channels": 4},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_baseline_all_cores": cpu_all,
         "rows": rows,
     }
     print(json.dumps(line), flush=True)

@@ -368,19 +368,45 @@ __device__ __forceinline__ gptr<T> as_global(U *p) {
 // (float32/float16/bfloat16 chosen per element), or any (generic path).
 enum EpiOut { kOutInt64 = 0, kOutFloat = 1, kOutAny = 2 };
 
+// Per-column factors of the float epilogue (w_scale[col], bias[col]), read
+// once per column before any output store: on this hardware loads and
+// stores share one completion counter, so a load issued after stores would
+// also wait for those stores.
+struct ColScale {
+  float w, b;
+};
+
+template <int RCAP>
+__device__ __forceinline__ ColScale col_scale(const Epi<RCAP> &e, int col, int n_lim) {
+  ColScale cs{0.0f, 0.0f};
+  if (e.out_dtype != RNSMX_INT64) {
+    const int c = min(col, n_lim - 1);
+    cs.w = as_global<const float>(e.w_scale)[c];
+    if (e.bias_ptr != nullptr) cs.b = as_global<const float>(e.bias_ptr)[c];
+  }
+  return cs;
+}
+
 // Writes one output element.  The float chain is
 // ((float)y * a_scale) * w_scale[col] + bias[col], each step rounded to
 // nearest even with no contraction: the op order of rns_linear.py:272-275.
+// The operators are written here, under the pragma, on purpose: HIP's
+// __fmul_rn / __fadd_rn are plain operators compiled with contraction on
+// in their own header, and after inlining the multiply and the add would
+// fuse into an FMA (one rounding instead of two).
 template <int RCAP, int OUT>
-__device__ __forceinline__ void store_value(const Epi<RCAP> &e, int64_t y, int64_t idx, int col) {
+__device__ __forceinline__ void store_value(const Epi<RCAP> &e, int64_t y, int64_t idx, ColScale cs) {
+#pragma clang fp contract(off)
   if (OUT == kOutInt64 || (OUT == kOutAny && e.out_dtype == RNSMX_INT64)) {
     as_global<int64_t>(e.out)[idx] = y;
     return;
   }
-  float f = __ll2float_rn(y);
-  f = __fmul_rn(f, e.a_scale);
-  f = __fmul_rn(f, as_global<const float>(e.w_scale)[col]);
-  if (e.bias_ptr != nullptr) f = __fadd_rn(f, as_global<const float>(e.bias_ptr)[col]);
+  // with up to 4 channels |y| <= P/2 < 2^31: the 32-bit conversion rounds
+  // the same integer the same way, in one instruction
+  float f = RCAP <= 4 ? static_cast<float>(static_cast<int32_t>(y)) : __ll2float_rn(y);
+  f = f * e.a_scale;
+  f = f * cs.w;
+  if (e.bias_ptr != nullptr) f = f + cs.b;
   if (e.out_dtype == RNSMX_FLOAT32) {
     as_global<float>(e.out)[idx] = f;
   } else if (e.out_dtype == RNSMX_FLOAT16) {
@@ -393,10 +419,11 @@ __device__ __forceinline__ void store_value(const Epi<RCAP> &e, int64_t y, int64
 // Reduction + reconstruction + store of one element from its channel sums.
 // FAST: every channel active and no byte table (the common case), so the
 // channel loop and Garner run with no per-element branch.
-// idx = row * out_ld + col, the element's offset in the output.
+// idx = row * out_ld + col, the element's offset in the output; cs the
+// column's float-epilogue factors (col_scale).
 template <int RCAP, bool FAST, int OUT>
 __device__ __forceinline__ void finish_element(KGemmArgs &g, const Epi<RCAP> &e, int c_act,
-                                               const int32_t (&v)[RCAP], int64_t idx, int col) {
+                                               const int32_t (&v)[RCAP], int64_t idx, ColScale cs) {
   uint32_t r[RCAP];
   int64_t y;
   if constexpr (FAST) {
@@ -412,7 +439,7 @@ __device__ __forceinline__ void finish_element(KGemmArgs &g, const Epi<RCAP> &e,
     });
     y = garner_value<RCAP>(e, r, c_act);
   }
-  store_value<RCAP, OUT>(e, y, idx, col);
+  store_value<RCAP, OUT>(e, y, idx, cs);
 }
 
 // Calls f(FAST, OUT) with the epilogue variant for this call: a uniform
@@ -567,17 +594,30 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
   Epi<RCAP> e;
   load_epi<RCAP>(g, e, c_act);
   pin_epi<RCAP>(e);
+  int m_lim = g.m, n_lim = g.n;
+  pin_sgpr(m_lim);
+  pin_sgpr(n_lim);
+  // float-epilogue column factors, read now so their latency hides behind
+  // the K loop: columns n0 + 16 j + (lane & 15) for the register epilogue
+  // (ks_n == 1, j < NB <= 4), n0 + (4 tid) % BN + v for the LDS one (the
+  // stride 4 * blockDim.x is a multiple of BN, so each thread keeps its
+  // columns every trip)
+  ColScale cs4[4];
+  static_for<4>([&](auto V) {
+    constexpr int v = decltype(V)::value;
+    const int col = ks_n == 1 ? n0 + (v < NB ? v : 0) * 16 + (lane & 15) : n0 + (threadIdx.x * 4) % BN + v;
+    cs4[v] = col_scale<RCAP>(e, col, n_lim);
+  });
   if (wave * U < nk) mfma_chunk();
   for (int q = wave * U + ks_n * U; q < nk; q += ks_n * U) {
     load_chunk(q);
     mfma_chunk();
   }
 
-  int m_lim = g.m, n_lim = g.n;
-  pin_sgpr(m_lim);
-  pin_sgpr(n_lim);
   if (ks_n == 1) {
     const int64_t idx0 = static_cast<int64_t>(m0 + 4 * (lane >> 4)) * e.out_ld + n0 + (lane & 15);
+    ColScale cs[NB];
+    static_for<NB>([&](auto J) { cs[J] = cs4[decltype(J)::value]; });
     with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) {
       static_for<MB>([&](auto I) {
         constexpr int i = decltype(I)::value;
@@ -592,7 +632,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
               static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
               // the row step is uniform: only idx0 is per lane
               const int64_t idx = idx0 + (i * 16 + t) * e.out_ld + j * 16;
-              finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(g, e, c_act, v, idx, col);
+              finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(g, e, c_act, v, idx, cs[j]);
             }
           });
         });
@@ -620,8 +660,10 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
   });
   __syncthreads();
 
-  // each thread finishes 4 adjacent columns of one row
+  // each thread finishes 4 adjacent columns of one row; the stride
+  // 4 * blockDim.x is a multiple of BN, so the columns are the same every trip
   const int rows_here = min(BM, m_lim - m0);
+  const ColScale(&cs)[4] = cs4;
   with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) {
     for (int x = threadIdx.x * 4; x < rows_here * BN; x += blockDim.x * 4) {
       const int row = x / BN, col = x % BN;
@@ -636,7 +678,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
           int32_t v[RCAP];
           static_for<RCAP>([&](auto C) { v[decltype(C)::value] = sv[decltype(C)::value][v4]; });
           finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(
-              g, e, c_act, v, static_cast<int64_t>(m0 + row) * e.out_ld + n0 + col + v4, n0 + col + v4);
+              g, e, c_act, v, static_cast<int64_t>(m0 + row) * e.out_ld + n0 + col + v4, cs[v4]);
         }
       });
     }
@@ -751,6 +793,9 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
   int m_lim = g.m, n_lim = g.n;
   pin_sgpr(m_lim);
   pin_sgpr(n_lim);
+  // float-epilogue column factors, read now so their latency hides behind the K loop
+  ColScale cs[NB];
+  static_for<NB>([&](auto J) { cs[J] = col_scale<RCAP>(e, n0 + decltype(J)::value * 16 + (lane & 15), n_lim); });
   lstore(std::integral_constant<int, 0>{}, 0);
   __syncthreads();
 
@@ -801,7 +846,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
             static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
             // the row step is uniform: only idx0 is per lane
             const int64_t idx = idx0 + (i * 16 + t) * e.out_ld + j * 16;
-            finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(g, e, c_act, v, idx, col);
+            finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(g, e, c_act, v, idx, cs[j]);
           }
         });
       });
@@ -965,6 +1010,11 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
   int m_lim = g.m, n_lim = g.n;
   pin_sgpr(m_lim);
   pin_sgpr(n_lim);
+  // float-epilogue column factors (loads complete in order, so the waits
+  // below cover them too)
+  const int rw0 = m0 + wm * (MI * 16), cw0 = n0 + wn * (NJ * 16);
+  ColScale cs[NJ];
+  static_for<NJ>([&](auto J) { cs[J] = col_scale<RCAP>(e, cw0 + decltype(J)::value * 16 + (lane & 15), n_lim); });
   wait_vmcnt<(S - 2) * NL>();
   __builtin_amdgcn_s_barrier();
   static_for<RCAP>([&](auto C) {
@@ -981,7 +1031,6 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
   wait_vmcnt<0>();
 
   // epilogue from registers: lane holds rows 4*(lane>>4)+t of column lane&15
-  const int rw0 = m0 + wm * (MI * 16), cw0 = n0 + wn * (NJ * 16);
   const int64_t idx0 = static_cast<int64_t>(rw0 + 4 * (lane >> 4)) * e.out_ld + cw0 + (lane & 15);
   with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) {
     static_for<MI>([&](auto I) {
@@ -996,7 +1045,7 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
             int32_t v[RCAP];
             static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
             const int64_t idx = idx0 + (i * 16 + t) * e.out_ld + j * 16;
-            finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(g, e, c_act, v, idx, col);
+            finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(g, e, c_act, v, idx, cs[j]);
           }
         });
       });

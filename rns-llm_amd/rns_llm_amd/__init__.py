@@ -16,6 +16,7 @@ from .layers import (
     RNSLinear,
     RNSQKVProjection,
     install_opt_qkv_fusion,
+    replace_opt_attention_blocks,
 )
 from .moduli import (
     DENSE_COPRIME_MODULI,
@@ -32,6 +33,7 @@ __all__ = [
     "AdaptiveMetadata", "HipRNSBackend", "PreparedAdaptiveRNSWeight", "PreparedRNSWeight",
     "RNSRequestBatchWorkspace", "RNSWorkspace", "hip_extension_available", "CachedRNSQKV",
     "InstalledQKVFusion", "RNSLinear", "RNSQKVProjection", "install_opt_qkv_fusion",
+    "replace_opt_attention_blocks",
     "DENSE_COPRIME_MODULI", "LARGE_PRIME_MODULI", "SMALL_PRIME_MODULI", "choose_moduli_for_dot",
     "minimal_prefix_channels", "safe_l1_dot_bound", "signed_capacity", "validate_moduli",
 ]

@@ -1,5 +1,6 @@
 from .rns_linear import RNSLinear
-from .rns_qkv import CachedRNSQKV, InstalledQKVFusion, RNSQKVProjection, install_opt_qkv_fusion
+from .rns_qkv import (CachedRNSQKV, InstalledQKVFusion, RNSQKVProjection, install_opt_qkv_fusion,
+                      replace_opt_attention_blocks)
 
 __all__ = ["RNSLinear", "RNSQKVProjection", "CachedRNSQKV", "InstalledQKVFusion",
-           "install_opt_qkv_fusion"]
+           "install_opt_qkv_fusion", "replace_opt_attention_blocks"]

@@ -155,3 +155,34 @@ def install_opt_qkv_fusion(attention: nn.Module, *, backend, quant_bits: int = 8
     attention.rns_qkv = coordinator
     attention.q_proj, attention.k_proj, attention.v_proj = coordinator.slices()
     return coordinator
+
+
+def replace_opt_attention_blocks(model: nn.Module, *, backend, blocks: int, quant_bits: int = 8,
+                                 include_out_proj: bool = True, adaptive_channels: bool = False,
+                                 fused_epilogue: bool = True):
+    """Fused RNS QKV (and, optionally, an RNS ``out_proj``) in the first
+    ``blocks`` attention modules of an OPT-style model, in module order
+    (``scripts/evaluate_ppl.py:53-94``): every module whose ``q_proj``,
+    ``k_proj`` and ``v_proj`` are ``nn.Linear`` is a candidate.  Returns the
+    replaced module names and the QKV coordinators."""
+    if blocks < 0:
+        raise ValueError("blocks must be non-negative")
+    candidates = [(name, module) for name, module in model.named_modules()
+                  if all(isinstance(getattr(module, attr, None), nn.Linear)
+                         for attr in ("q_proj", "k_proj", "v_proj"))]
+    replaced: list[str] = []
+    coordinators: list[CachedRNSQKV] = []
+    for name, attention in candidates[:blocks]:
+        coordinators.append(install_opt_qkv_fusion(
+            attention, backend=backend, quant_bits=quant_bits, moduli_strategy="dense_coprime",
+            lut_channels=2, adaptive_channels=adaptive_channels, fused_epilogue=fused_epilogue))
+        replaced.append(f"{name}.qkv_fused")
+        if include_out_proj:
+            if not isinstance(getattr(attention, "out_proj", None), nn.Linear):
+                raise TypeError(f"{name}.out_proj is not nn.Linear")
+            attention.out_proj = RNSLinear.from_linear(
+                attention.out_proj, backend=backend, mode="rns", quant_bits=quant_bits, fused=True,
+                lut_channels=2, moduli_strategy="dense_coprime",
+                adaptive_channels=adaptive_channels, fused_epilogue=fused_epilogue).eval()
+            replaced.append(f"{name}.out_proj")
+    return replaced, coordinators
