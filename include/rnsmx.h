@@ -109,9 +109,12 @@ int64_t rnsmx_fused_workspace_bytes(int64_t m, int64_t k, int64_t n,
 /*
  * Drop-in fused op: a_dev [R][M][K] and b_dev [R][K][N] centered int8
  * residue planes (contiguous, the reference layout) -> out_dev [M][N] int64.
- * Per-channel int8 GEMM on MFMA, modular reduction (Barrett, or the byte
- * LUT `lut_dev` [R][4][256] for channels < lut_channels), Garner mixed
- * radix and signed correction, all in one GEMM epilogue.  No K%4 / N%4
+ * Per-channel int8 GEMM on MFMA, modular reduction, Garner mixed radix and
+ * signed correction, all in one GEMM epilogue.  `lut_dev` / `lut_channels`
+ * are the reference's byte-table arguments: validated as the reference
+ * does (lut_channels in {0, 1, 2}, <= R, table present when > 0); the
+ * residue is unique, so results do not depend on them and every channel
+ * uses the 24-bit arithmetic reduction.  No K%4 / N%4
  * restriction.  `workspace_dev` holds the repacked operands (B in the
  * fragment-major order of rnsmx_prepare_weight).
  * Replaces _C.matmul_centered_fused_out (csrc/rns_cuda.cu:887-980: cuBLAS

@@ -85,21 +85,6 @@ __device__ __forceinline__ uint32_t canon_i32(int32_t v, uint32_t m, uint32_t ma
   return r >= c31 ? r - c31 : r + m - c31;
 }
 
-// Same residue through the compact byte table of one channel (int16 [4][256],
-// entry [p][b] = b * 256^p mod m), applied to the biased value.
-__device__ __forceinline__ uint32_t canon_i32_lut(int32_t v, const int16_t *__restrict__ t,
-                                                  uint32_t m, uint32_t c31) {
-  const uint32_t u = static_cast<uint32_t>(v) ^ 0x80000000u;
-  uint32_t s = static_cast<uint32_t>(t[u & 255u]) +
-               static_cast<uint32_t>(t[256 + ((u >> 8) & 255u)]) +
-               static_cast<uint32_t>(t[512 + ((u >> 16) & 255u)]) +
-               static_cast<uint32_t>(t[768 + (u >> 24)]);
-  // s < 4m
-  if (s >= 2 * m) s -= 2 * m;
-  if (s >= m) s -= m;
-  return s >= c31 ? s - c31 : s + m - c31;
-}
-
 // Centered residue in [-floor(m/2), floor(m/2)] of a signed 32-bit value.
 __device__ __forceinline__ int32_t centered_i32(int32_t v, uint32_t m, uint32_t magic,
                                                 uint32_t c31) {

@@ -116,21 +116,6 @@ __device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
   return v;
 }
 
-// Sum over the 64 lanes of a wave, returned as a wave-uniform value.  DPP
-// row shifts build prefix sums inside each 16-lane row (lane 15 then holds
-// its row's total), two row broadcasts fold the rows into lane 63, and
-// readlane moves that total to a scalar register: 6 DPP adds instead of 6
-// LDS-latency shuffles.
-__device__ __forceinline__ int32_t wave_total(int32_t v) {
-  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);  // row_shr:1
-  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);  // row_shr:2
-  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);  // row_shr:4
-  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);  // row_shr:8
-  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, true);  // row_bcast:15 -> rows 1, 3
-  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, true);  // row_bcast:31 -> rows 2, 3
-  return __builtin_amdgcn_readlane(v, 63);
-}
-
 __device__ __forceinline__ i32x4 load16(const int8_t *p) { return *reinterpret_cast<const i32x4 *>(p); }
 
 // Initial value of one MFMA accumulator: zero, hidden from the compiler.
@@ -214,7 +199,7 @@ struct Epi {
   uint32_t u[RCAP][RCAP];  // u[j][c], j < c
   int64_t prefix[RCAP + 1];
   int64_t p_act;  // prefix[c_act], the modulus of the signed correction
-  int32_t lut_channels, out_dtype;
+  int32_t out_dtype;
   int64_t out_ld;
   void *out;
   const float *w_scale;
@@ -246,7 +231,6 @@ __device__ __forceinline__ void fill_moduli(Epi<RCAP> &e, const Mods &mods, int 
 template <int RCAP>
 __device__ __forceinline__ void load_epi(KGemmArgs &g, Epi<RCAP> &e, int c_act) {
   fill_moduli<RCAP>(e, g.mods, c_act);
-  e.lut_channels = g.lut_channels;
   e.out_dtype = g.out_dtype;
   e.out_ld = g.out_ld;
   e.out = g.out;
@@ -288,19 +272,19 @@ __device__ __forceinline__ void pin_epi(Epi<RCAP> &e) {
   pin_sgpr(e.p_act);
   pin_sgpr(e.out_ld);
   pin_sgpr(e.out);
-  pin_sgpr(e.lut_channels);
   pin_sgpr(e.out_dtype);
   pin_sgpr(e.a_scale);
   pin_sgpr(e.w_scale);
   pin_sgpr(e.bias_ptr);
 }
 
-// Canonical residue of one int32 accumulator of channel c: the byte table
-// for the first lut_channels channels (reference semantics, the same
-// residue), the 24-bit reduction otherwise.
+// Canonical residue of one int32 accumulator of channel c.  The reference
+// reduces its first lut_channels channels through a byte table
+// (csrc/rns_cuda.cu:69-96) and the rest with Barrett; the residue is unique,
+// so every channel here takes the 24-bit arithmetic reduction, which needs
+// no table loads (those would queue behind the output stores).
 template <int RCAP>
-__device__ __forceinline__ uint32_t reduce_acc(KGemmArgs &g, const Epi<RCAP> &e, int c, int32_t v) {
-  if (c < e.lut_channels) return canon_i32_lut(v, g.lut + c * 1024, e.m[c], g.mods.c31[c]);
+__device__ __forceinline__ uint32_t reduce_acc(const Epi<RCAP> &e, int c, int32_t v) {
   return canon_fast(v, FastMod{e.m[c], e.m24[c], e.c16[c], e.bias[c], e.negm[c]});
 }
 
@@ -417,8 +401,8 @@ __device__ __forceinline__ void store_value(const Epi<RCAP> &e, int64_t y, int64
 }
 
 // Reduction + reconstruction + store of one element from its channel sums.
-// FAST: every channel active and no byte table (the common case), so the
-// channel loop and Garner run with no per-element branch.
+// FAST: every channel active (the common case), so the channel loop and
+// Garner run with no per-element branch.
 // idx = row * out_ld + col, the element's offset in the output; cs the
 // column's float-epilogue factors (col_scale).
 template <int RCAP, bool FAST, int OUT>
@@ -427,15 +411,12 @@ __device__ __forceinline__ void finish_element(KGemmArgs &g, const Epi<RCAP> &e,
   uint32_t r[RCAP];
   int64_t y;
   if constexpr (FAST) {
-    static_for<RCAP>([&](auto C) {
-      constexpr int c = decltype(C)::value;
-      r[c] = canon_fast(v[c], FastMod{e.m[c], e.m24[c], e.c16[c], e.bias[c], e.negm[c]});
-    });
+    static_for<RCAP>([&](auto C) { r[decltype(C)::value] = reduce_acc<RCAP>(e, decltype(C)::value, v[decltype(C)::value]); });
     y = garner_value<RCAP>(e, r, RCAP);
   } else {
     static_for<RCAP>([&](auto C) {
       constexpr int c = decltype(C)::value;
-      r[c] = c < c_act ? reduce_acc<RCAP>(g, e, c, v[c]) : 0u;
+      r[c] = c < c_act ? reduce_acc<RCAP>(e, c, v[c]) : 0u;
     });
     y = garner_value<RCAP>(e, r, c_act);
   }
@@ -446,7 +427,7 @@ __device__ __forceinline__ void finish_element(KGemmArgs &g, const Epi<RCAP> &e,
 // branch taken once per workgroup instead of once per element.
 template <int RCAP, typename F>
 __device__ __forceinline__ void with_epilogue(const Epi<RCAP> &e, int c_act, F &&f) {
-  if (c_act == RCAP && e.lut_channels == 0) {
+  if (c_act == RCAP) {
     if (e.out_dtype == RNSMX_INT64)
       f(std::true_type{}, std::integral_constant<int, kOutInt64>{});
     else

@@ -338,8 +338,9 @@ static int stream_ks_cap(int rcap, int mb, int nb) {
 // Kernel family and tile for an M x N x kp problem, from sweeps on MI355X
 // (K = 768 and 4096, N = 2304 and 12288).  Up to 128 rows the stream kernel
 // (K split over 4 waves) keeps the most weight loads in flight.  Beyond
-// that the LDS-staged kernel (256 x 64 tiles) wherever it applies and its
-// tiles alone give every CU a workgroup; otherwise the MFMA kernel:
+// that the LDS-staged kernel (256 x 64 tiles) wherever it applies, K is at
+// least 2048 (at K = 768 the MFMA kernel's 64 x 64 tiles measured faster)
+// and its tiles alone give every CU a workgroup; otherwise the MFMA kernel:
 // 128 x 128 tiles once they give >= 1024 workgroups (their weight reuse then
 // pays for one wave per SIMD), else 64 x 64 tiles (two waves per SIMD)
 // while they give >= 256 workgroups, else 32 x 64 tiles.
@@ -358,7 +359,7 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
     c.ks = std::min(stream_ks_cap(rcap, c.mb, c.nb), std::max(1, (nk + u - 1) / u));
     return c;
   }
-  if (lds_kernel_fits(g, araw, rcap) && tiles(kLdsBM, kLdsBN) >= 256) {
+  if (lds_kernel_fits(g, araw, rcap) && g.kp >= 2048 && tiles(kLdsBM, kLdsBN) >= 256) {
     c.kind = kLds;
     return c;
   }
