@@ -215,6 +215,26 @@ int32_t rnsmx_matmul_residues_prepared(
 int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb,
                                 int32_t ks);
 
+/* int32 scratch words rnsmx_quantize_symmetric needs (zeroed once). */
+#define RNSMX_QUANT_SCRATCH 1025
+
+/*
+ * Per-tensor symmetric quantization of activations, two launches:
+ * scale_dev[0] = max(amax|x| * fl32(1 / qmax), FLT_EPSILON) and
+ * q_dev[i] = clamp(rint(x[i] / scale), -qmax, qmax) with qmax =
+ * 2^(quant_bits-1) - 1, int8 for 8 bits, int16 for 12 or 16.  x_dev is
+ * float32, float16 or bfloat16 [count], contiguous.  scratch_dev holds
+ * RNSMX_QUANT_SCRATCH int32 that the caller zeroes once and keeps per
+ * stream (calls on one scratch must not overlap); each call leaves it
+ * zeroed again.  NaN inputs are not propagated (the reference's amax would
+ * propagate them).
+ * Replaces RNSLinear._symmetric_scale + _quantize on activations
+ * (src/rns_llm/layers/rns_linear.py:154-166, called at 249-250).
+ */
+int32_t rnsmx_quantize_symmetric(const void *x_dev, int32_t x_dtype, int64_t count,
+                                 int32_t quant_bits, int32_t *scratch_dev, float *scale_dev,
+                                 void *q_dev, void *stream);
+
 /*
  * Garner reconstruction of centered residues [R][count] int8 -> int64.
  * Replaces _C.decode_garner (csrc/rns_cuda.cu:818-885, kernel 416-440).

@@ -432,6 +432,86 @@ static size_t dtype_size(int32_t dtype) {
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// ---------------------------------------------------------------------------
+// Per-tensor symmetric quantization of activations: RNSLinear's
+// _symmetric_scale + _quantize (src/rns_llm/layers/rns_linear.py:154-166)
+// in two launches instead of a chain of elementwise and reduction ops.
+//   scale = max(amax|x| * fl32(1 / qmax), eps_f32)   (the GPU reference
+//           divides by the Python float qmax as a multiply by its float
+//           reciprocal)
+//   q     = clamp(rint(x / scale), -qmax, qmax)      (correctly rounded
+//           division: tensor / tensor)
+// The amax pass writes per-block maxima; the last block to finish (an
+// atomic ticket) folds them, writes the scale and resets the ticket, so the
+// scratch (RNSMX_QUANT_SCRATCH int32, zeroed once by the caller) is left
+// ready for the next call on the same stream.
+// ---------------------------------------------------------------------------
+struct QuantArgs {
+  const void *x;
+  int64_t count;
+  int32_t dtype;
+  float qmax, rcp;  // rcp = fl32(1 / qmax)
+  uint32_t *partial, *ticket;
+  float *scale;
+  void *q;
+  int32_t out16;
+};
+
+__device__ __forceinline__ float quant_input(const QuantArgs &a, int64_t i) {
+  switch (a.dtype) {
+    case RNSMX_FLOAT16: return __half2float(static_cast<const __half *>(a.x)[i]);
+    case RNSMX_BFLOAT16:
+      return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t *>(a.x)[i]) << 16);
+    default: return static_cast<const float *>(a.x)[i];
+  }
+}
+
+__global__ __launch_bounds__(256) void quant_amax_kernel(const QuantArgs a) {
+  __shared__ float wmax[4];
+  __shared__ int last;
+  float m = 0.0f;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < a.count;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    m = fmaxf(m, fabsf(quant_input(a, i)));
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = wmax[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) b = fmaxf(b, wmax[w]);
+    __hip_atomic_store(a.partial + blockIdx.x, __float_as_uint(b), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __threadfence();
+    last = atomicAdd(a.ticket, 1u) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  float t = 0.0f;
+  for (unsigned b = threadIdx.x; b < gridDim.x; b += blockDim.x)
+    t = fmaxf(t, __uint_as_float(__hip_atomic_load(a.partial + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+  for (int off = 32; off > 0; off >>= 1) t = fmaxf(t, __shfl_xor(t, off, 64));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = t;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float amax = wmax[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) amax = fmaxf(amax, wmax[w]);
+    *a.scale = fmaxf(amax * a.rcp, 1.1920928955078125e-07f);  // FLT_EPSILON
+    __hip_atomic_store(a.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+__global__ __launch_bounds__(256) void quant_apply_kernel(const QuantArgs a) {
+  const float s = *a.scale;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < a.count;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const float t = fminf(fmaxf(rintf(quant_input(a, i) / s), -a.qmax), a.qmax);
+    if (a.out16)
+      static_cast<int16_t *>(a.q)[i] = static_cast<int16_t>(t);
+    else
+      static_cast<int8_t *>(a.q)[i] = static_cast<int8_t>(t);
+  }
+}
+
 }  // namespace rnsmx
 
 // ---------------------------------------------------------------------------
@@ -753,6 +833,40 @@ int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb, int32_t ks
   if (kind != kLds && (mb < 1 || nb < 1)) return fail(RNSMX_EINVAL, "tile blocks must be positive");
   g_override = GemmChoice{kind, mb, nb, ks};
   return RNSMX_OK;
+}
+
+int32_t rnsmx_quantize_symmetric(const void *x_dev, int32_t x_dtype, int64_t count,
+                                 int32_t quant_bits, int32_t *scratch_dev, float *scale_dev,
+                                 void *q_dev, void *stream) {
+  clear_error();
+  if (x_dtype != RNSMX_FLOAT32 && x_dtype != RNSMX_FLOAT16 && x_dtype != RNSMX_BFLOAT16)
+    return fail(RNSMX_EINVAL, "activations must be float32, float16 or bfloat16");
+  if (quant_bits != 8 && quant_bits != 12 && quant_bits != 16)
+    return fail(RNSMX_EINVAL, "quant_bits must be 8, 12 or 16");
+  if (count < 0) return fail(RNSMX_EINVAL, "bad element count");
+  if (!scratch_dev || !scale_dev || (count > 0 && (!x_dev || !q_dev)))
+    return fail(RNSMX_EINVAL, "null pointer");
+  QuantArgs a{};
+  a.x = x_dev;
+  a.count = count;
+  a.dtype = x_dtype;
+  const int32_t qmax = (1 << (quant_bits - 1)) - 1;
+  a.qmax = static_cast<float>(qmax);
+  a.rcp = 1.0f / a.qmax;
+  a.partial = reinterpret_cast<uint32_t *>(scratch_dev) + 1;
+  a.ticket = reinterpret_cast<uint32_t *>(scratch_dev);
+  a.scale = scale_dev;
+  a.q = q_dev;
+  a.out16 = quant_bits != 8;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned blocks = static_cast<unsigned>(
+      std::max<int64_t>(1, std::min<int64_t>((count + 2047) / 2048, RNSMX_QUANT_SCRATCH - 1)));
+  hipLaunchKernelGGL(quant_amax_kernel, dim3(blocks), dim3(256), 0, st, a);
+  if (int32_t rc = check_launch("quant_amax")) return rc;
+  if (count == 0) return RNSMX_OK;
+  const unsigned qblocks = static_cast<unsigned>(std::min<int64_t>((count + 255) / 256, 16384));
+  hipLaunchKernelGGL(quant_apply_kernel, dim3(qblocks), dim3(256), 0, st, a);
+  return check_launch("quant_apply");
 }
 
 int32_t rnsmx_decode_garner(const int8_t *residues_dev, int64_t count, const rnsmx_moduli_t *mods,

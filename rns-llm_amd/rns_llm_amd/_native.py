@@ -35,8 +35,11 @@ EXPORTED_SYMBOLS = (
     "rnsmx_matmul_prepared_fused",
     "rnsmx_matmul_residues_prepared",
     "rnsmx_set_gemm_override",
+    "rnsmx_quantize_symmetric",
     "rnsmx_decode_garner",
 )
+
+QUANT_SCRATCH = 1025  # RNSMX_QUANT_SCRATCH
 
 
 class Moduli(ctypes.Structure):
@@ -98,6 +101,7 @@ _SIGNATURES = {
         _I32, [_P, _I64, _I32, _I32, _I32, _P, ctypes.POINTER(Moduli), _P, _I32,
                ctypes.POINTER(Epilogue), _P, _P]),
     "rnsmx_set_gemm_override": (_I32, [_I32, _I32, _I32, _I32]),
+    "rnsmx_quantize_symmetric": (_I32, [_P, _I32, _I64, _I32, _P, _P, _P, _P]),
     "rnsmx_decode_garner": (_I32, [_P, _I64, ctypes.POINTER(Moduli), _P, _P]),
 }
 

@@ -180,6 +180,7 @@ class HipRNSBackend:
             raise RuntimeError("no GPU is visible to this PyTorch (ROCm) installation")
         self._lib = _native.lib()
         self._device_cache: dict[tuple[int, tuple[int, ...]], _DeviceConstants] = {}
+        self._quant_scratch: dict[tuple[int, int], torch.Tensor] = {}
         self._stats: Counter[str] = Counter()
 
     # ------------------------------------------------------------------
@@ -249,6 +250,39 @@ class HipRNSBackend:
             src.data_ptr(), _native.dtype_code(values.dtype), 1, n, n, consts.native_ref,
             out.data_ptr(), None, None, _stream_handle(values.device)))
         return out
+
+    # ------------------------------------------------------------------
+    # Activation quantization (RNSLinear._symmetric_scale / _quantize,
+    # rns_linear.py:154-166 of the reference)
+    # ------------------------------------------------------------------
+    def quantize_symmetric(self, values: torch.Tensor, quant_bits: int = 8):
+        """Per-tensor symmetric quantization of float activations in two
+        launches: ``(q, scale)`` with ``scale = max(amax|v| / qmax, eps)``
+        ([1, 1] float32, the division rounded as the GPU reference rounds
+        ``tensor / python_float``) and ``q = clamp(round(v / scale), ±qmax)``
+        (int8 for 8 bits, int16 for 12 or 16), ``q`` shaped like ``values``.
+        Bit-identical to the reference's torch chain for finite inputs."""
+        if values.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            raise ValueError("quantize_symmetric expects float32, float16 or bfloat16 values")
+        if not values.is_cuda:
+            raise ValueError("values must be on a GPU")
+        if quant_bits not in (8, 12, 16):
+            raise ValueError("quant_bits must be 8, 12 or 16")
+        x = values.contiguous()
+        device = x.device
+        q = torch.empty(x.shape, dtype=torch.int8 if quant_bits == 8 else torch.int16, device=device)
+        scale = torch.empty((1, 1), dtype=torch.float32, device=device)
+        stream = _stream_handle(device)
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        scratch = self._quant_scratch.get((index, stream))
+        if scratch is None:
+            # zeroed once; every call leaves it zeroed again
+            scratch = torch.zeros((_native.QUANT_SCRATCH,), dtype=torch.int32, device=device)
+            self._quant_scratch[(index, stream)] = scratch
+        _native.check(self._lib.rnsmx_quantize_symmetric(
+            x.data_ptr(), _native.dtype_code(x.dtype), int(x.numel()), int(quant_bits),
+            scratch.data_ptr(), scale.data_ptr(), q.data_ptr(), stream))
+        return q, scale
 
     # ------------------------------------------------------------------
     # Bounds and selection (cuda_backend.py:205-261)

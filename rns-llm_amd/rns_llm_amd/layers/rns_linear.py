@@ -125,6 +125,17 @@ class RNSLinear(nn.Module):
         return torch.clamp(torch.round(values / scale), -self.quant_max,
                            self.quant_max).to(self.quant_dtype)
 
+    def _bias_float(self):
+        """float32 copy of the bias for the fused epilogue, cached per bias
+        version (one conversion per weight update, not per call)."""
+        if self.bias is None:
+            return None
+        key = (self.bias.data_ptr(), self.bias._version, self.bias.dtype)
+        if getattr(self, "_bias_key", None) != key:
+            self._bias_f32 = self.bias.detach().float().contiguous()
+            self._bias_key = key
+        return self._bias_f32
+
     @torch.no_grad()
     def prepare_weight(self) -> None:
         if self.backend is None:
@@ -192,16 +203,23 @@ class RNSLinear(nn.Module):
 
         self.prepare_weight()
         original_shape = inputs.shape[:-1]
-        flat = inputs.reshape(-1, self.in_features).float().contiguous()
-        activation_scale = self._symmetric_scale(flat)
-        quantized_a = self._quantize(flat, activation_scale).contiguous()
+        flat = inputs.reshape(-1, self.in_features)
+        if (hasattr(self.backend, "quantize_symmetric") and flat.is_cuda
+                and flat.dtype in (torch.float32, torch.float16, torch.bfloat16)):
+            # the same scale and integers as the torch chain below, in two launches
+            quantized_a, activation_scale = self.backend.quantize_symmetric(
+                flat, self.quant_bits)
+        else:
+            flat = flat.float().contiguous()
+            activation_scale = self._symmetric_scale(flat)
+            quantized_a = self._quantize(flat, activation_scale).contiguous()
         rows = flat.shape[0]
 
         fused_epi = (self.fused_epilogue and hasattr(self.backend, "prepare_weight_nk")
                      and inputs.dtype in (torch.float32, torch.float16, torch.bfloat16))
         if fused_epi and (self.adaptive_channels or (self.fused and self._supports_fused())):
             out = torch.empty((rows, self.out_features), dtype=inputs.dtype, device=inputs.device)
-            bias = self.bias.float().contiguous() if self.bias is not None else None
+            bias = self._bias_float()
             epi = dict(out=out, a_scale=activation_scale.reshape(1), w_scale=self._weight_scale,
                        bias=bias)
             if self.adaptive_channels:

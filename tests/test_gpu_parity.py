@@ -381,3 +381,31 @@ def test_rnslinear_weight_version_invalidates_cache(backend):
     assert layer._prepared_weight is not first
     want, _ = linear_oracle.linear_forward(x.cpu(), layer.weight.detach().cpu(), layer.bias.detach().cpu())
     assert torch.equal(y.cpu(), want)
+
+
+# ---------------------------------------------------------------------------
+# activation quantization (RNSLinear._symmetric_scale / _quantize)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(1, 768), (3, 100), (256, 768), (4096, 768), (2, 5, 33)])
+@pytest.mark.parametrize("bits", [8, 12])
+def test_quantize_symmetric_matches_reference_chain(backend, dtype, shape, bits):
+    gen = torch.Generator().manual_seed(sum(shape) + bits)
+    x = (torch.randn(shape, generator=gen) * 3).to(dtype)
+    # a few fixed values: zeros of both signs, halves, the largest magnitude
+    x.view(-1)[: min(8, x.numel())] = torch.tensor([0.5, -0.5, 1.5, -2.5, 0.0, -0.0, 3.5, 127.0],
+                                                  dtype=dtype)[: min(8, x.numel())]
+    q, scale = backend.quantize_symmetric(x.to(DEV), bits)
+    want_q, want_scale = linear_oracle.quantize_activations(x, shape[-1], bits)
+    assert scale.shape == (1, 1) and torch.equal(scale.cpu(), want_scale)
+    assert torch.equal(q.cpu().reshape(-1, shape[-1]), want_q)
+    # the scratch is left ready: a second call on the same stream agrees
+    q2, scale2 = backend.quantize_symmetric(x.to(DEV), bits)
+    assert torch.equal(q2, q) and torch.equal(scale2, scale)
+
+
+def test_quantize_symmetric_validation(backend):
+    with pytest.raises(ValueError):
+        backend.quantize_symmetric(torch.ones(4, 4, dtype=torch.int8, device=DEV))
+    with pytest.raises(ValueError):
+        backend.quantize_symmetric(torch.ones(4, 4, device=DEV), quant_bits=7)
