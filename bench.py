@@ -199,9 +199,18 @@ def measure_shape(backend, name, m, k, n_each, parts, steps, warmup, rotate_byte
 
 # --- HBM traffic from PMC counters -----------------------------------------
 
+# shapes of the counter workload: (name, m, k, n_each, parts, calls)
+PMC_SHAPES = {
+    "headline": [("C2", None, 768, 768, 3, 12)],
+    "all": [("C2", 256, 768, 768, 3, 6), ("C3", 1, 768, 768, 1, 6), ("C5", 1, 4096, 4096, 3, 4),
+            ("C5", 2048, 4096, 4096, 3, 3)],
+}
+
+
 def pmc_child(args):
     """Workload of one counter pass: a 64 MiB device copy (calibration) and
-    the headline GEMM calls."""
+    GEMM calls on rotated weights (the headline shape, or with
+    --pmc-shapes all the C2 M=256, C3, C5 M=1 and C5 M=2048 shapes)."""
     import torch
 
     from rns_llm_amd import HipRNSBackend
@@ -213,14 +222,18 @@ def pmc_child(args):
     for _ in range(3):
         y.copy_(x)
     torch.cuda.synchronize()
-    k, n = 768, 2304
-    count = rotation_count(k, n, int(args.rotate_mb * 1e6))
-    prepared, _ = make_weights(backend, k, 768, 3, count, 17, device)
-    a = make_tokens(args.m, k, 18, device)
-    ws = backend.create_workspace(device=device, channels=4, m=args.m, n=n, k=k)
-    for i in range(12):
-        backend.matmul_prepared_fused(a, prepared[(i + 1) % count], workspace=ws)
-    torch.cuda.synchronize()
+    for name, m, k, n_each, parts, calls in PMC_SHAPES[args.pmc_shapes]:
+        m = args.m if m is None else m
+        n = n_each * parts
+        count = rotation_count(k, n, int(min(args.rotate_mb, 450.0) * 1e6))
+        prepared, _ = make_weights(backend, k, n_each, parts, count, 17, device)
+        a = make_tokens(m, k, 18, device)
+        ws = backend.create_workspace(device=device, channels=4, m=m, n=n, k=k)
+        for i in range(calls):
+            backend.matmul_prepared_fused(a, prepared[(i + 1) % count], workspace=ws)
+        torch.cuda.synchronize()
+        del prepared, ws
+        torch.cuda.empty_cache()
     print("pmc child done", flush=True)
 
 
@@ -392,7 +405,9 @@ def main():
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--no-extra", action="store_true", help="headline shape only")
     parser.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
-    parser.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
+    parser.add_argument("--pmc-child", action="store_true",
+                        help="run only the counter workload (under rocprofv3 --pmc)")
+    parser.add_argument("--pmc-shapes", choices=sorted(PMC_SHAPES), default="headline")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): the RNS GEMM path has "
