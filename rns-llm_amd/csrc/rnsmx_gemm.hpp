@@ -838,10 +838,13 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
 // ---------------------------------------------------------------------------
 // Large-M GEMM with LDS staging (raw int8 A, up to 4 channels).  A workgroup
 // of NW waves owns a 256 x 64 output tile for every channel; per K step of
-// 64 bytes it stages 16 A fragments (256 rows) and 4*R B fragments (64
-// columns x R channels), 1 KB each in MFMA fragment order, with
-// direct-to-LDS loads (global_load_lds_dwordx4: no register staging, so
-// S - 1 steps of loads are in flight).  The waves split the tile
+// 64 bytes it stages 256 rows of A and 4*R B fragments (64 columns x R
+// channels, 1 KB each in MFMA fragment order) with direct-to-LDS loads
+// (global_load_lds_dwordx4: no register staging, so S - 1 steps of loads
+// are in flight).  A is loaded two K steps at a time as whole 128-byte row
+// segments, so every load instruction touches 8 cache lines rather than 16
+// half-used ones: the vector-memory address unit, not the MFMAs, bounds
+// this loop, and A's share of its work halves.  The waves split the tile
 // (NW / 2) x 2; while a wave runs the MFMAs of step k it reads the
 // fragments of step k + 1 from LDS into the registers the MFMAs have just
 // released.  One barrier per K step.  Rows past M and columns past N are
@@ -886,9 +889,8 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
   constexpr int STAGE = (AF + BF) * 1024;
   constexpr int WM = NW / 2, WN = 2;          // wave grid
   constexpr int MI = AF / WM, NJ = kLdsBN / 16 / WN;  // fragments of a wave's tile
-  constexpr int AU = AF / NW, BU = BF / NW;   // direct-to-LDS loads per wave per step
-  constexpr int NL = AU + BU;
-  static_assert(AF % NW == 0 && BF % NW == 0, "fragments split evenly over the waves");
+  constexpr int BU = BF / NW;                 // B loads per wave per step
+  static_assert(BF % NW == 0, "B fragments split evenly over the waves");
   __shared__ __attribute__((aligned(1024))) int8_t smem[S * STAGE];
   __shared__ int64_t red[NW];
   __shared__ int bcast;
@@ -901,17 +903,26 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
   const int m0 = mt * kLdsBM, n0 = nt * kLdsBN;
   const int nk = g.kp >> 6;
 
-  // Direct-to-LDS sources.  A fragment f = wave + NW u: rows m0 + 16 f +
-  // (lane & 15) (clamped to M - 1), bytes 16 (lane >> 4) of each 64-byte K
-  // step: a per-lane offset from A's base.  B fragment q = wave + NW u:
-  // channel q / 4, column block q % 4 (clamped to the last), one contiguous
-  // 1 KB block per K step: a per-wave base and offset 16 * lane.  Channels
-  // past c_act read channel 0 (their sums are not used).
-  uint32_t aoff[AU];
-  static_for<AU>([&](auto U) {
+  // Direct-to-LDS sources.  A is loaded two K steps at a time, as whole
+  // 128-byte row segments: block b (8 rows, 1 KB) of the pair of steps
+  // (e, e + 1), e even, lands in the A region of stage (e % S) + b / 16 at
+  // slot (b % 16); its LDS 16-byte chunk s holds row 8 b + (s >> 3) and
+  // bytes 16 ((s & 7) ^ (s >> 3)) of the 128-byte segment (the XOR spreads
+  // the 8 rows that one fragment read serves over distinct banks).  Block
+  // b = wave + NW u is loaded by this wave: a per-lane offset from A's base.
+  // B fragment q = wave + NW u: channel q / 4, column block q % 4 (clamped
+  // to the last), one contiguous 1 KB block per K step: a per-wave base and
+  // offset 16 * lane.  Channels past c_act read channel 0 (their sums are
+  // not used).
+  constexpr int ABLK = kLdsBM / 8;            // A blocks per pair of steps
+  constexpr int AU2 = ABLK / NW;              // A loads per wave per pair
+  static_assert(ABLK % NW == 0 && 16 % NW == 0 && ABLK == 2 * AF, "A blocks split evenly, 16 per stage");
+  static_assert(S % 2 == 0, "pairs of steps share a stage pair");
+  uint32_t aoff[AU2];
+  static_for<AU2>([&](auto U) {
     constexpr int u = decltype(U)::value;
-    const int row = min(m0 + (wave + NW * u) * 16 + (lane & 15), g.m - 1);
-    aoff[u] = static_cast<uint32_t>(row * g.a_ld + (lane >> 4) * 16);
+    const int row = min(m0 + (wave + NW * u) * 8 + (lane >> 3), g.m - 1);
+    aoff[u] = static_cast<uint32_t>(row * g.a_ld + ((lane & 7) ^ (lane >> 3)) * 16);
   });
   const int8_t *bbase[BU];
   const int nblk = (g.n + 15) >> 4;
@@ -926,29 +937,53 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
   const uint32_t sbase = __builtin_amdgcn_readfirstlane(
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t *)(smem))) +
       wave * 1024);
-  // loads of K step ks into stage ST (steps past K, issued near the end,
-  // load the last step again; their stages are never read)
-  auto dma = [&](auto ST, int ks) {
-    constexpr int st = decltype(ST)::value;
+  // B load L of K step ks into stage ST; A load U of the pair of steps
+  // starting at ks (even) into the stage pair starting at ST.  Loads past
+  // K, issued near the end, load the last step (pair) again into stages
+  // that are never read.
+  auto dma_b = [&](auto ST, auto L, int ks) {
+    constexpr int st = decltype(ST)::value, l = decltype(L)::value;
     const int kc = min(ks, nk - 1);
-    static_for<AU>([&](auto U) {
-      constexpr int u = decltype(U)::value;
-      lds_dma16<st * STAGE + NW * u * 1024>(abase + kc * 64, aoff[u], sbase);
-    });
-    static_for<BU>([&](auto U) {
-      constexpr int u = decltype(U)::value;
-      lds_dma16<st * STAGE + (AF + NW * u) * 1024>(bbase[u] + static_cast<int64_t>(kc) * 1024, boff, sbase);
-    });
+    lds_dma16<st * STAGE + (AF + NW * l) * 1024>(bbase[l] + static_cast<int64_t>(kc) * 1024, boff, sbase);
+  };
+  auto dma_a = [&](auto ST, auto U, int ks) {
+    constexpr int st = decltype(ST)::value, u = decltype(U)::value;
+    const int kc = min(ks, nk - 2);
+    // block wave + NW u: stage st + (NW u) / 16, slot (NW u) % 16 + wave
+    lds_dma16<(st + (NW * u) / 16) * STAGE + ((NW * u) % 16) * 1024>(abase + kc * 64, aoff[u], sbase);
+  };
+  // the loads of step k (stage st = k % S): B of step k + S - 1 and, when
+  // k is odd, the A pair (k + S - 1, k + S); spread over the (c, j) groups
+  constexpr int NLE = BU, NLO = BU + AU2;     // loads issued at even / odd steps
+  auto dma_part = [&](auto H, auto L, int k) {
+    constexpr int h = decltype(H)::value, l = decltype(L)::value;
+    if constexpr (l < BU)
+      dma_b(std::integral_constant<int, (h + S - 1) % S>{}, L, k + S - 1);
+    else
+      dma_a(std::integral_constant<int, (h + S - 1) % S>{}, std::integral_constant<int, l - BU>{}, k + S - 1);
   };
 
-  // Rolling fragment registers: A fragment i of the next step is read as
-  // soon as the MFMAs of this step are done with it, B fragment (c, j)
-  // during the MFMAs of the last A fragment.
-  i32x4 fa[MI], fb[RCAP][NJ];
+  // Fragment registers: B fragment (c, j) of the next step is read as soon
+  // as the last MFMA of this step that uses it has issued; A fragments are
+  // double-buffered by step parity and the next step's are read during the
+  // first MI (c, j) groups, so every read has most of a step to land before
+  // its first use and no read waits at the step boundary.
+  i32x4 fa[2][MI], fb[RCAP][NJ];
   const int8_t *rbase = smem + lane * 16;
-  auto read_a = [&](auto ST, auto I) {
-    constexpr int st = decltype(ST)::value, i = decltype(I)::value;
-    fa[i] = *reinterpret_cast<const i32x4 *>(rbase + st * STAGE + (wm * MI + i) * 1024);
+  // A fragment i of this wave, parity p of a pair: rows 16 f + (lane & 15)
+  // with f = wm MI + i, i.e. block 2 f + ((lane >> 3) & 1), chunk
+  // 4 p + (lane >> 4) of row (lane & 7)
+  static_assert(16 % (2 * MI) == 0, "a wave's A fragments share one stage of the pair");
+  const int8_t *rabase[2];
+  static_for<2>([&](auto P) {
+    constexpr int p = decltype(P)::value;
+    const int f0 = wm * MI;
+    rabase[p] = smem + ((2 * f0) / 16) * STAGE + ((2 * f0) % 16) * 1024 + ((lane >> 3) & 1) * 1024 +
+                ((lane & 7) * 8 + ((4 * p + (lane >> 4)) ^ (lane & 7))) * 16;
+  });
+  auto read_a = [&](auto H, auto BUF, auto I) {
+    constexpr int h = decltype(H)::value, buf = decltype(BUF)::value, i = decltype(I)::value;
+    fa[buf][i] = *reinterpret_cast<const i32x4 *>(rabase[h & 1] + (h & ~1) * STAGE + 2 * i * 1024);
   };
   auto read_b = [&](auto ST, auto C, auto J) {
     constexpr int st = decltype(ST)::value, c = decltype(C)::value, j = decltype(J)::value;
@@ -959,32 +994,52 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
     static_for<MI>([&](auto I) { static_for<NJ>([&](auto J) { acc[C][I][J] = acc_zero(); }); });
   });
   // one K step k at stage h: wait until step k + 1 landed (own loads, then
-  // everyone's, which also frees the stage of k - 1), refill that stage
-  // with step k + S - 1, then the MFMAs of step k (every channel: no branch
-  // in the loop, inactive channels' sums are dropped by the epilogue) with
-  // the reads of step k + 1's fragments behind them.
+  // everyone's, which also frees the stage of k - 1 and, at odd k with the
+  // LDS reads of this step drained first, the A region of stage k), refill
+  // them, then the MFMAs of step k (every channel: no branch in the loop,
+  // inactive channels' sums are dropped by the epilogue) with the reads of
+  // step k + 1's fragments between them.  The loads of step k - 1 may still
+  // be in flight: NLO of them after an odd step, NLE after an even one.
+  static_assert(RCAP * NJ >= MI, "the A reads ride on the first MI (c, j) groups");
+  static_assert(RCAP * NJ >= NLO, "a step's loads fit one per (c, j) group");
   auto step = [&](auto H, int k) {
     constexpr int h = decltype(H)::value;
-    constexpr int nxt = (h + 1) % S;
-    wait_vmcnt<(S - 3) * NL>();
+    constexpr int nxt = (h + 1) % S, buf = h & 1, nl = (h & 1) ? NLO : NLE;
+    if constexpr (h & 1) __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x3 << 14));  // lgkmcnt(0)
+    wait_vmcnt<(h & 1) ? NLE : NLO>();
     __builtin_amdgcn_s_barrier();
-    dma(std::integral_constant<int, (h + S - 1) % S>{}, k + S - 1);
-    static_for<MI>([&](auto I) {
-      constexpr int i = decltype(I)::value;
-      static_for<RCAP>([&](auto C) {
-        constexpr int c = decltype(C)::value;
-        static_for<NJ>([&](auto J) {
-          constexpr int j = decltype(J)::value;
-          acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[c][j], acc[c][i][j], 0, 0, 0);
-          if constexpr (i == MI - 1) read_b(std::integral_constant<int, nxt>{}, C, J);
+    static_for<RCAP>([&](auto C) {
+      constexpr int c = decltype(C)::value;
+      static_for<NJ>([&](auto J) {
+        constexpr int j = decltype(J)::value, q = c * NJ + j;
+        // load L at group (L * groups) / nl
+        static_for<nl>([&](auto L) {
+          constexpr int l = decltype(L)::value;
+          if constexpr ((l * RCAP * NJ) / nl == q) dma_part(H, L, k);
         });
+        static_for<MI>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[buf][i], fb[c][j], acc[c][i][j], 0, 0, 0);
+        });
+        read_b(std::integral_constant<int, nxt>{}, C, J);
+        if constexpr (q < MI)
+          read_a(std::integral_constant<int, nxt>{}, std::integral_constant<int, buf ^ 1>{},
+                 std::integral_constant<int, q>{});
+        // keep the reads where they are: the scheduler otherwise sinks each
+        // one to just before its first use, which exposes its latency
+        __builtin_amdgcn_sched_barrier(0);
       });
-      read_a(std::integral_constant<int, nxt>{}, I);
     });
   };
 
-  // prologue: steps 0 .. S-2 in flight in stages 0 .. S-2
-  static_for<S - 1>([&](auto T) { dma(T, static_cast<int>(decltype(T)::value)); });
+  // prologue: steps 0 .. S-2 in flight (A pairs (0, 1) and (2, 3), B of
+  // steps 0 .. 2), in the order the loop's waits count them
+  static_assert(S == 4, "the prologue covers one trip's first three steps");
+  static_for<AU2>([&](auto U) { dma_a(std::integral_constant<int, 0>{}, U, 0); });
+  static_for<BU>([&](auto L) { dma_b(std::integral_constant<int, 0>{}, L, 0); });
+  static_for<BU>([&](auto L) { dma_b(std::integral_constant<int, 1>{}, L, 1); });
+  static_for<AU2>([&](auto U) { dma_a(std::integral_constant<int, 2>{}, U, 2); });
+  static_for<BU>([&](auto L) { dma_b(std::integral_constant<int, 2>{}, L, 2); });
   Epi<RCAP> e;
   load_epi<RCAP>(g, e, c_act);
   pin_epi<RCAP>(e);
@@ -996,12 +1051,21 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
   const int rw0 = m0 + wm * (MI * 16), cw0 = n0 + wn * (NJ * 16);
   ColScale cs[NJ];
   static_for<NJ>([&](auto J) { cs[J] = col_scale<RCAP>(e, cw0 + decltype(J)::value * 16 + (lane & 15), n_lim); });
-  wait_vmcnt<(S - 2) * NL>();
+  // step 0 landed: at most the B loads of steps 1, 2 and the second A pair
+  // (or fewer, when column factors were loaded after them) in flight
+  wait_vmcnt<2 * BU + AU2>();
   __builtin_amdgcn_s_barrier();
+  // the loop's read order, so the wait counts at the loop head are the
+  // same whether it is entered from here or from the last step of a trip
   static_for<RCAP>([&](auto C) {
-    static_for<NJ>([&](auto J) { read_b(std::integral_constant<int, 0>{}, C, J); });
+    static_for<NJ>([&](auto J) {
+      constexpr int q = decltype(C)::value * NJ + decltype(J)::value;
+      read_b(std::integral_constant<int, 0>{}, C, J);
+      if constexpr (q < MI)
+        read_a(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, std::integral_constant<int, q>{});
+      __builtin_amdgcn_sched_barrier(0);
+    });
   });
-  static_for<MI>([&](auto I) { read_a(std::integral_constant<int, 0>{}, I); });
 
   // S steps per trip (the stage of each step is a constant); the launcher
   // guarantees nk % S == 0 and K % 64 == 0
