@@ -215,7 +215,7 @@ int32_t rnsmx_matmul_residues_prepared(
 int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb,
                                 int32_t ks);
 
-/* int32 scratch words rnsmx_quantize_symmetric needs (zeroed once). */
+/* 32-bit scratch words rnsmx_quantize_symmetric needs (per-block maxima). */
 #define RNSMX_QUANT_SCRATCH 1025
 
 /*
@@ -224,10 +224,11 @@ int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb,
  * q_dev[i] = clamp(rint(x[i] / scale), -qmax, qmax) with qmax =
  * 2^(quant_bits-1) - 1, int8 for 8 bits, int16 for 12 or 16.  x_dev is
  * float32, float16 or bfloat16 [count], contiguous.  scratch_dev holds
- * RNSMX_QUANT_SCRATCH int32 that the caller zeroes once and keeps per
- * stream (calls on one scratch must not overlap); each call leaves it
- * zeroed again.  NaN inputs are not propagated (the reference's amax would
- * propagate them).
+ * RNSMX_QUANT_SCRATCH 32-bit words of per-block maxima passed from the
+ * first launch to the second; its contents before a call do not matter,
+ * and calls that share one scratch must not overlap (keep one per stream).
+ * NaN inputs are not propagated (the reference's amax would propagate
+ * them).
  * Replaces RNSLinear._symmetric_scale + _quantize on activations
  * (src/rns_llm/layers/rns_linear.py:154-166, called at 249-250).
  */

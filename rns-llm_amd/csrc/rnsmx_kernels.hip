@@ -359,7 +359,15 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
     c.ks = std::min(stream_ks_cap(rcap, c.mb, c.nb), std::max(1, (nk + u - 1) / u));
     return c;
   }
-  if (lds_kernel_fits(g, araw, rcap) && g.kp >= 2048 && tiles(kLdsBM, kLdsBN) >= 256) {
+  // The LDS kernel's 256 x 64 tiles run one workgroup per CU (128 KB of
+  // LDS each), so at short K, where a tile's prologue and epilogue weigh
+  // more, it wins only when its tiles fill whole rounds of the chip's 256
+  // CUs (measured at K = 768-1024: 3 and 1 full rounds faster than the
+  // MFMA kernel by 7 % and 30 %; 2.25 rounds slower by 6 %).
+  const int64_t lds_tiles = tiles(kLdsBM, kLdsBN);
+  const int64_t rounds = (lds_tiles + 255) / 256;
+  const bool full_rounds = 8 * lds_tiles >= 7 * 256 * rounds;
+  if (lds_kernel_fits(g, araw, rcap) && lds_tiles >= 256 && (g.kp >= 2048 || full_rounds)) {
     c.kind = kLds;
     return c;
   }
@@ -441,75 +449,105 @@ static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 
 //           reciprocal)
 //   q     = clamp(rint(x / scale), -qmax, qmax)      (correctly rounded
 //           division: tensor / tensor)
-// The amax pass writes per-block maxima; the last block to finish (an
-// atomic ticket) folds them, writes the scale and resets the ticket, so the
-// scratch (RNSMX_QUANT_SCRATCH int32, zeroed once by the caller) is left
-// ready for the next call on the same stream.
+// The amax pass writes one maximum per block (at most 256 blocks) into the
+// scratch; every block of the quantize pass folds them
+// again (a few hundred floats from L2) and derives the same scale, so no
+// atomics or last-block logic are needed and the scratch carries nothing
+// from one call to the next.  Both passes read 16 bytes per lane when the
+// activations are 16-byte aligned.
 // ---------------------------------------------------------------------------
 struct QuantArgs {
   const void *x;
   int64_t count;
-  int32_t dtype;
+  int32_t vec;      // 1: x is 16-byte aligned, read in 16-byte vectors
+  int32_t nparts;   // blocks of the amax pass
   float qmax, rcp;  // rcp = fl32(1 / qmax)
-  uint32_t *partial, *ticket;
+  float *partial;
   float *scale;
   void *q;
-  int32_t out16;
 };
 
-__device__ __forceinline__ float quant_input(const QuantArgs &a, int64_t i) {
-  switch (a.dtype) {
-    case RNSMX_FLOAT16: return __half2float(static_cast<const __half *>(a.x)[i]);
-    case RNSMX_BFLOAT16:
-      return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t *>(a.x)[i]) << 16);
-    default: return static_cast<const float *>(a.x)[i];
-  }
-}
+// Input element decoding: float32, or the bits of a float16 / bfloat16.
+template <typename T>
+struct QuantIn;
+template <>
+struct QuantIn<float> {
+  __device__ static float get(float v) { return v; }
+};
+struct Bf16Bits {
+  uint16_t bits;
+};
+template <>
+struct QuantIn<__half> {
+  __device__ static float get(uint16_t v) { return __half2float(__ushort_as_half(v)); }
+};
+template <>
+struct QuantIn<Bf16Bits> {
+  __device__ static float get(uint16_t v) { return __uint_as_float(static_cast<uint32_t>(v) << 16); }
+};
+template <typename T>
+using QuantRaw = typename std::conditional<std::is_same<T, float>::value, float, uint16_t>::type;
 
-__global__ __launch_bounds__(256) void quant_amax_kernel(const QuantArgs a) {
-  __shared__ float wmax[4];
-  __shared__ int last;
-  float m = 0.0f;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < a.count;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    m = fmaxf(m, fabsf(quant_input(a, i)));
+// Block-wide max of non-negative floats (256 threads).
+__device__ __forceinline__ float block_max256(float m, float *wmax) {
   for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
   if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float b = wmax[0];
-    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) b = fmaxf(b, wmax[w]);
-    __hip_atomic_store(a.partial + blockIdx.x, __float_as_uint(b), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __threadfence();
-    last = atomicAdd(a.ticket, 1u) == gridDim.x - 1;
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  float t = 0.0f;
-  for (unsigned b = threadIdx.x; b < gridDim.x; b += blockDim.x)
-    t = fmaxf(t, __uint_as_float(__hip_atomic_load(a.partial + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
-  for (int off = 32; off > 0; off >>= 1) t = fmaxf(t, __shfl_xor(t, off, 64));
-  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = t;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float amax = wmax[0];
-    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) amax = fmaxf(amax, wmax[w]);
-    *a.scale = fmaxf(amax * a.rcp, 1.1920928955078125e-07f);  // FLT_EPSILON
-    __hip_atomic_store(a.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  return fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
 }
 
-__global__ __launch_bounds__(256) void quant_apply_kernel(const QuantArgs a) {
-  const float s = *a.scale;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < a.count;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const float t = fminf(fmaxf(rintf(quant_input(a, i) / s), -a.qmax), a.qmax);
-    if (a.out16)
-      static_cast<int16_t *>(a.q)[i] = static_cast<int16_t>(t);
-    else
-      static_cast<int8_t *>(a.q)[i] = static_cast<int8_t>(t);
+template <typename T>
+__global__ __launch_bounds__(256) void quant_amax_kernel(const QuantArgs a) {
+  using R = QuantRaw<T>;
+  constexpr int V = 16 / sizeof(R);
+  __shared__ float wmax[4];
+  const R *x = static_cast<const R *>(a.x);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t nvec = a.vec ? a.count / V : 0;
+  float m = 0.0f;
+  for (int64_t i = tid; i < nvec; i += stride) {
+    R v[V];
+    *reinterpret_cast<uint4 *>(v) = reinterpret_cast<const uint4 *>(x)[i];
+    static_for<V>([&](auto E) { m = fmaxf(m, fabsf(QuantIn<T>::get(v[decltype(E)::value]))); });
   }
+  for (int64_t i = nvec * V + tid; i < a.count; i += stride) m = fmaxf(m, fabsf(QuantIn<T>::get(x[i])));
+  m = block_max256(m, wmax);
+  if (threadIdx.x == 0) a.partial[blockIdx.x] = m;
+}
+
+template <typename T, typename Q>
+__global__ __launch_bounds__(256) void quant_apply_kernel(const QuantArgs a) {
+  using R = QuantRaw<T>;
+  constexpr int V = 16 / sizeof(R);
+  __shared__ float wmax[4];
+  float t = 0.0f;
+  for (int b = threadIdx.x; b < a.nparts; b += blockDim.x) t = fmaxf(t, a.partial[b]);
+  const float amax = block_max256(t, wmax);
+  const float s = fmaxf(amax * a.rcp, 1.1920928955078125e-07f);  // FLT_EPSILON
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale = s;
+  const R *x = static_cast<const R *>(a.x);
+  Q *q = static_cast<Q *>(a.q);
+  auto quant = [&](R raw) {
+    return static_cast<Q>(fminf(fmaxf(rintf(QuantIn<T>::get(raw) / s), -a.qmax), a.qmax));
+  };
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t nvec = a.vec ? a.count / V : 0;
+  for (int64_t i = tid; i < nvec; i += stride) {
+    R v[V];
+    *reinterpret_cast<uint4 *>(v) = reinterpret_cast<const uint4 *>(x)[i];
+    Q o[V];
+    static_for<V>([&](auto E) { o[decltype(E)::value] = quant(v[decltype(E)::value]); });
+    // V outputs: 4-16 bytes, aligned to their size (q is 16-byte aligned)
+    if constexpr (sizeof(o) == 16)
+      reinterpret_cast<uint4 *>(q)[i] = *reinterpret_cast<const uint4 *>(o);
+    else if constexpr (sizeof(o) == 8)
+      reinterpret_cast<uint2 *>(q)[i] = *reinterpret_cast<const uint2 *>(o);
+    else
+      reinterpret_cast<uint32_t *>(q)[i] = *reinterpret_cast<const uint32_t *>(o);
+  }
+  for (int64_t i = nvec * V + tid; i < a.count; i += stride) q[i] = quant(x[i]);
 }
 
 }  // namespace rnsmx
@@ -849,24 +887,39 @@ int32_t rnsmx_quantize_symmetric(const void *x_dev, int32_t x_dtype, int64_t cou
   QuantArgs a{};
   a.x = x_dev;
   a.count = count;
-  a.dtype = x_dtype;
   const int32_t qmax = (1 << (quant_bits - 1)) - 1;
   a.qmax = static_cast<float>(qmax);
   a.rcp = 1.0f / a.qmax;
-  a.partial = reinterpret_cast<uint32_t *>(scratch_dev) + 1;
-  a.ticket = reinterpret_cast<uint32_t *>(scratch_dev);
+  a.partial = reinterpret_cast<float *>(scratch_dev);
   a.scale = scale_dev;
   a.q = q_dev;
-  a.out16 = quant_bits != 8;
+  // vector reads need x and q 16-byte aligned (q holds V outputs per vector)
+  a.vec = aligned16(x_dev) && aligned16(q_dev);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned blocks = static_cast<unsigned>(
-      std::max<int64_t>(1, std::min<int64_t>((count + 2047) / 2048, RNSMX_QUANT_SCRATCH - 1)));
-  hipLaunchKernelGGL(quant_amax_kernel, dim3(blocks), dim3(256), 0, st, a);
-  if (int32_t rc = check_launch("quant_amax")) return rc;
-  if (count == 0) return RNSMX_OK;
-  const unsigned qblocks = static_cast<unsigned>(std::min<int64_t>((count + 255) / 256, 16384));
-  hipLaunchKernelGGL(quant_apply_kernel, dim3(qblocks), dim3(256), 0, st, a);
+  // ~32 KB of input per block, at most 256 blocks (the chip's CU count)
+  const int64_t bytes = count * (x_dtype == RNSMX_FLOAT32 ? 4 : 2);
+  const unsigned blocks =
+      static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>((bytes + 32767) / 32768, 256)));
+  static_assert(256 < RNSMX_QUANT_SCRATCH, "the scratch holds one maximum per block");
+  a.nparts = static_cast<int32_t>(blocks);
+  const int vlen = x_dtype == RNSMX_FLOAT32 ? 4 : 8;
+  const unsigned qblocks = static_cast<unsigned>(
+      std::max<int64_t>(1, std::min<int64_t>((count / vlen + 255) / 256 + 1, 2048)));
+  const bool out16 = quant_bits != 8;
+#define RNSMX_QUANT(T)                                                                               \
+  hipLaunchKernelGGL(quant_amax_kernel<T>, dim3(blocks), dim3(256), 0, st, a);                       \
+  if (int32_t rc = check_launch("quant_amax")) return rc;                                            \
+  if (out16)                                                                                         \
+    hipLaunchKernelGGL((quant_apply_kernel<T, int16_t>), dim3(qblocks), dim3(256), 0, st, a);        \
+  else                                                                                               \
+    hipLaunchKernelGGL((quant_apply_kernel<T, int8_t>), dim3(qblocks), dim3(256), 0, st, a);         \
   return check_launch("quant_apply");
+  switch (x_dtype) {
+    case RNSMX_FLOAT16: { RNSMX_QUANT(__half) }
+    case RNSMX_BFLOAT16: { RNSMX_QUANT(Bf16Bits) }
+    default: { RNSMX_QUANT(float) }
+  }
+#undef RNSMX_QUANT
 }
 
 int32_t rnsmx_decode_garner(const int8_t *residues_dev, int64_t count, const rnsmx_moduli_t *mods,

@@ -276,8 +276,8 @@ class HipRNSBackend:
         index = device.index if device.index is not None else torch.cuda.current_device()
         scratch = self._quant_scratch.get((index, stream))
         if scratch is None:
-            # zeroed once; every call leaves it zeroed again
-            scratch = torch.zeros((_native.QUANT_SCRATCH,), dtype=torch.int32, device=device)
+            # per-block maxima passed between the two launches of one call
+            scratch = torch.empty((_native.QUANT_SCRATCH,), dtype=torch.int32, device=device)
             self._quant_scratch[(index, stream)] = scratch
         _native.check(self._lib.rnsmx_quantize_symmetric(
             x.data_ptr(), _native.dtype_code(x.dtype), int(x.numel()), int(quant_bits),
