@@ -63,6 +63,8 @@ typedef struct rnsmx_moduli {
   uint32_t ucoef[RNSMX_MAX_CHANNELS][RNSMX_MAX_CHANNELS];
                                        /* [j][i], j<i: -(prod_{l<j} m_l)*qinv_i mod m_i */
   int64_t prefix[RNSMX_MAX_CHANNELS + 1]; /* prod_{j<i} m_j, i = 0..channels  */
+  int32_t qk16[RNSMX_MAX_CHANNELS];    /* 2^16 * qinv_i mod m_i, centered (|.| <= m_i/2) */
+  uint32_t qk8[RNSMX_MAX_CHANNELS];    /* 2^8 * qinv_i mod m_i                */
 } rnsmx_moduli_t;
 
 /* Thread-local text of the last error (empty string when none). */

@@ -194,8 +194,8 @@ __device__ __forceinline__ int active_channels(KGemmArgs &g, int64_t *red, int *
 // round of scalar-cache misses is exposed.
 template <int RCAP>
 struct Epi {
-  uint32_t m[RCAP], m24[RCAP], c16[RCAP], bias[RCAP], qinv[RCAP];
-  int32_t negm[RCAP];
+  uint32_t m[RCAP], m24[RCAP], c16[RCAP], bias[RCAP], qinv[RCAP], qk8[RCAP];
+  int32_t negm[RCAP], qk16[RCAP];
   uint32_t u[RCAP][RCAP];  // u[j][c], j < c
   int64_t prefix[RCAP + 1];
   int64_t p_act;  // prefix[c_act], the modulus of the signed correction
@@ -216,6 +216,8 @@ __device__ __forceinline__ void fill_moduli(Epi<RCAP> &e, const Mods &mods, int 
     const uint32_t m = static_cast<uint32_t>(mods.moduli[c]), magic = mods.magic[c];
     e.m[c] = m;
     e.qinv[c] = mods.qinv[c];
+    e.qk16[c] = mods.qk16[c];
+    e.qk8[c] = mods.qk8[c];
     static_for<c>([&](auto J) { e.u[decltype(J)::value][c] = mods.ucoef[decltype(J)::value][c]; });
     // the 24-bit reduction constants (see canon_fast); channels past the
     // set's size have m = 0 and are never used
@@ -266,6 +268,10 @@ __device__ __forceinline__ void pin_epi(Epi<RCAP> &e) {
     pin_sgpr(e.bias[c]);
     pin_sgpr(e.negm[c]);
     pin_sgpr(e.qinv[c]);
+    if constexpr (c > 0) {
+      pin_sgpr(e.qk16[c]);
+      pin_sgpr(e.qk8[c]);
+    }
     static_for<c>([&](auto J) { pin_sgpr(e.u[decltype(J)::value][c]); });
   });
   static_for<RCAP + 1>([&](auto C) { pin_sgpr(e.prefix[decltype(C)::value]); });
@@ -325,6 +331,58 @@ __device__ __forceinline__ int64_t garner_value(const Epi<RCAP> &e, const uint32
   if constexpr (RCAP <= 4) {
     // x = x32 < P <= 255^4 < 2^32: the correction x - P lies in [-P/2, 0),
     // so its high word is -1 and its low word is x - P mod 2^32.
+    const uint32_t p32 = static_cast<uint32_t>(e.p_act);
+    const bool neg = x32 > (p32 >> 1);
+    const uint32_t lo = neg ? x32 - p32 : x32;
+    const uint32_t hi = neg ? 0xFFFFFFFFu : 0u;
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+  } else {
+    const int64_t p = e.p_act;
+    int64_t y = static_cast<int64_t>(static_cast<uint64_t>(x32) + x64);
+    if (y > (p >> 1)) y -= p;
+    return y;
+  }
+}
+
+// The same signed integer straight from the int32 channel sums v[0..c_act).
+// Channel 0's digit is its canonical residue; every later digit takes one
+// reduction instead of two (residue, then digit): with v = a2 2^16 + a1 2^8
+// + a0 (a2 = v >> 16 signed, a1 and a0 bytes),
+//   v q_c = a2 qk16_c + a1 qk8_c + a0 q_c (mod m_c),
+// qk16_c = 2^16 q_c mod m_c centered (|qk16_c| <= 127) and qk8_c = 2^8 q_c
+// mod m_c.  |a2 qk16_c| <= 2^15 * 127 = 4,161,536 < bias_c (a multiple of
+// m_c above 2^23 - 256), so s = a2 qk16_c + a1 qk8_c + a0 q_c + bias_c +
+// sum_{j<c} d_j u_{j,c} is positive and at most 4,161,536 + 2 * 255 * 254 +
+// 2^23 + 9 * 254^2 = 13,260,328 < 2^24: one mod_small gives d_c.  Every
+// multiply is 24-bit.
+template <int RCAP>
+__device__ __forceinline__ int64_t garner_from_sums(const Epi<RCAP> &e, const int32_t (&v)[RCAP], int c_act) {
+  uint32_t d[RCAP];
+  uint32_t x32 = 0;
+  uint64_t x64 = 0;
+  static_for<RCAP>([&](auto C) {
+    constexpr int c = decltype(C)::value;
+    if (c >= c_act) {
+      d[c] = 0;
+      return;
+    }
+    if constexpr (c == 0) {
+      d[0] = reduce_acc<RCAP>(e, 0, v[0]);  // q_0 = 1
+    } else {
+      const int32_t a2 = v[c] >> 16;
+      const uint32_t a1 = (static_cast<uint32_t>(v[c]) >> 8) & 0xFFu, a0 = static_cast<uint32_t>(v[c]) & 0xFFu;
+      uint32_t s = static_cast<uint32_t>(__mul24(a2, e.qk16[c])) + __umul24(a1, e.qk8[c]) +
+                   __umul24(a0, e.qinv[c]) + e.bias[c];
+      static_for<c>([&](auto J) { s += __umul24(d[decltype(J)::value], e.u[decltype(J)::value][c]); });
+      d[c] = mod_small(s, e.m[c], e.m24[c], e.negm[c]);
+    }
+    if constexpr (c < 4) {
+      x32 += __umul24(d[c], static_cast<uint32_t>(e.prefix[c]));
+    } else {
+      x64 += static_cast<uint64_t>(d[c]) * static_cast<uint64_t>(e.prefix[c]);
+    }
+  });
+  if constexpr (RCAP <= 4) {
     const uint32_t p32 = static_cast<uint32_t>(e.p_act);
     const bool neg = x32 > (p32 >> 1);
     const uint32_t lo = neg ? x32 - p32 : x32;
@@ -408,18 +466,7 @@ __device__ __forceinline__ void store_value(const Epi<RCAP> &e, int64_t y, int64
 template <int RCAP, bool FAST, int OUT>
 __device__ __forceinline__ void finish_element(KGemmArgs &g, const Epi<RCAP> &e, int c_act,
                                                const int32_t (&v)[RCAP], int64_t idx, ColScale cs) {
-  uint32_t r[RCAP];
-  int64_t y;
-  if constexpr (FAST) {
-    static_for<RCAP>([&](auto C) { r[decltype(C)::value] = reduce_acc<RCAP>(e, decltype(C)::value, v[decltype(C)::value]); });
-    y = garner_value<RCAP>(e, r, RCAP);
-  } else {
-    static_for<RCAP>([&](auto C) {
-      constexpr int c = decltype(C)::value;
-      r[c] = c < c_act ? reduce_acc<RCAP>(e, c, v[c]) : 0u;
-    });
-    y = garner_value<RCAP>(e, r, c_act);
-  }
+  const int64_t y = garner_from_sums<RCAP>(e, v, FAST ? RCAP : c_act);
   store_value<RCAP, OUT>(e, y, idx, cs);
 }
 

@@ -40,7 +40,7 @@ extern "C" {
 
 const char *rnsmx_last_error(void) { return rnsmx::g_error; }
 
-int32_t rnsmx_abi_version(void) { return 1; }
+int32_t rnsmx_abi_version(void) { return 2; }
 
 int32_t rnsmx_moduli_init(const int32_t *moduli, int32_t channels,
                           rnsmx_moduli_t *out) {
@@ -82,6 +82,11 @@ int32_t rnsmx_moduli_init(const int32_t *moduli, int32_t channels,
     r.c31[i] = static_cast<uint32_t>((1LL << 31) % m);
     const int64_t p_mod = r.prefix[i] % m;
     r.qinv[i] = inverse_mod(p_mod, m);
+    // the Garner digit of channel i straight from its int32 sum v = a2 2^16 +
+    // a1 2^8 + a0: v qinv_i = a2 qk16_i + a1 qk8_i + a0 qinv_i (mod m_i)
+    const int64_t k16 = (65536 % m) * static_cast<int64_t>(r.qinv[i]) % m;
+    r.qk16[i] = static_cast<int32_t>(2 * k16 > m ? k16 - m : k16);
+    r.qk8[i] = static_cast<uint32_t>((256 % m) * static_cast<int64_t>(r.qinv[i]) % m);
     for (int j = 0; j < i; ++j) {
       const int64_t pj = r.prefix[j] % m;
       const int64_t t = (pj * static_cast<int64_t>(r.qinv[i])) % m;

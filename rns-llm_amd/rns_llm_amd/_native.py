@@ -53,6 +53,8 @@ class Moduli(ctypes.Structure):
         ("qinv", ctypes.c_uint32 * MAX_CHANNELS),
         ("ucoef", (ctypes.c_uint32 * MAX_CHANNELS) * MAX_CHANNELS),
         ("prefix", ctypes.c_int64 * (MAX_CHANNELS + 1)),
+        ("qk16", ctypes.c_int32 * MAX_CHANNELS),
+        ("qk8", ctypes.c_uint32 * MAX_CHANNELS),
     ]
 
 
@@ -105,7 +107,7 @@ _SIGNATURES = {
     "rnsmx_decode_garner": (_I32, [_P, _I64, ctypes.POINTER(Moduli), _P, _P]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class NativeError(RuntimeError):

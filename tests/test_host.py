@@ -37,8 +37,8 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_struct_layout_matches_header():
-    # sizeof(rnsmx_moduli_t) with natural alignment: 4 + 4*10*4 + 4*100 + pad + 8*11
-    assert ctypes.sizeof(_native.Moduli) == 4 + 40 * 4 + 400 + 4 + 88
+    # sizeof(rnsmx_moduli_t) with natural alignment: 4 + 4*10*4 + 4*100 + pad + 8*11 + 2*4*10
+    assert ctypes.sizeof(_native.Moduli) == 4 + 40 * 4 + 400 + 4 + 88 + 80
     assert _native.lib().rnsmx_abi_version() == _native.ABI_VERSION
 
 
@@ -55,6 +55,9 @@ def test_native_moduli_constants(mods):
     for i, m in enumerate(mods):
         assert c.magic[i] == (1 << 32) // m
         assert c.c31[i] == (1 << 31) % m
+        # digit constants: 2^16 q and 2^8 q mod m (the first centered)
+        assert (c.qk16[i] - (1 << 16) * c.qinv[i]) % m == 0 and 2 * abs(c.qk16[i]) <= m
+        assert c.qk8[i] == ((1 << 8) * c.qinv[i]) % m
     rng = np.random.default_rng(0)
     res = np.stack([rng.integers(0, m, 300) for m in mods])
     # digits from the native constants: d_i = (r_i q_i + sum_j d_j u_ji) mod m_i
