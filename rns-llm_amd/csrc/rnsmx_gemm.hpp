@@ -45,6 +45,8 @@ struct GemmArgs {
   int32_t m, n, kp;  // kp: multiple of 64, <= b_ld
   int32_t a_k;       // A bytes per row that are read; 16-byte chunks at or past it load as 0
   int32_t tiles_m, tiles_n;  // output tile grid (set at launch)
+  int32_t threads;           // workgroup size (set at launch; read here rather than
+                             // from the hidden arguments, a cache line of its own)
   int32_t lut_channels;
   const int16_t *lut;  // [R][4][256]
   // adaptive prefix
@@ -107,6 +109,31 @@ __device__ __forceinline__ RNSMX_KARG(T) & kernel_args() {
 }
 typedef RNSMX_KARG(GemmArgs) KGemmArgs;
 
+// Touches the first BYTES of the argument block, one read per 64-byte line,
+// in one round at kernel entry.  The block is written for each launch, so
+// its first reads miss the caches; the kernels read the fields that the
+// first operand loads depend on in dependent rounds (the adaptive check,
+// then the tile counts, then the operand pointers), and each of those would
+// otherwise wait a full memory round trip.  With the lines in the scalar
+// cache the later reads hit.  The stream kernel takes only the fields its
+// first operand loads need (kGemmHotArgBytes) and leaves the epilogue's
+// constants (the moduli block) to a round of their own that overlaps those
+// loads: a longer first round measured 1-2 % slower at decode shapes.  The
+// kernels that stage through LDS take the whole block: scalar loads and LDS
+// reads share one completion counter, so epilogue constants still in flight
+// would hold up every LDS wait of the first K steps (C2 M=256: 13.1 -> 12.4 us).
+template <int BYTES>
+__device__ __forceinline__ void prefetch_kernel_args() {
+  const __attribute__((address_space(4))) uint32_t *p =
+      (const __attribute__((address_space(4))) uint32_t *)(__builtin_amdgcn_kernarg_segment_ptr());
+  uint32_t x = 0;
+  static_for<(BYTES + 63) / 64>([&](auto L) { x ^= p[decltype(L)::value * 16]; });
+  asm volatile("" : : "s"(x));
+}
+// GemmArgs through mods.channels: every field read before the first
+// operand loads of the GEMM kernels
+constexpr int kGemmHotArgBytes = static_cast<int>(offsetof(GemmArgs, mods) + sizeof(int32_t));
+
 __device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
@@ -150,16 +177,16 @@ __device__ __forceinline__ int64_t prefix_at(const Mods &mods, int idx) {
 // the full set is used and meta[3] flags the overflow (the reference raises
 // OverflowError on the host, which a device-side selector cannot).
 template <int RCAP>
-__device__ __forceinline__ int active_channels(KGemmArgs &g, int64_t *red, int *bcast) {
+__device__ __forceinline__ int active_channels(KGemmArgs &g, int64_t *red, int *bcast, int nthreads) {
   const int full = g.mods.channels;
   if (g.min_channels <= 0) return full;
   int64_t mx = 0;
-  for (int r = threadIdx.x; r < g.m; r += blockDim.x) {
+  for (int r = threadIdx.x; r < g.m; r += nthreads) {
     const int64_t v = g.row_l1[r];
     mx = v > mx ? v : mx;
   }
   mx = wave_max_i64(mx);
-  const int nw = blockDim.x >> 6;
+  const int nw = nthreads >> 6;
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -536,6 +563,7 @@ constexpr int stream_u_of(int rcap, bool araw, int mb, int nb) {
 template <int RCAP, int MB, int NB, bool ARAW>
 __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
   KGemmArgs &g = kernel_args<GemmArgs>();
+  prefetch_kernel_args<kGemmHotArgBytes>();
   constexpr int BM = 16 * MB, BN = 16 * NB, TILE = BM * BN;
   constexpr int AP = ARAW ? 1 : RCAP;
   constexpr int U = stream_u_of(RCAP, ARAW, MB, NB);
@@ -544,8 +572,8 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
   __shared__ int bcast;
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ks_n = blockDim.x >> 6;
-  const int c_act = active_channels<RCAP>(g, red, &bcast);
+  const int nthreads = g.threads, ks_n = nthreads >> 6;
+  const int c_act = active_channels<RCAP>(g, red, &bcast, nthreads);
   int mt, nt;
   tile_of(g.tiles_m, g.tiles_n, mt, nt);
   const int m0 = mt * BM, n0 = nt * BN;
@@ -669,7 +697,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
     return;
   }
 
-  for (int i = threadIdx.x; i < RCAP * TILE; i += blockDim.x) sacc[i] = 0;
+  for (int i = threadIdx.x; i < RCAP * TILE; i += nthreads) sacc[i] = 0;
   __syncthreads();
   static_for<RCAP>([&](auto C) {
     constexpr int c = decltype(C)::value;
@@ -693,7 +721,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
   const int rows_here = min(BM, m_lim - m0);
   const ColScale(&cs)[4] = cs4;
   with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) {
-    for (int x = threadIdx.x * 4; x < rows_here * BN; x += blockDim.x * 4) {
+    for (int x = threadIdx.x * 4; x < rows_here * BN; x += nthreads * 4) {
       const int row = x / BN, col = x % BN;
       i32x4 sv[RCAP];
       static_for<RCAP>([&](auto C) {
@@ -736,6 +764,7 @@ constexpr int mfma_ac_of(int rcap, int mb, bool araw) {
 template <int RCAP, int MB, int NB, int P, bool ARAW>
 __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
   KGemmArgs &g = kernel_args<GemmArgs>();
+  prefetch_kernel_args<static_cast<int>(sizeof(GemmArgs))>();
   constexpr int BM = 16 * MB, BNW = 16 * NB;
   constexpr int AP = ARAW ? 1 : RCAP;
   constexpr int PLANE = BM * kLdsRow;
@@ -747,7 +776,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
   __shared__ int bcast;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c_act = active_channels<RCAP>(g, red, &bcast);
+  const int c_act = active_channels<RCAP>(g, red, &bcast, 256);
   int mt, nt;
   tile_of(g.tiles_m, g.tiles_n, mt, nt);
   const int m0 = mt * BM, n0 = nt * (4 * BNW) + wave * BNW;
@@ -931,6 +960,7 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
   static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   constexpr int S = kLdsStages;               // even: each step's stage is a constant in a trip
   KGemmArgs &g = kernel_args<GemmArgs>();
+  prefetch_kernel_args<static_cast<int>(sizeof(GemmArgs))>();
   constexpr int AF = kLdsBM / 16;             // A fragments per stage
   constexpr int BF = RCAP * (kLdsBN / 16);    // B fragments per stage
   constexpr int STAGE = (AF + BF) * 1024;
@@ -944,7 +974,7 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
-  const int c_act = active_channels<RCAP>(g, red, &bcast);
+  const int c_act = active_channels<RCAP>(g, red, &bcast, 64 * NW);
   int mt, nt;
   tile_of(g.tiles_m, g.tiles_n, mt, nt);
   const int m0 = mt * kLdsBM, n0 = nt * kLdsBN;
@@ -1156,6 +1186,7 @@ bool launch_stream(GemmArgs g, int mb, int nb, int ks, hipStream_t st) {
     g.tiles_n = (g.n + 16 * NB_ - 1) / (16 * NB_);                                          \
     const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));                          \
     const size_t lds = ks > 1 ? static_cast<size_t>(RCAP) * 256 * MB_ * NB_ * 4 : 0;         \
+    g.threads = 64 * ks;                                                                    \
     hipLaunchKernelGGL((stream_kernel<RCAP, MB_, NB_, ARAW>), grid, dim3(64 * ks), lds, st, g); \
     return true;                                                                            \
   }
