@@ -47,8 +47,6 @@ struct GemmArgs {
   int32_t tiles_m, tiles_n;  // output tile grid (set at launch)
   int32_t threads;           // workgroup size (set at launch; read here rather than
                              // from the hidden arguments, a cache line of its own)
-  int32_t lut_channels;
-  const int16_t *lut;  // [R][4][256]
   // adaptive prefix
   int32_t min_channels;  // 0: all channels
   const int64_t *row_l1;

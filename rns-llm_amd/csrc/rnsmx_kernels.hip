@@ -669,8 +669,6 @@ int32_t rnsmx_matmul_centered_fused_out(const int8_t *a_dev, const int8_t *b_dev
   g.m = m;
   g.n = n;
   g.kp = static_cast<int32_t>(kp);
-  g.lut_channels = lut_channels;
-  g.lut = lut_dev;
   g.min_channels = 0;
   g.out = out_dev;
   g.out_ld = n;
@@ -794,8 +792,6 @@ int32_t rnsmx_matmul_prepared_fused(const void *a_dev, int32_t a_dtype, int32_t 
   g.m = m;
   g.n = n;
   g.kp = static_cast<int32_t>(kp);
-  g.lut_channels = lut_channels;
-  g.lut = lut_dev;
   g.min_channels = min_ch;
   g.row_l1 = row_l1;
   g.w_absmax = min_ch != 0 ? adaptive->w_absmax_dev : nullptr;
@@ -847,8 +843,6 @@ int32_t rnsmx_matmul_residues_prepared(const int8_t *a_res_dev, int64_t a_ld, in
   g.m = m;
   g.n = n;
   g.kp = static_cast<int32_t>(kp);
-  g.lut_channels = lut_channels;
-  g.lut = lut_dev;
   g.min_channels = 0;
   g.out = out_dev;
   g.out_ld = n;
