@@ -1240,11 +1240,13 @@ bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, hipStream_t st) {
   return false;
 }
 
-// The LDS-staged kernel: raw int8 A, K a multiple of 256 (whole trips of
-// four 64-byte steps), 4-channel capacity (16 B fragments per stage split
-// over 8 waves).
+// The LDS-staged kernel: raw int8 A below 4 GB, K a multiple of 256 (whole
+// trips of four 64-byte steps), 4-channel capacity (16 B fragments per stage
+// split over 8 waves).
 inline bool lds_kernel_fits(const GemmArgs &g, bool araw, int rcap) {
-  return araw && rcap == 4 && g.a_k == g.kp && g.kp % (64 * kLdsStages) == 0;
+  // the A loads address rows through a 32-bit per-lane offset from A's base
+  const bool a_offsets_fit = static_cast<int64_t>(g.m) * g.a_ld < (int64_t{1} << 32) - 256;
+  return araw && rcap == 4 && g.a_k == g.kp && g.kp % (64 * kLdsStages) == 0 && a_offsets_fit;
 }
 
 template <int RCAP>
