@@ -628,9 +628,10 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
   auto mfma_chunk = [&]() {
     static_for<U>([&](auto UU) {
       constexpr int u = decltype(UU)::value;
+      // every channel, with no branch (inactive channels read channel 0's
+      // plane; their sums are dropped by the epilogue)
       static_for<RCAP>([&](auto C) {
         constexpr int c = decltype(C)::value;
-        if (c >= c_act) return;
         static_for<MB>([&](auto I) {
           constexpr int i = decltype(I)::value;
           static_for<NB>([&](auto J) {
@@ -862,6 +863,8 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
       const int ks = ks0 + s;
       const int buf = ks & 1;
       i32x4 fa[MB];
+      // skip inactive channels and the steps past K (a straight-line form
+      // measured 13 % slower here: C2 M=256 12.2 -> 13.8 us)
       static_for<RCAP>([&](auto C) {
         constexpr int c = decltype(C)::value;
         if (c >= c_act || ks >= nk) return;
