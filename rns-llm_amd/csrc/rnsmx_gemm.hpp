@@ -2,13 +2,16 @@
 // modular reduction, Garner mixed-radix reconstruction, signed correction
 // and optional dequantization fused into the epilogue.
 //
-// Two families, chosen by the number of output rows M and the tile count:
+// Three families, chosen by the number of output rows M, K and the tile
+// count (choose_gemm):
 //   stream_kernel  decode and small batches: MFMA tiles of (16*MB) x (16*NB),
 //                  K split over the waves of a workgroup, every wave issuing
 //                  all loads of its K slice before its first MFMA
 //   mfma_kernel    larger M: tiles of (16*MB) x (64*NB), A staged through
 //                  LDS with quad-contiguous loads, B streamed into a register
 //                  ring, P K steps of loads in flight
+//   lds_kernel     large M and K (raw int8 A, up to 4 channels): 256 x 64
+//                  tiles, A and B staged by direct-to-LDS loads, 8 waves
 //
 // Layouts: A is [M][a_ld] int8 activations shared by every channel (a_cs = 0;
 // an int8 value is its own representative mod every m_c, so the channel-c
@@ -540,7 +543,7 @@ __device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int &mt, int &
 }
 
 // ---------------------------------------------------------------------------
-// Stream GEMM (M <= 256: continuous batches and the C2 shapes).  The weight
+// Stream GEMM (M <= 128: decode, continuous batches, small C2 shapes).  The weight
 // residues are read once and the problem is a few MB, so latency rules:
 // every wave issues all the loads of a chunk of U K steps before its first
 // MFMA.  A workgroup owns a (16*MB) x (16*NB) output tile; its KS waves
@@ -741,7 +744,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
 }
 
 // ---------------------------------------------------------------------------
-// MFMA GEMM (M > 256: prefill, C4/C5 shapes), bound by MFMA throughput.  A
+// MFMA GEMM (M > 128 where the LDS kernel does not apply: C2 M=256, C4).  A
 // workgroup of 4 waves owns a (16*MB) x (4*16*NB) tile: the A rows (shared by
 // all waves, and in raw mode by all channels) pass through a P-deep register
 // ring into double-buffered LDS with rows padded to 80 bytes (the 16-byte
