@@ -1,0 +1,37 @@
+"""Automatic kernel choice (no override) at the boundaries of its rules:
+stream vs MFMA at M = 128 / 129, the LDS kernel's K >= 2048 gate and its
+full-round rule below it (256 tiles of 256 x 64 vs 2.25 rounds), ragged N
+and K, and K that the LDS kernel cannot take (K % 256 != 0).  Every output
+must equal the exact product."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+DENSE4 = (255, 253, 251, 247)
+
+SHAPES = [
+    (128, 768, 2304),    # stream (M <= 128)
+    (129, 768, 2304),    # MFMA (M > 128)
+    (64, 4096, 1000),    # stream, ragged N
+    (512, 4096, 12288),  # LDS, K >= 2048
+    (1024, 2048, 4096),  # LDS at the K gate, 256 tiles
+    (512, 2048, 4096),   # MFMA: 128 LDS tiles are too few
+    (1024, 1024, 4096),  # LDS below the K gate: 256 tiles, one full round
+    (4096, 768, 2304),   # MFMA: 576 LDS tiles would be 2.25 rounds
+    (1024, 1024, 4090),  # LDS with ragged N (columns clamped)
+    (1000, 1088, 4096),  # K % 256 != 0: MFMA
+    (300, 100, 37),      # ragged everything: K padded to 128
+]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+def test_auto_choice_is_exact(backend, m, k, n):
+    gen = torch.Generator(device=DEV).manual_seed(m * 7 + k + n)
+    w = torch.randint(-127, 128, (n, k), generator=gen, device=DEV, dtype=torch.int8)
+    a = torch.randint(-127, 128, (m, k), generator=gen, device=DEV, dtype=torch.int8)
+    prepared = backend.prepare_weight_nk(w, DENSE4)
+    out = backend.matmul_prepared_fused(a, prepared)
+    want = a.double() @ w.double().t()  # exact: integer sums below 2^53
+    assert torch.equal(out.double(), want)
