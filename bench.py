@@ -70,8 +70,10 @@ def quant_rows_int8(w):
     return torch.clamp(torch.round(w / scale), -127, 127).to(torch.int8)
 
 
-def make_weights(backend, k, n_each, parts, count, seed, device):
-    """`count` prepared fused weights (B^T = [parts*n_each, k]) and the first one's int8."""
+def make_weights(backend, k, n_each, parts, count, seed, device, adaptive=False):
+    """`count` prepared fused weights (B^T = [parts*n_each, k]) and the first
+    one's int8; adaptive: prefix variants from 3 channels (the reference's
+    prepare_weight_adaptive)."""
     import torch
 
     gen = torch.Generator(device=device).manual_seed(seed)
@@ -81,7 +83,8 @@ def make_weights(backend, k, n_each, parts, count, seed, device):
                                               dtype=torch.float32).half().float() * 0.02)
                   for _ in range(parts)]
         w = torch.cat(blocks, dim=0).contiguous()           # [N, K] int8
-        prepared.append(backend.prepare_weight_nk(w, DENSE4))
+        prepared.append(backend.prepare_weight_adaptive_nk(w, DENSE4, min_channels=3) if adaptive
+                        else backend.prepare_weight_nk(w, DENSE4))
         if i == 0:
             first = w
     return prepared, first
@@ -159,24 +162,42 @@ def rotation_count(k, n, rotate_bytes):
     return max(2, math.ceil(rotate_bytes / res_bytes))
 
 
-def measure_shape(backend, name, m, k, n_each, parts, steps, warmup, rotate_bytes, seed, device):
+def measure_shape(backend, name, m, k, n_each, parts, steps, warmup, rotate_bytes, seed, device,
+                  adaptive=False):
+    """One row.  adaptive: the device-side channel prefix
+    (matmul_prepared_adaptive_fused: a row-L1 pass over the activations,
+    then the GEMM choosing its prefix with no host synchronisation); ops_eff
+    counts the channels the device picked."""
     import torch
 
     n = n_each * parts
     r = len(DENSE4)
     count = rotation_count(k, n, rotate_bytes)
-    prepared, w0 = make_weights(backend, k, n_each, parts, count, seed, device)
+    prepared, w0 = make_weights(backend, k, n_each, parts, count, seed, device, adaptive)
     a = make_tokens(m, k, seed + 1, device)
     ws = backend.create_workspace(device=device, channels=r, m=m, n=n, k=k)
-    out0 = backend.matmul_prepared_fused(a, prepared[0], workspace=ws).clone()
+    if adaptive:
+        by_channels = {r: ws}  # the full-set workspace serves every prefix
+
+        def call(i):
+            return backend.matmul_prepared_adaptive_fused(a, prepared[i % count],
+                                                          workspace_by_channels=by_channels)
+        out0, meta = backend.matmul_prepared_adaptive_fused(
+            a, prepared[0], workspace_by_channels=by_channels, return_metadata=True)
+        out0 = out0.clone()
+        r = meta["channels"]
+    else:
+        def call(i):
+            return backend.matmul_prepared_fused(a, prepared[i % count], workspace=ws)
+        out0 = call(0).clone()
     exact_check(out0, a, w0, max_rows=256 if k * n < 4_000_000 else 16)
 
     def step(i):
-        backend.matmul_prepared_fused(a, prepared[i % count], workspace=ws)
+        call(i)
 
     ms, host_ms = graph_steps(step, steps, warmup)
     p50, p95 = per_call(step, min(200, max(50, steps)))
-    if not torch.equal(backend.matmul_prepared_fused(a, prepared[0], workspace=ws), out0):
+    if not torch.equal(call(0), out0):
         raise SystemExit("parity failure: repeated call differs")
     ops = 2 * r * m * k * n
     bytes_alg = m * k + r * k * n + m * n * 8
@@ -184,6 +205,7 @@ def measure_shape(backend, name, m, k, n_each, parts, steps, warmup, rotate_byte
     bound = "hbm" if t_bytes >= t_ops else "mfma"
     row = {
         "config": name, "m": m, "k": k, "n": n, "channels": r, "weight_copies": count,
+        "adaptive": adaptive,
         "ms_per_step": ms, "host_ms_per_step": host_ms,
         "us_per_call_graph": ms * 1000.0, "us_per_call_p50": p50, "us_per_call_p95": p95,
         "eff_tops": ops / (ms * 1e-3) / 1e12, "useful_tops": ops / r / (ms * 1e-3) / 1e12,
@@ -443,10 +465,12 @@ def main():
         extra = [("C2 fused QKV", m, 768, 768, 3, 17) for m in (1, 16, 128)]
         extra += [(f"C3 decode {q} requests", q, 768, 768, 1, 33) for q in (1, 2, 4)]
         extra += [("C5 OPT-6.7B QKV", m, 4096, 4096, 3, 67) for m in (1, 512, 2048)]
+        extra += [("C5 OPT-6.7B QKV adaptive", m, 4096, 4096, 3, 67) for m in (1, 2048)]
         for name, m, k, n_each, parts, seed in extra:
             rows.append(measure_shape(backend, name, m, k, n_each, parts, args.steps, args.warmup,
-                                      rot, seed, device))
+                                      rot, seed, device, adaptive="adaptive" in name))
             log(f"bench: {name} M={m}: {rows[-1]['us_per_call_graph']:.2f} us/step, "
+                f"{rows[-1]['channels']} channels, "
                 f"{rows[-1]['eff_tops']:.1f} eff TOPS, {rows[-1]['gbs_alg']:.0f} GB/s alg, "
                 f"{rows[-1]['bound']} roofline {rows[-1]['roofline_frac']:.3f}")
         try:
