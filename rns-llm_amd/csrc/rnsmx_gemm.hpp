@@ -404,7 +404,9 @@ __device__ __forceinline__ int64_t garner_from_sums(const Epi<RCAP> &e, const in
       static_for<c>([&](auto J) { s += __umul24(d[decltype(J)::value], e.u[decltype(J)::value][c]); });
       d[c] = mod_small(s, e.m[c], e.m24[c], e.negm[c]);
     }
-    if constexpr (c < 4) {
+    if constexpr (c == 0) {
+      x32 = d[0];  // P_0 = 1
+    } else if constexpr (c < 4) {
       x32 += __umul24(d[c], static_cast<uint32_t>(e.prefix[c]));
     } else {
       x64 += static_cast<uint64_t>(d[c]) * static_cast<uint64_t>(e.prefix[c]);
@@ -510,6 +512,50 @@ __device__ __forceinline__ void with_epilogue(const Epi<RCAP> &e, int c_act, F &
   } else {
     f(std::false_type{}, std::integral_constant<int, kOutAny>{});
   }
+}
+
+// Reduction + reconstruction + stores of a wave's (16 MI) x (16 NJ) tile
+// straight from its MFMA accumulators: the lane holds rows 4 (lane >> 4) + t
+// of column lane & 15 of each 16 x 16 block, whose top-left output element
+// is (r0, c0) (wave-uniform).  The row offsets are uniform and kept in
+// scalar registers (left to itself the compiler forms each element's 64-bit
+// offset with a quarter-rate vector multiply-add), and a tile that lies
+// wholly inside the output (nearly every tile) runs a copy of the loop with
+// no per-element bounds test.
+template <int RCAP, int MI, int NJ>
+__device__ __forceinline__ void register_epilogue(KGemmArgs &g, const Epi<RCAP> &e, int c_act,
+                                                  const i32x4 (&acc)[RCAP][MI][NJ], int r0, int c0,
+                                                  int m_lim, int n_lim, const ColScale (&cs)[NJ]) {
+  const int lane = threadIdx.x & 63;
+  const int64_t idx0 = static_cast<int64_t>(r0 + 4 * (lane >> 4)) * e.out_ld + c0 + (lane & 15);
+  const bool interior = r0 + 16 * MI <= m_lim && c0 + 16 * NJ <= n_lim;
+  auto run = [&](auto FAST, auto OUT, auto INTERIOR) {
+    static_for<MI>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      static_for<4>([&](auto T) {
+        constexpr int t = decltype(T)::value;
+        int64_t roff = (i * 16 + t) * e.out_ld;
+        pin_sgpr(roff);
+        const int row = r0 + i * 16 + 4 * (lane >> 4) + t;
+        static_for<NJ>([&](auto J) {
+          constexpr int j = decltype(J)::value;
+          const int col = c0 + j * 16 + (lane & 15);
+          if (decltype(INTERIOR)::value || (row < m_lim && col < n_lim)) {
+            int32_t v[RCAP];
+            static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
+            finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(g, e, c_act, v,
+                                                                              idx0 + roff + j * 16, cs[j]);
+          }
+        });
+      });
+    });
+  };
+  with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) {
+    if (interior)
+      run(FAST, OUT, std::true_type{});
+    else
+      run(FAST, OUT, std::false_type{});
+  });
 }
 
 // Byte offset of channel c's plane with the channel clamped to a valid one:
@@ -891,28 +937,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
     });
   }
 
-  // epilogue from registers: lane holds rows 4*(lane>>4)+t of column lane&15
-  const int64_t idx0 = static_cast<int64_t>(m0 + 4 * (lane >> 4)) * e.out_ld + n0 + (lane & 15);
-  with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) {
-    static_for<MB>([&](auto I) {
-      constexpr int i = decltype(I)::value;
-      static_for<NB>([&](auto J) {
-        constexpr int j = decltype(J)::value;
-        const int col = n0 + j * 16 + (lane & 15);
-        static_for<4>([&](auto T) {
-          constexpr int t = decltype(T)::value;
-          const int row = m0 + i * 16 + 4 * (lane >> 4) + t;
-          if (row < m_lim && col < n_lim) {
-            int32_t v[RCAP];
-            static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
-            // the row step is uniform: only idx0 is per lane
-            const int64_t idx = idx0 + (i * 16 + t) * e.out_ld + j * 16;
-            finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(g, e, c_act, v, idx, cs[j]);
-          }
-        });
-      });
-    });
-  });
+  register_epilogue<RCAP, MB, NB>(g, e, c_act, acc, m0, n0, m_lim, n_lim, cs);
 }
 
 // ---------------------------------------------------------------------------
@@ -1156,27 +1181,7 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
   // the loads issued for steps past K land before the workgroup ends
   wait_vmcnt<0>();
 
-  // epilogue from registers: lane holds rows 4*(lane>>4)+t of column lane&15
-  const int64_t idx0 = static_cast<int64_t>(rw0 + 4 * (lane >> 4)) * e.out_ld + cw0 + (lane & 15);
-  with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) {
-    static_for<MI>([&](auto I) {
-      constexpr int i = decltype(I)::value;
-      static_for<NJ>([&](auto J) {
-        constexpr int j = decltype(J)::value;
-        const int col = cw0 + j * 16 + (lane & 15);
-        static_for<4>([&](auto T) {
-          constexpr int t = decltype(T)::value;
-          const int row = rw0 + i * 16 + 4 * (lane >> 4) + t;
-          if (row < m_lim && col < n_lim) {
-            int32_t v[RCAP];
-            static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
-            const int64_t idx = idx0 + (i * 16 + t) * e.out_ld + j * 16;
-            finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(g, e, c_act, v, idx, cs[j]);
-          }
-        });
-      });
-    });
-  });
+  register_epilogue<RCAP, MI, NJ>(g, e, c_act, acc, rw0, cw0, m_lim, n_lim, cs);
 }
 
 // ---------------------------------------------------------------------------
