@@ -165,18 +165,23 @@ def make_moduli(moduli) -> Moduli:
     return out
 
 
-def dtype_code(dtype) -> int:
-    import torch
+_DTYPE_CODES: dict = {}
 
-    table = {
-        torch.int8: INT8,
-        torch.int16: INT16,
-        torch.int32: INT32,
-        torch.int64: INT64,
-        torch.float32: FLOAT32,
-        torch.float16: FLOAT16,
-        torch.bfloat16: BFLOAT16,
-    }
-    if dtype not in table:
+
+def dtype_code(dtype) -> int:
+    if not _DTYPE_CODES:
+        import torch
+
+        _DTYPE_CODES.update({
+            torch.int8: INT8,
+            torch.int16: INT16,
+            torch.int32: INT32,
+            torch.int64: INT64,
+            torch.float32: FLOAT32,
+            torch.float16: FLOAT16,
+            torch.bfloat16: BFLOAT16,
+        })
+    code = _DTYPE_CODES.get(dtype)
+    if code is None:
         raise ValueError(f"unsupported dtype {dtype}")
-    return table[dtype]
+    return code
