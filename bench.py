@@ -417,6 +417,61 @@ def measure_c4(backend, device, steps, warmup):
     return row
 
 
+# The reference's fused-QKV RNSLinear p50 on its Tesla T4 run
+# (results/v0.5/qkv_fusion.json:20-22, 53-55, 86-88, 119-121), in ms.
+REFERENCE_T4_QKV_P50_MS = {1: 0.859, 16: 0.592, 128: 0.635, 256: 0.702}
+
+
+def measure_qkv_layer(backend, device, tokens_list=(1, 16, 128, 256), warmup=20, iterations=80):
+    """The reference's layer-level QKV benchmark protocol
+    (benchmarks/benchmark_qkv_fusion.py:21-34, 47-75): three fp16
+    nn.Linear(768, 768) fused into one RNSQKVProjection (fused=True,
+    lut_channels=2) and the same three as separate RNSLinear layers, input
+    randn(1, tokens, 768) fp16; per call CUDA events around the eager
+    forward, p50 / p95 over 80 calls after 20 warmup calls.  The fused
+    outputs must equal the separate ones bit for bit."""
+    import torch
+    from torch import nn
+
+    from rns_llm_amd import RNSLinear, RNSQKVProjection
+
+    def measure(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        samples = []
+        for _ in range(iterations):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            fn()
+            end.record()
+            end.synchronize()
+            samples.append(start.elapsed_time(end))
+        samples.sort()
+        return statistics.median(samples), samples[min(len(samples) - 1, math.ceil(0.95 * len(samples)) - 1)]
+
+    torch.manual_seed(17)
+    originals = tuple(nn.Linear(768, 768, bias=True, device=device, dtype=torch.float16).eval()
+                      for _ in range(3))
+    kw = dict(backend=backend, mode="rns", quant_bits=8, fused=True, lut_channels=2)
+    separate = tuple(RNSLinear.from_linear(layer, **kw).eval() for layer in originals)
+    fused = RNSQKVProjection.from_linears(*originals, **kw).eval()
+    rows = []
+    with torch.no_grad():
+        for tokens in tokens_list:
+            x = torch.randn(1, tokens, 768, device=device, dtype=torch.float16)
+            for part, layer in zip(fused(x), separate):
+                if not torch.equal(part, layer(x)):
+                    raise SystemExit(f"parity failure: fused QKV != separate RNSLinear at {tokens} tokens")
+            f50, f95 = measure(lambda: fused(x))
+            s50, s95 = measure(lambda: tuple(layer(x) for layer in separate))
+            rows.append({"tokens": tokens, "fused_p50_us": f50 * 1e3, "fused_p95_us": f95 * 1e3,
+                         "separate_p50_us": s50 * 1e3, "separate_p95_us": s95 * 1e3,
+                         "reference_t4_fused_p50_us": REFERENCE_T4_QKV_P50_MS[tokens] * 1e3})
+    return {"config": "C2 fused QKV RNSLinear layer (fp16 in/out, eager), reference protocol",
+            "rows": rows}
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -473,6 +528,12 @@ def main():
                 f"{rows[-1]['channels']} channels, "
                 f"{rows[-1]['eff_tops']:.1f} eff TOPS, {rows[-1]['gbs_alg']:.0f} GB/s alg, "
                 f"{rows[-1]['bound']} roofline {rows[-1]['roofline_frac']:.3f}")
+        layer = measure_qkv_layer(backend, device)
+        rows.append(layer)
+        for r in layer["rows"]:
+            log(f"bench: QKV RNSLinear layer {r['tokens']} tokens: fused p50 {r['fused_p50_us']:.1f} us "
+                f"(p95 {r['fused_p95_us']:.1f}), separate p50 {r['separate_p50_us']:.1f} us; "
+                f"reference T4 fused p50 {r['reference_t4_fused_p50_us']:.0f} us")
         try:
             c4 = measure_c4(backend, device, steps=5, warmup=2)
             rows.append(c4)
