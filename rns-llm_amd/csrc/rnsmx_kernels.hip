@@ -1,7 +1,8 @@
 // rnsmx device code for gfx950 (MI355X) outside the GEMM: residue
 // encoders, Garner decode of residue planes, operand repacking for the
 // drop-in fused op, the GEMM kernel choice and the C ABI.  The GEMM kernels
-// themselves live in rnsmx_gemm.hpp (instantiated in rnsmx_gemm_r*.hip).
+// themselves live in rnsmx_gemm.hpp (instantiated in rnsmx_gemm_part.hip,
+// once per channel capacity and part).
 //
 // Data layout in HBM
 //   residue planes   [R][rows][ld] int8, K contiguous, ld a multiple of 64
@@ -376,7 +377,11 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   if (rcap <= 4 && tiles(128, 128) >= 1024) {
     c.mb = 8;
     c.nb = 2;
-  } else if (tiles(64, 64) >= 256) {
+  } else if (tiles(64, 64) >= 128) {
+    // one 64 x 64 tile per CU beats twice as many 32 x 64 tiles (which leave
+    // some CUs with two) as long as at least half the 256 CUs get one:
+    // C2 M=256 (144 tiles) 11.9 vs 12.2 us, M=320 12.1 vs 12.6, N=3072
+    // 12.3 vs 13.1; at M=192 (108 tiles) 11.8 vs 9.9 the other way
     c.mb = 4;
     c.nb = 1;
   } else {
