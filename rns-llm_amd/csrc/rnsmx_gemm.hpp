@@ -793,8 +793,10 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
 // MFMA GEMM (M > 128 where the LDS kernel does not apply: C2 M=256, C4).  A
 // workgroup of 4 waves owns a (16*MB) x (4*16*NB) tile: the A rows (shared by
 // all waves, and in raw mode by all channels) pass through a P-deep register
-// ring into double-buffered LDS with rows padded to 80 bytes (the 16-byte
-// fragment reads of 16 lanes hit disjoint banks); each wave owns 16*NB
+// ring into double-buffered LDS, 64-byte rows whose four 16-byte chunks are
+// XOR-swizzled by row bits 1-2 (a_chunk_off), so both the row-wise writes
+// (4 lanes per row) and the fragment reads (16 lanes down a column of
+// chunks) hit disjoint banks in every group of 8 lanes; each wave owns 16*NB
 // columns and streams their weight residues straight from global memory into
 // a P-deep register ring.  Loads of K step ks + P are issued while step ks
 // computes; the loop runs a multiple of P steps with the steps past K fed
@@ -802,7 +804,12 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
 // channels, so all channel accumulators finish together and the reduction +
 // Garner + store run from registers.
 // ---------------------------------------------------------------------------
-constexpr int kLdsRow = 80;
+constexpr int kLdsRow = 64;
+
+// LDS offset of 16-byte chunk `part` (0..3) of A row `row` in one plane.
+__device__ __forceinline__ int a_chunk_off(int row, int part) {
+  return row * kLdsRow + ((part ^ ((row >> 1) & 3)) << 4);
+}
 
 constexpr int mfma_ac_of(int rcap, int mb, bool araw) {
   const int chunks = (araw ? 1 : rcap) * 16 * mb * 4;
@@ -829,7 +836,6 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
   tile_of(g.tiles_m, g.tiles_n, mt, nt);
   const int m0 = mt * BM, n0 = nt * (4 * BNW) + wave * BNW;
   const int nk = g.kp >> 6;
-  const int kofs = (lane >> 4) * 16;
 
   // A staging: chunk q -> plane p, row, 16-byte part
   const int8_t *asrc[AC];
@@ -843,7 +849,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
     const int p = qq / (BM * 4), w = qq % (BM * 4), row = w >> 2, part = w & 3;
     const int grow = min(m0 + row, g.m - 1);
     asrc[i] = g.a + plane_off(p, c_act, g.a_cs) + static_cast<int64_t>(grow) * g.a_ld;
-    alds[i] = inside ? p * PLANE + row * kLdsRow + part * 16 : AP * PLANE;
+    alds[i] = inside ? p * PLANE + a_chunk_off(row, part) : AP * PLANE;
     apart[i] = part * 16;
     aon[i] = inside && (ARAW || p < c_act);
   });
@@ -905,7 +911,8 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
   __syncthreads();
 
   const int steps = (nk + P - 1) / P * P;
-  const int a_frag = (lane & 15) * kLdsRow + kofs;
+  // rows 16 i + (lane & 15) share (row >> 1) & 3 for every i: one per-lane offset
+  const int a_frag = a_chunk_off(lane & 15, lane >> 4);
   for (int ks0 = 0; ks0 < steps; ks0 += P) {
     static_for<P>([&](auto SS) {
       constexpr int s = decltype(SS)::value;
