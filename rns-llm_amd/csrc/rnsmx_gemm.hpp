@@ -1118,7 +1118,14 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
   auto step = [&](auto H, int k) {
     constexpr int h = decltype(H)::value;
     constexpr int nxt = (h + 1) % S, buf = h & 1, nl = (h & 1) ? NLO : NLE;
-    if constexpr (h & 1) __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x3 << 14));  // lgkmcnt(0)
+    // odd steps overwrite this step's A region: this wave's reads of it (the
+    // A fragments read during the previous step, each followed by at least
+    // LAFTER B reads in issue order) must have completed before the barrier;
+    // LDS reads complete in order and the loop issues no scalar loads, so
+    // lgkmcnt(LAFTER) suffices and the trailing B reads stay in flight
+    constexpr int LAFTER = RCAP * NJ - MI;
+    static_assert(LAFTER >= 0 && LAFTER < 16, "lgkmcnt is 4 bits");
+    if constexpr (h & 1) __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (LAFTER << 8) | (0x3 << 14));
     wait_vmcnt<(h & 1) ? NLE : NLO>();
     __builtin_amdgcn_s_barrier();
     static_for<RCAP>([&](auto C) {
