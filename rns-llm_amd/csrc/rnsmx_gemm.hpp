@@ -913,7 +913,11 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
   const int steps = (nk + P - 1) / P * P;
   // rows 16 i + (lane & 15) share (row >> 1) & 3 for every i: one per-lane offset
   const int a_frag = a_chunk_off(lane & 15, lane >> 4);
-  for (int ks0 = 0; ks0 < steps; ks0 += P) {
+  // One trip round the ring.  MORE: later trips follow, so each step issues
+  // the loads of step ks + P; the last trip issues none (every step it
+  // could load lies past K), and its last step stages nothing.
+  auto trip = [&](int ks0, auto MORE) {
+    constexpr bool more = decltype(MORE)::value;
     static_for<P>([&](auto SS) {
       constexpr int s = decltype(SS)::value;
       const int ks = ks0 + s;
@@ -938,11 +942,15 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
           });
         });
       });
-      gload(SS, ks + P);
-      lstore(std::integral_constant<int, (s + 1) % P>{}, buf ^ 1);
-      __syncthreads();
+      if constexpr (more) gload(SS, ks + P);
+      if constexpr (more || s + 1 < P) {
+        lstore(std::integral_constant<int, (s + 1) % P>{}, buf ^ 1);
+        __syncthreads();
+      }
     });
-  }
+  };
+  for (int ks0 = 0; ks0 < steps - P; ks0 += P) trip(ks0, std::true_type{});
+  trip(steps - P, std::false_type{});
 
   register_epilogue<RCAP, MB, NB>(g, e, c_act, acc, m0, n0, m_lim, n_lim, cs);
 }
@@ -1225,7 +1233,9 @@ bool launch_stream(GemmArgs g, int mb, int nb, int ks, hipStream_t st) {
 
 // p_req: ring depth (K steps of A and B loads in flight), 0 = the tile's
 // default.  Deeper rings than 3-4 steps cost occupancy (registers) and
-// measured slower on every shape tried.  NBSEL: the tile widths this
+// measured slower on every shape tried, also where a workgroup per CU
+// leaves one wave per SIMD anyway (C2 M=256 with 64 x 64 tiles: ring of 12,
+// i.e. all of K = 768 in flight, 12.1 us against 11.0 us with 3).  NBSEL: the tile widths this
 // instantiation covers (0 all, 1 or 2 only NB = NBSEL).
 template <int RCAP, bool ARAW, int NBSEL>
 bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, hipStream_t st) {
