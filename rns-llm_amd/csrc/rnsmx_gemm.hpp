@@ -1258,6 +1258,7 @@ bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, hipStream_t st) {
   if constexpr (RCAP <= 4) {
     RNSMX_MFMA(2, 1, 3, RNSMX_MFMA_P(2, 1, 3) RNSMX_MFMA_P(2, 1, 4))
     RNSMX_MFMA(4, 1, 3, RNSMX_MFMA_P(4, 1, 3) RNSMX_MFMA_P(4, 1, 4))
+    RNSMX_MFMA(3, 1, 3, RNSMX_MFMA_P(3, 1, 3) RNSMX_MFMA_P(3, 1, 4))
     RNSMX_MFMA(2, 2, 3, RNSMX_MFMA_P(2, 2, 3) RNSMX_MFMA_P(2, 2, 4))
     RNSMX_MFMA(4, 2, 3, RNSMX_MFMA_P(4, 2, 3) RNSMX_MFMA_P(4, 2, 4))
     RNSMX_MFMA(8, 2, 3, RNSMX_MFMA_P(8, 2, 3) RNSMX_MFMA_P(8, 2, 4))

@@ -343,8 +343,8 @@ static int stream_ks_cap(int rcap, int mb, int nb) {
 // least 2048 (at K = 768 the MFMA kernel's 64 x 64 tiles measured faster)
 // and its tiles alone give every CU a workgroup; otherwise the MFMA kernel:
 // 128 x 128 tiles once they give >= 1024 workgroups (their weight reuse then
-// pays for one wave per SIMD), else 64 x 64 tiles (two waves per SIMD)
-// while they give >= 256 workgroups, else 32 x 64 tiles.
+// pays for one wave per SIMD), else 32, 48 or 64 x 64 tiles, the height
+// that leaves the fewest rows on any CU.
 static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   const int rcap = rcap_for(g.mods.channels);
   const int nk = g.kp / 64;
@@ -374,20 +374,32 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   }
   c.kind = kMfma;
   c.ks = 0;  // the tile's default ring depth
+  c.nb = 1;
   if (rcap <= 4 && tiles(128, 128) >= 1024) {
     c.mb = 8;
     c.nb = 2;
-  } else if (tiles(64, 64) >= 128) {
-    // one 64 x 64 tile per CU beats twice as many 32 x 64 tiles (which leave
-    // some CUs with two) as long as at least half the 256 CUs get one:
-    // C2 M=256 (144 tiles) 11.9 vs 12.2 us, M=320 12.1 vs 12.6, N=3072
-    // 12.3 vs 13.1; at M=192 (108 tiles) 11.8 vs 9.9 the other way
-    c.mb = 4;
-    c.nb = 1;
-  } else {
-    c.mb = 2;
-    c.nb = 1;
+    return c;
   }
+  // 32, 48 or 64 x 64 tiles: the height that gives the fewest rows per CU,
+  // counted as rounds of 256 workgroups times the tile height; on a tie
+  // the taller tile (fewer workgroups).  Measured on MI355X at K = 768 (and
+  // K = 4096, N = 12288), this picks the fastest height at every shape
+  // swept: C2 M=256 (N=2304) 48 rows, 216 tiles, 9.9 us against 11.0 with
+  // 64 and 11.1 with 32; M=160-224 32 rows (8.98-9.20 against 9.6-9.8 and
+  // 10.8-10.9); M=384-448 64 rows (11.3-11.6 against 11.7-12.0 and
+  // 12.6-12.9); N=4608 M=256 48 rows (13.6 against 15.2 and 15.7); N=3072
+  // M=256 64 rows (11.5 against 11.9 and 12.2).  The 48-row tile is built
+  // for up to 4 channels.
+  int64_t best_rows = -1;
+  for (int mb = 4; mb >= 2; --mb) {
+    if (mb == 3 && rcap > 4) continue;
+    const int64_t rows = (tiles(16 * mb, 64) + 255) / 256 * (16 * mb);
+    if (best_rows < 0 || rows < best_rows) {
+      best_rows = rows;
+      c.mb = mb;
+    }
+  }
+  if (c.mb == 3) c.ks = 4;  // measured 1-2 % faster than 3 steps at this height
   return c;
 }
 

@@ -1,7 +1,8 @@
 """Automatic kernel choice (no override) at the boundaries of its rules:
 stream vs MFMA at M = 128 / 129, the LDS kernel's K >= 2048 gate and its
 full-round rule below it (256 tiles of 256 x 64 vs 2.25 rounds), ragged N
-and K, and K that the LDS kernel cannot take (K % 256 != 0).  Every output
+and K, K that the LDS kernel cannot take (K % 256 != 0), and the MFMA
+kernel's tile height (32, 48 or 64 rows, fewest rows per CU).  Every output
 must equal the exact product."""
 import pytest
 import torch
@@ -23,6 +24,11 @@ SHAPES = [
     (1024, 1024, 4090),  # LDS with ragged N (columns clamped)
     (1000, 1088, 4096),  # K % 256 != 0: MFMA
     (300, 100, 37),      # ragged everything: K padded to 128
+    (224, 768, 2304),    # MFMA 32 x 64 tiles: 252 fit one round
+    (256, 768, 2304),    # MFMA 48 x 64 tiles: 216 in one round (the headline shape)
+    (250, 768, 2290),    # 48 x 64 tiles with ragged M and N
+    (384, 768, 2304),    # MFMA 64 x 64 tiles: 216 (48 rows would need 288)
+    (256, 768, 4608),    # no height fits one round: 48 rows (2 rounds) ties 32 (3)
 ]
 
 

@@ -19,7 +19,7 @@ SETS = {3: (254, 253, 251), 4: DENSE4, 6: (255, 253, 251, 247, 241, 239),
 RCAP = {3: 3, 4: 4, 6: 6, 10: 10}
 STREAM_TILES = [(1, 1), (2, 1), (4, 1), (1, 2)]
 # MFMA tiles (mb, nb) -> ring depths built for them
-_MFMA4 = {(2, 1): (3, 4), (4, 1): (3, 4), (2, 2): (3, 4), (4, 2): (3, 4), (8, 2): (3, 4)}
+_MFMA4 = {(2, 1): (3, 4), (3, 1): (3, 4), (4, 1): (3, 4), (2, 2): (3, 4), (4, 2): (3, 4), (8, 2): (3, 4)}
 MFMA_TILES = {3: _MFMA4, 4: _MFMA4, 6: {(2, 1): (3, 4), (4, 1): (3, 4), (4, 2): (3,)},
               10: {(2, 1): (3,), (4, 1): (3,), (2, 2): (2,)}}
 
