@@ -337,9 +337,11 @@ static int stream_ks_cap(int rcap, int mb, int nb) {
 }
 
 // Kernel family and tile for an M x N x kp problem, from sweeps on MI355X
-// (K = 768 and 4096, N = 2304 and 12288).  Up to 128 rows the stream kernel
-// (K split over 4 waves) keeps the most weight loads in flight.  Beyond
-// that the LDS-staged kernel (256 x 64 tiles) wherever it applies, K is at
+// (K = 768 to 4096, N = 768 to 12288).  For few rows (up to 16; up to 64
+// unless K is long and N wide; up to 128 while its 32-row tiles number at
+// most 512) the stream kernel (K split over 4 waves) keeps the most weight
+// loads in flight.  Beyond 128 rows the LDS-staged kernel (256 x 64 tiles)
+// wherever it applies, K is at
 // least 2048 (at K = 768 the MFMA kernel's 64 x 64 tiles measured faster)
 // and its tiles alone give every CU a workgroup; otherwise the MFMA kernel:
 // 128 x 128 tiles once they give >= 1024 workgroups (their weight reuse then
@@ -352,7 +354,18 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
     return static_cast<int64_t>((g.m + bm - 1) / bm) * ((g.n + bn - 1) / bn);
   };
   GemmChoice c{};
-  if (g.m <= 128) {
+  // Stream kernel up to 16 rows; up to 64 unless K > 1024 and its 16 x 16
+  // tiles number over 1024 (K=4096, N=12288: M=64 45 us with the MFMA
+  // kernel against 79, M=32 39 against 54; at K=768, N=2304, M=64 the
+  // stream kernel's 6.9 against 8.7); up to 128 while its 32 x 16 tiles
+  // number at most 512 (M=128: N=2304 8.8 us with the MFMA kernel against
+  // 9.6, N=4608 10.3 against 14.0, K=4096 N=12288 62 against 110; at
+  // N=768, 192 tiles, 5.1 against 7.4; at M=96, N=2304, 432 tiles, 7.6
+  // against 8.7).
+  const bool long_k = nk > 16;
+  const bool stream = g.m <= 16 || (g.m <= 64 && !(long_k && tiles(16, 16) > 1024)) ||
+                      (g.m > 64 && g.m <= 128 && tiles(32, 16) <= 512);
+  if (stream) {
     c.kind = kStream;
     c.mb = g.m <= 64 ? 1 : 2;
     c.nb = 1;
@@ -368,38 +381,45 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   const int64_t lds_tiles = tiles(kLdsBM, kLdsBN);
   const int64_t rounds = (lds_tiles + 255) / 256;
   const bool full_rounds = 8 * lds_tiles >= 7 * 256 * rounds;
-  if (lds_kernel_fits(g, araw, rcap) && lds_tiles >= 256 && (g.kp >= 2048 || full_rounds)) {
+  if (g.m > 128 && lds_kernel_fits(g, araw, rcap) && lds_tiles >= 256 && (g.kp >= 2048 || full_rounds)) {
     c.kind = kLds;
     return c;
   }
   c.kind = kMfma;
   c.ks = 0;  // the tile's default ring depth
   c.nb = 1;
-  if (rcap <= 4 && tiles(128, 128) >= 1024) {
+  if (g.m > 128 && rcap <= 4 && tiles(128, 128) >= 1024) {
     c.mb = 8;
     c.nb = 2;
     return c;
   }
-  // 32, 48 or 64 x 64 tiles: the height that gives the fewest rows per CU,
-  // counted as rounds of 256 workgroups times the tile height; on a tie
-  // the taller tile (fewer workgroups).  Measured on MI355X at K = 768 (and
-  // K = 4096, N = 12288), this picks the fastest height at every shape
-  // swept: C2 M=256 (N=2304) 48 rows, 216 tiles, 9.9 us against 11.0 with
-  // 64 and 11.1 with 32; M=160-224 32 rows (8.98-9.20 against 9.6-9.8 and
-  // 10.8-10.9); M=384-448 64 rows (11.3-11.6 against 11.7-12.0 and
-  // 12.6-12.9); N=4608 M=256 48 rows (13.6 against 15.2 and 15.7); N=3072
-  // M=256 64 rows (11.5 against 11.9 and 12.2).  The 48-row tile is built
-  // for up to 4 channels.
+  // 32, 48 or 64 x 64 tiles: among the heights that give at most 512
+  // workgroups, the one with the fewest rows per CU, counted as rounds of
+  // 256 workgroups times the tile height, the taller on a tie; 64 rows when
+  // none does (more tiles then re-read every weight column more often).
+  // Swept on MI355X at K = 768 (N = 768-4608, M = 96-448), K = 2048 and
+  // K = 4096 (N = 12288, M = 16-256), this picks the fastest height at
+  // every shape: C2 M=256 (N=2304) 48 rows, 216 tiles, 9.9 us against 11.0
+  // with 64 and 11.1 with 32; M=160-224 32 rows (8.98-9.20 against 9.6-9.8
+  // and 10.8-10.9); M=384-448 64 rows (11.3-11.6 against 11.7-12.0 and
+  // 12.6-12.9); N=4608 M=256 48 rows (13.6 against 15.2 and 15.7); C5
+  // M=128 64 rows (62 us against 68 with 32 rows, 768 tiles); C5 M=32 32
+  // rows (38 against 42).  The 48-row tile is built for up to 4 channels.
+  c.mb = 4;
   int64_t best_rows = -1;
   for (int mb = 4; mb >= 2; --mb) {
     if (mb == 3 && rcap > 4) continue;
-    const int64_t rows = (tiles(16 * mb, 64) + 255) / 256 * (16 * mb);
+    const int64_t t = tiles(16 * mb, 64);
+    if (t > 512) continue;
+    const int64_t rows = (t + 255) / 256 * (16 * mb);
     if (best_rows < 0 || rows < best_rows) {
       best_rows = rows;
       c.mb = mb;
     }
   }
-  if (c.mb == 3) c.ks = 4;  // measured 1-2 % faster than 3 steps at this height
+  // a ring of 4 K steps measured 1-3 % faster than 3 for 32- and 48-row
+  // tiles (and slower for 64-row ones)
+  if (c.mb < 4) c.ks = 4;
   return c;
 }
 

@@ -1,5 +1,6 @@
 """Automatic kernel choice (no override) at the boundaries of its rules:
-stream vs MFMA at M = 128 / 129, the LDS kernel's K >= 2048 gate and its
+stream vs MFMA (M <= 16; M <= 64 unless K > 1024 with over 1024 stream
+tiles; M <= 128 with at most 512 stream tiles), the LDS kernel's K >= 2048 gate and its
 full-round rule below it (256 tiles of 256 x 64 vs 2.25 rounds), ragged N
 and K, K that the LDS kernel cannot take (K % 256 != 0), and the MFMA
 kernel's tile height (32, 48 or 64 rows, fewest rows per CU).  Every output
@@ -13,7 +14,16 @@ DEV = "cuda"
 DENSE4 = (255, 253, 251, 247)
 
 SHAPES = [
-    (128, 768, 2304),    # stream (M <= 128)
+    (128, 768, 2304),    # MFMA: 576 stream tiles of 32 x 16 would be too many
+    (96, 768, 2304),     # stream: 432 tiles
+    (128, 768, 768),     # stream: 192 tiles
+    (64, 768, 4608),     # stream (M <= 64, K <= 1024)
+    (16, 2048, 12288),   # stream (M <= 16)
+    (32, 2048, 8192),    # stream: K > 1024 but 1024 stream tiles of 16 x 16
+    (24, 2048, 12288),   # MFMA 32-row tiles (K > 1024, 1536 stream tiles)
+    (40, 2048, 12288),   # MFMA 48-row tiles
+    (64, 2048, 12288),   # MFMA 64-row tiles
+    (128, 4096, 4096),   # MFMA past K = 1024: 64-row tiles
     (129, 768, 2304),    # MFMA (M > 128)
     (64, 4096, 1000),    # stream, ragged N
     (512, 4096, 12288),  # LDS, K >= 2048
