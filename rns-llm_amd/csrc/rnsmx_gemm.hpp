@@ -790,7 +790,8 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
 }
 
 // ---------------------------------------------------------------------------
-// MFMA GEMM (M > 128 where the LDS kernel does not apply: C2 M=256, C4).  A
+// MFMA GEMM (M > 128 where the LDS kernel does not apply: C2 M=256, C4;
+// also smaller batches of wide or long-K shapes, e.g. C5 M=32-128).  A
 // workgroup of 4 waves owns a (16*MB) x (4*16*NB) tile: the A rows (shared by
 // all waves, and in raw mode by all channels) pass through a P-deep register
 // ring into double-buffered LDS, 64-byte rows whose four 16-byte chunks are
