@@ -217,6 +217,20 @@ int32_t rnsmx_matmul_residues_prepared(
 int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb,
                                 int32_t ks);
 
+/*
+ * The GEMM kernel the fused entry points would launch for an M x N x K
+ * product with `channels` moduli: kind (1 stream, 2 MFMA, 3 LDS-staged),
+ * tile blocks mb, nb and ks, in the meaning of rnsmx_set_gemm_override
+ * (whose setting, when one is active, is what it reports).  raw_a != 0:
+ * int8 activations read in place, as the fused entry points do for int8
+ * sources with K a multiple of 16 whose accumulators fit int32; 0: residue
+ * planes.  Host code only (no GPU call, no stream).  No counterpart in the
+ * reference (cuBLAS picks its own kernels there); for tests and tuning.
+ */
+int32_t rnsmx_gemm_plan(int64_t m, int64_t n, int64_t k, int32_t channels,
+                        int32_t raw_a, int32_t *kind, int32_t *mb,
+                        int32_t *nb, int32_t *ks);
+
 /* 32-bit scratch words rnsmx_quantize_symmetric needs (per-block maxima). */
 #define RNSMX_QUANT_SCRATCH 1025
 

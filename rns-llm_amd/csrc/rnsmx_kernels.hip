@@ -904,6 +904,33 @@ int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb, int32_t ks
   return RNSMX_OK;
 }
 
+int32_t rnsmx_gemm_plan(int64_t m, int64_t n, int64_t k, int32_t channels, int32_t raw_a,
+                        int32_t *kind, int32_t *mb, int32_t *nb, int32_t *ks) {
+  clear_error();
+  if (kind == nullptr || mb == nullptr || nb == nullptr || ks == nullptr)
+    return fail(RNSMX_EINVAL, "gemm plan needs four output pointers");
+  if (m < 1 || n < 1 || k < 1 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX - 63)
+    return fail(RNSMX_EINVAL, "gemm plan needs 1 <= M, N, K < 2^31");
+  if (channels < 2 || channels > RNSMX_MAX_CHANNELS)
+    return fail(RNSMX_EINVAL, "gemm plan needs 2..10 channels");
+  // the fields choose_gemm reads, as the fused entry points fill them:
+  // raw int8 activations are read in place (row stride K), residue planes
+  // are padded to kp
+  GemmArgs g{};
+  g.m = static_cast<int32_t>(m);
+  g.n = static_cast<int32_t>(n);
+  g.kp = static_cast<int32_t>((k + 63) / 64 * 64);
+  g.a_k = raw_a ? static_cast<int32_t>(k) : g.kp;
+  g.a_ld = raw_a ? k : g.kp;
+  g.mods.channels = channels;
+  const GemmChoice c = g_override.kind != kAuto ? g_override : choose_gemm(g, raw_a != 0);
+  *kind = c.kind;
+  *mb = c.mb;
+  *nb = c.nb;
+  *ks = c.ks;
+  return RNSMX_OK;
+}
+
 int32_t rnsmx_quantize_symmetric(const void *x_dev, int32_t x_dtype, int64_t count,
                                  int32_t quant_bits, int32_t *scratch_dev, float *scale_dev,
                                  void *q_dev, void *stream) {

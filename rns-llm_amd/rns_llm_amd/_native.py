@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "rnsmx_matmul_prepared_fused",
     "rnsmx_matmul_residues_prepared",
     "rnsmx_set_gemm_override",
+    "rnsmx_gemm_plan",
     "rnsmx_quantize_symmetric",
     "rnsmx_decode_garner",
 )
@@ -103,6 +104,9 @@ _SIGNATURES = {
         _I32, [_P, _I64, _I32, _I32, _I32, _P, ctypes.POINTER(Moduli), _P, _I32,
                ctypes.POINTER(Epilogue), _P, _P]),
     "rnsmx_set_gemm_override": (_I32, [_I32, _I32, _I32, _I32]),
+    "rnsmx_gemm_plan": (_I32, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _I32, _I32,
+                                ctypes.POINTER(_I32), ctypes.POINTER(_I32),
+                                ctypes.POINTER(_I32), ctypes.POINTER(_I32)]),
     "rnsmx_quantize_symmetric": (_I32, [_P, _I32, _I64, _I32, _P, _P, _P, _P]),
     "rnsmx_decode_garner": (_I32, [_P, _I64, ctypes.POINTER(Moduli), _P, _P]),
 }

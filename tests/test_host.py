@@ -42,6 +42,61 @@ def test_abi_struct_layout_matches_header():
     assert _native.lib().rnsmx_abi_version() == _native.ABI_VERSION
 
 
+def gemm_plan(m, n, k, channels=4, raw_a=1):
+    out = [ctypes.c_int32() for _ in range(4)]
+    _native.check(_native.lib().rnsmx_gemm_plan(m, n, k, channels, raw_a, *[ctypes.byref(v) for v in out]))
+    return tuple(v.value for v in out)
+
+
+# (M, N, K, channels) -> (kind, mb, nb, ks): kind 1 stream, 2 MFMA, 3 LDS-staged
+PLANS = [
+    ((1, 2304, 768, 4), (1, 1, 1, 3)),       # decode: stream, 3 waves split 12 K steps
+    ((64, 2304, 768, 4), (1, 1, 1, 3)),      # stream up to 64 rows at short K
+    ((96, 2304, 768, 4), (1, 2, 1, 3)),      # stream: 432 tiles of 32 x 16
+    ((128, 768, 768, 4), (1, 2, 1, 3)),      # stream: 192 tiles
+    ((128, 2304, 768, 4), (2, 2, 1, 4)),     # 576 stream tiles: MFMA, 32 rows (144 tiles)
+    ((224, 2304, 768, 4), (2, 2, 1, 4)),     # 252 tiles of 32 rows: one round
+    ((256, 2304, 768, 4), (2, 3, 1, 4)),     # headline: 216 tiles of 48 rows
+    ((320, 2304, 768, 4), (2, 3, 1, 4)),     # 252 tiles of 48 rows
+    ((384, 2304, 768, 4), (2, 4, 1, 0)),     # 64 rows (216 tiles) tie 32 rows (2 rounds)
+    ((256, 4608, 768, 4), (2, 3, 1, 4)),     # no height fits one round: 48 rows (2 rounds)
+    ((256, 2304, 768, 6), (2, 4, 1, 0)),     # no 48-row tile past 4 channels
+    ((4096, 2304, 768, 4), (2, 4, 1, 0)),    # C4 QKV: over 512 tiles at every height
+    ((16, 12288, 4096, 4), (1, 1, 1, 4)),    # long K, 16 rows: stream
+    ((32, 12288, 4096, 4), (2, 2, 1, 4)),    # long K, wide N: MFMA, 32 rows
+    ((48, 12288, 4096, 4), (2, 3, 1, 4)),
+    ((64, 12288, 4096, 4), (2, 4, 1, 0)),
+    ((128, 12288, 4096, 4), (2, 4, 1, 0)),   # 32 rows would need 768 tiles
+    ((512, 12288, 4096, 4), (3, 0, 0, 0)),   # LDS-staged, 256 x 64 tiles
+    ((2048, 12288, 4096, 4), (3, 0, 0, 0)),
+    ((2048, 12288, 4096, 6), (2, 4, 1, 0)),  # the LDS kernel holds at most 4 channels
+]
+
+
+@pytest.mark.parametrize("shape,plan", PLANS)
+def test_gemm_plan_rules(shape, plan):
+    """The kernel choice at the boundaries of its rules (host logic of the
+    library; the GPU tests check that every choice computes the exact
+    product)."""
+    m, n, k, channels = shape
+    assert gemm_plan(m, n, k, channels) == plan
+
+
+def test_gemm_plan_reports_override_and_rejects_bad_shapes():
+    lib = _native.lib()
+    _native.check(lib.rnsmx_set_gemm_override(2, 2, 2, 3))
+    try:
+        assert gemm_plan(256, 2304, 768) == (2, 2, 2, 3)
+    finally:
+        _native.check(lib.rnsmx_set_gemm_override(0, 0, 0, 0))
+    assert gemm_plan(256, 2304, 768) == (2, 3, 1, 4)
+    # residue-plane activations (K not a multiple of 16): never the LDS kernel
+    assert gemm_plan(2048, 12288, 4104, raw_a=0)[0] == 2
+    for bad in ((0, 8, 8, 4), (8, 8, 8, 1), (8, 8, 8, 11)):
+        with pytest.raises(ValueError):
+            gemm_plan(*bad)
+
+
 @pytest.mark.parametrize("mods", [DENSE4, (251, 241, 239, 233), (3, 5, 7, 11, 13, 17, 19, 23, 29, 31),
                                   (127, 125, 121, 113), (2, 3), (254, 253, 251)])
 def test_native_moduli_constants(mods):
