@@ -65,7 +65,8 @@ struct GemmArgs {
   rnsmx_moduli_t mods;
 };
 
-enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kLds = 3 };
+// kStreamWide: the stream kernel with chunks of up to 8 K steps (long K).
+enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kLds = 3, kStreamWide = 4 };
 
 // ks: waves splitting K (stream kernel) or ring depth, 0 = automatic (MFMA kernel).
 struct GemmChoice {
@@ -81,7 +82,7 @@ struct GemmChoice {
 // launch_gemm_rR_pP returns false when the part has no kernel for the choice.
 constexpr int kGemmParts = 5;
 inline int gemm_part_of(const GemmChoice &c, bool araw) {
-  if (c.kind == kStream) return 0;
+  if (c.kind == kStream || c.kind == kStreamWide) return 0;
   if (c.kind == kLds) return 4;
   if (!araw) return 3;
   return c.nb == 1 ? 1 : 2;
@@ -600,20 +601,22 @@ __device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int &mt, int &
 // KS = 1 the epilogue runs straight from the MFMA registers.
 // ---------------------------------------------------------------------------
 // K steps per chunk: as many as fit next to the accumulators in 240
-// registers (two waves per SIMD), at most 4.
-constexpr int stream_u_of(int rcap, bool araw, int mb, int nb) {
+// registers (two waves per SIMD), at most ucap (4; 8 for the wide form,
+// which long-K decode takes: C5 M=1 39.5 us against 42.5 with 4, while at
+// K = 768 the larger chunks cost 7-15 %).
+constexpr int stream_u_of(int rcap, bool araw, int mb, int nb, int ucap = 4) {
   const int frags = (araw ? 1 : rcap) * mb + rcap * nb;  // 16-byte loads per K step
   const int u = (240 - 4 * rcap * mb * nb) / (4 * frags);
-  return u < 1 ? 1 : (u > 4 ? 4 : u);
+  return u < 1 ? 1 : (u > ucap ? ucap : u);
 }
 
-template <int RCAP, int MB, int NB, bool ARAW>
+template <int RCAP, int MB, int NB, bool ARAW, int UCAP>
 __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
   KGemmArgs &g = kernel_args<GemmArgs>();
   prefetch_kernel_args<kGemmHotArgBytes>();
   constexpr int BM = 16 * MB, BN = 16 * NB, TILE = BM * BN;
   constexpr int AP = ARAW ? 1 : RCAP;
-  constexpr int U = stream_u_of(RCAP, ARAW, MB, NB);
+  constexpr int U = stream_u_of(RCAP, ARAW, MB, NB, UCAP);
   extern __shared__ __attribute__((aligned(16))) int32_t sacc[];  // [RCAP][TILE] when KS > 1
   __shared__ int64_t red[4];
   __shared__ int bcast;
@@ -1211,22 +1214,23 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
 // Launchers for one channel capacity (instantiated per translation unit).
 // ---------------------------------------------------------------------------
 template <int RCAP, bool ARAW>
-bool launch_stream(GemmArgs g, int mb, int nb, int ks, hipStream_t st) {
-#define RNSMX_STREAM(MB_, NB_)                                                              \
-  if (mb == MB_ && nb == NB_) {                                                             \
+bool launch_stream(GemmArgs g, int mb, int nb, int ks, int ucap, hipStream_t st) {
+#define RNSMX_STREAM(MB_, NB_, UCAP_)                                                        \
+  if (mb == MB_ && nb == NB_ && ucap == UCAP_) {                                            \
     g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                                          \
     g.tiles_n = (g.n + 16 * NB_ - 1) / (16 * NB_);                                          \
     const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));                          \
     const size_t lds = ks > 1 ? static_cast<size_t>(RCAP) * 256 * MB_ * NB_ * 4 : 0;         \
     g.threads = 64 * ks;                                                                    \
-    hipLaunchKernelGGL((stream_kernel<RCAP, MB_, NB_, ARAW>), grid, dim3(64 * ks), lds, st, g); \
+    hipLaunchKernelGGL((stream_kernel<RCAP, MB_, NB_, ARAW, UCAP_>), grid, dim3(64 * ks), lds, st, g); \
     return true;                                                                            \
   }
-  RNSMX_STREAM(1, 1)
-  RNSMX_STREAM(2, 1)
+  RNSMX_STREAM(1, 1, 4)
+  RNSMX_STREAM(2, 1, 4)
   if constexpr (RCAP <= 4) {
-    RNSMX_STREAM(4, 1)
-    RNSMX_STREAM(1, 2)
+    RNSMX_STREAM(4, 1, 4)
+    RNSMX_STREAM(1, 2, 4)
+    RNSMX_STREAM(1, 1, 8)
   }
 #undef RNSMX_STREAM
   return false;
@@ -1307,8 +1311,9 @@ bool launch_gemm_part(const GemmArgs &g, bool araw, const GemmChoice &c, hipStre
   if constexpr (PART == 4) {
     return launch_lds<RCAP>(g, araw, st);
   } else if constexpr (PART == 0) {
-    return araw ? launch_stream<RCAP, true>(g, c.mb, c.nb, c.ks, st)
-                : launch_stream<RCAP, false>(g, c.mb, c.nb, c.ks, st);
+    const int ucap = c.kind == kStreamWide ? 8 : 4;
+    return araw ? launch_stream<RCAP, true>(g, c.mb, c.nb, c.ks, ucap, st)
+                : launch_stream<RCAP, false>(g, c.mb, c.nb, c.ks, ucap, st);
   } else if constexpr (PART == 1 || PART == 2) {
     return launch_mfma<RCAP, true, PART>(g, c.mb, c.nb, c.ks, st);
   } else {

@@ -339,8 +339,8 @@ static int stream_ks_cap(int rcap, int mb, int nb) {
 // Kernel family and tile for an M x N x kp problem, from sweeps on MI355X
 // (K = 768 to 4096, N = 768 to 12288).  For few rows (up to 16; up to 64
 // unless K is long and N wide; up to 128 while its 32-row tiles number at
-// most 512) the stream kernel (K split over 4 waves) keeps the most weight
-// loads in flight.  Beyond 128 rows the LDS-staged kernel (256 x 64 tiles)
+// most 512) the stream kernel (K split over 4 waves, chunks of 8 K steps
+// from K = 4096) keeps the most weight loads in flight.  Beyond 128 rows the LDS-staged kernel (256 x 64 tiles)
 // wherever it applies, K is at
 // least 2048 (at K = 768 the MFMA kernel's 64 x 64 tiles measured faster)
 // and its tiles alone give every CU a workgroup; otherwise the MFMA kernel:
@@ -366,10 +366,13 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   const bool stream = g.m <= 16 || (g.m <= 64 && !(long_k && tiles(16, 16) > 1024)) ||
                       (g.m > 64 && g.m <= 128 && tiles(32, 16) <= 512);
   if (stream) {
-    c.kind = kStream;
     c.mb = g.m <= 64 ? 1 : 2;
     c.nb = 1;
-    const int u = stream_u_of(rcap, araw, c.mb, c.nb);
+    // chunks of 8 K steps once K >= 4096 (16-row tiles, up to 4 channels):
+    // each wave then has half as many dependent round trips to memory
+    const bool wide = c.mb == 1 && rcap <= 4 && nk >= 64;
+    c.kind = wide ? kStreamWide : kStream;
+    const int u = stream_u_of(rcap, araw, c.mb, c.nb, wide ? 8 : 4);
     c.ks = std::min(stream_ks_cap(rcap, c.mb, c.nb), std::max(1, (nk + u - 1) / u));
     return c;
   }
@@ -427,7 +430,7 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
 static int32_t launch_gemm(const GemmArgs &g, bool araw, hipStream_t st) {
   const int rcap = rcap_for(g.mods.channels);
   GemmChoice c = g_override.kind != kAuto ? g_override : choose_gemm(g, araw);
-  if (c.kind == kStream) {
+  if (c.kind == kStream || c.kind == kStreamWide) {
     const int cap = stream_ks_cap(rcap, c.mb, c.nb);
     if (c.ks < 1 || c.ks > cap) {
       set_error("stream GEMM needs 1 <= ks <= %d for this tile", cap);
@@ -451,7 +454,9 @@ static int32_t launch_gemm(const GemmArgs &g, bool araw, hipStream_t st) {
               g.mods.channels);
     return RNSMX_EINVAL;
   }
-  return check_launch(c.kind == kStream ? "gemm_stream" : c.kind == kLds ? "gemm_lds" : "gemm_mfma");
+  return check_launch(c.kind == kStream || c.kind == kStreamWide ? "gemm_stream"
+                      : c.kind == kLds                           ? "gemm_lds"
+                                                                 : "gemm_mfma");
 }
 
 static int32_t launch_encode_rows(int32_t dtype, const EncodeArgs &e, hipStream_t st) {
@@ -897,8 +902,8 @@ int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb, int32_t ks
     g_override = GemmChoice{kAuto, 0, 0, 0};
     return RNSMX_OK;
   }
-  if (kind != kStream && kind != kMfma && kind != kLds)
-    return fail(RNSMX_EINVAL, "kind must be 0 (auto), 1 (stream), 2 (mfma) or 3 (lds)");
+  if (kind != kStream && kind != kMfma && kind != kLds && kind != kStreamWide)
+    return fail(RNSMX_EINVAL, "kind must be 0 (auto), 1 (stream), 2 (mfma), 3 (lds) or 4 (wide stream)");
   if (kind != kLds && (mb < 1 || nb < 1)) return fail(RNSMX_EINVAL, "tile blocks must be positive");
   g_override = GemmChoice{kind, mb, nb, ks};
   return RNSMX_OK;

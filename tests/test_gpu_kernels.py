@@ -102,6 +102,16 @@ def test_stream_kernel_instances(backend, override, r, mb, nb, ks):
     run_case(backend, mods, 7, 150, 37, dtype=torch.int16, seed=ks + 1)
 
 
+@pytest.mark.parametrize("r,ks", [(r, ks) for r in (3, 4) for ks in (1, 2, 4)])
+def test_wide_stream_kernel_instances(backend, override, r, ks):
+    # 8-step chunks: several chunks per wave, the last past K
+    override(4, 1, 1, ks)
+    mods = SETS[r]
+    run_case(backend, mods, 19, 64 * (8 * ks * 2 + 3) + 16, 16 * 3 + 5, seed=r * 10 + ks)
+    run_case(backend, mods, 5, 208, 21, seed=ks)
+    run_case(backend, mods, 7, 150, 37, dtype=torch.int16, seed=ks + 1)
+
+
 @pytest.mark.parametrize("r,mb,nb,p", mfma_cases())
 def test_mfma_kernel_instances(backend, override, r, mb, nb, p):
     override(2, mb, nb, p)

@@ -48,7 +48,8 @@ def gemm_plan(m, n, k, channels=4, raw_a=1):
     return tuple(v.value for v in out)
 
 
-# (M, N, K, channels) -> (kind, mb, nb, ks): kind 1 stream, 2 MFMA, 3 LDS-staged
+# (M, N, K, channels) -> (kind, mb, nb, ks): kind 1 stream, 2 MFMA, 3 LDS-staged,
+# 4 stream with 8-step chunks
 PLANS = [
     ((1, 2304, 768, 4), (1, 1, 1, 3)),       # decode: stream, 3 waves split 12 K steps
     ((64, 2304, 768, 4), (1, 1, 1, 3)),      # stream up to 64 rows at short K
@@ -62,7 +63,10 @@ PLANS = [
     ((256, 4608, 768, 4), (2, 3, 1, 4)),     # no height fits one round: 48 rows (2 rounds)
     ((256, 2304, 768, 6), (2, 4, 1, 0)),     # no 48-row tile past 4 channels
     ((4096, 2304, 768, 4), (2, 4, 1, 0)),    # C4 QKV: over 512 tiles at every height
-    ((16, 12288, 4096, 4), (1, 1, 1, 4)),    # long K, 16 rows: stream
+    ((1, 12288, 4096, 4), (4, 1, 1, 4)),     # C5 decode: stream with 8-step chunks
+    ((16, 12288, 4096, 4), (4, 1, 1, 4)),    # long K, 16 rows: stream, 8-step chunks
+    ((16, 2048, 2048, 4), (1, 1, 1, 4)),     # K = 2048: 4-step chunks
+    ((1, 12288, 4096, 6), (1, 1, 1, 4)),     # 8-step chunks only up to 4 channels
     ((32, 12288, 4096, 4), (2, 2, 1, 4)),    # long K, wide N: MFMA, 32 rows
     ((48, 12288, 4096, 4), (2, 3, 1, 4)),
     ((64, 12288, 4096, 4), (2, 4, 1, 0)),
