@@ -145,6 +145,12 @@ __device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
   return v;
 }
 
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
 __device__ __forceinline__ i32x4 load16(const int8_t *p) { return *reinterpret_cast<const i32x4 *>(p); }
 
 // Initial value of one MFMA accumulator: zero, hidden from the compiler.
@@ -172,7 +178,9 @@ __device__ __forceinline__ int64_t prefix_at(const Mods &mods, int idx) {
 
 // Number of moduli channels to use.  Without the adaptive prefix this is the
 // full set.  With it, every workgroup derives the same answer from the row
-// L1 norms written by the encoder and max|B| written at weight preparation:
+// L1 norms (written by the encoder, or, when row_l1 is null, summed here
+// from the raw int8 activations: the launcher does so for a few rows only,
+// since every workgroup reads them) and max|B| written at weight preparation:
 // bound = max_i sum_k |a_ik| * max|B| (adaptive.py:44-52); the answer is the
 // smallest c >= min_channels with 2 * bound < prod_{i<c} m_i
 // (adaptive.py:15-41), i.e. bound <= (P_c - 1) / 2.  When no prefix fits,
@@ -182,18 +190,43 @@ template <int RCAP>
 __device__ __forceinline__ int active_channels(KGemmArgs &g, int64_t *red, int *bcast, int nthreads) {
   const int full = g.mods.channels;
   if (g.min_channels <= 0) return full;
-  int64_t mx = 0;
-  for (int r = threadIdx.x; r < g.m; r += nthreads) {
-    const int64_t v = g.row_l1[r];
-    mx = v > mx ? v : mx;
-  }
-  mx = wave_max_i64(mx);
   const int nw = nthreads >> 6;
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-  __syncthreads();
+  int64_t best = 0;  // max_i sum_k |a_ik|, in thread 0
+  if (g.row_l1 != nullptr) {
+    int64_t mx = 0;
+    for (int r = threadIdx.x; r < g.m; r += nthreads) {
+      const int64_t v = g.row_l1[r];
+      mx = v > mx ? v : mx;
+    }
+    mx = wave_max_i64(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int w = 0; w < nw; ++w) best = red[w] > best ? red[w] : best;
+  } else {
+    // raw int8 rows of a_ld bytes, a_k of them read (a multiple of 16)
+    for (int r = 0; r < g.m; ++r) {
+      int64_t sum = 0;
+      for (int k0 = threadIdx.x * 16; k0 < g.a_k; k0 += nthreads * 16) {
+        const i32x4 w = *reinterpret_cast<const i32x4 *>(g.a + static_cast<int64_t>(r) * g.a_ld + k0);
+        static_for<16>([&](auto Q) {
+          constexpr int q = decltype(Q)::value;
+          const int32_t b = static_cast<int8_t>((static_cast<uint32_t>(w[q >> 2]) >> (8 * (q & 3))) & 0xFFu);
+          sum += b < 0 ? -b : b;
+        });
+      }
+      sum = wave_sum_i64(sum);
+      if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sum;
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        int64_t row = 0;
+        for (int w = 0; w < nw; ++w) row += red[w];
+        best = row > best ? row : best;
+      }
+      __syncthreads();
+    }
+  }
   if (threadIdx.x == 0) {
-    int64_t best = 0;
-    for (int w = 0; w < nw; ++w) best = red[w] > best ? red[w] : best;
     const int64_t wmax = *g.w_absmax;
     const int64_t bound = (wmax != 0 && best > LLONG_MAX / wmax) ? LLONG_MAX : best * wmax;
     int c = full, overflow = 1;

@@ -147,6 +147,8 @@ def test_lds_kernel_rejects_unfit_shapes(backend, override):
 def test_kernel_adaptive_prefix(backend, override, kind, mb, nb, ks, k):
     override(kind, mb, nb, ks)
     run_case(backend, DENSE4, 50, k, 90, seed=5, adaptive=True)
+    # up to 4 raw rows: the row norms are summed inside the GEMM
+    run_case(backend, DENSE4, 3, k, 90, seed=6, adaptive=True)
 
 
 @pytest.mark.parametrize("kind,mb,nb,ks", [(1, 1, 2, 2), (1, 4, 1, 4), (1, 2, 1, 1), (2, 8, 2, 0), (2, 2, 1, 0),

@@ -247,6 +247,24 @@ def test_adaptive_prefix_exact_and_falls_back(backend):
     assert adaptive.max_abs_weight == int(weight.abs().max())
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("k", [4096, 1040])
+def test_adaptive_small_batches(backend, m, k):
+    # up to 4 raw int8 rows the GEMM workgroups sum the row norms themselves
+    # (no encoder launch); 5 and more take the encoder's norms: both must
+    # give the oracle's prefix, bound and capacity and the exact product
+    gen = torch.Generator().manual_seed(m * 10 + k)
+    b = rand_i8(gen, (k, 48))
+    adaptive = backend.prepare_weight_adaptive(b.to(DEV), DENSE4, min_channels=3)
+    for lo in (4, 127):
+        a = rand_i8(gen, (m, k), -lo, lo)
+        a[m - 1, : k // 2] = lo  # the largest row last
+        out, meta = backend.matmul_prepared_adaptive_fused(a.to(DEV), adaptive, return_metadata=True)
+        np.testing.assert_array_equal(out.cpu().numpy(), exact(a, b))
+        c, bound, cap = ro.adaptive_select(a.numpy(), int(b.abs().max()), DENSE4, min_channels=3)
+        assert (meta["channels"], meta["bound"], meta["capacity"]) == (c, bound, cap)
+
+
 def test_adaptive_adversarial_full_set_k4096(backend):
     # C5 edge: all +-127 at K=4096 -> bound 66,064,384, prefix 3 cannot hold
     # it, so the device must pick the full 4-channel set
