@@ -488,7 +488,8 @@ def main():
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): the RNS GEMM path has "
-              "no collective; DESIGN.md describes how it would shard", file=sys.stderr)
+              "no collective; across GPUs it would split N column-parallel (each GPU its "
+              "share of the weight columns, the same kernel on its columns)", file=sys.stderr)
         sys.exit(2)
     if args.pmc_child:
         pmc_child(args)

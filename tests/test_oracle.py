@@ -193,7 +193,8 @@ def test_overflowing_product_wraps_identically():
 # moduli selection and adaptive prefix
 # --------------------------------------------------------------------------
 def test_dense_moduli_known_answer():
-    # SURVEY/results: int8 at K=768..4096 -> (255, 253, 251, 247); 3 channels up to K=501
+    # greedy dense prefix until the product reaches 2*K*127^2 + 1 (reference.py:238-265):
+    # 255*253*251 = 16,193,265 holds K <= 501 (2*501*127^2 + 1 = 16,161,259), K = 502 needs 4
     for k in (502, 768, 4096, 123_992):
         assert ro.choose_moduli_for_dot(k, 127, 127, strategy="dense_coprime") == DENSE4
     assert ro.choose_moduli_for_dot(501, 127, 127, strategy="dense_coprime") == DENSE4[:3]
