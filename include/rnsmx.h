@@ -210,7 +210,9 @@ int32_t rnsmx_matmul_residues_prepared(
  * K steps of loads in flight, 0 = automatic), kind 3 = LDS-staged kernel
  * (256 x 64 tiles; int8 activations, 4-channel capacity, K a multiple of
  * 256; mb, nb, ks ignored), kind 4 = the stream kernel loading chunks of
- * up to 8 K steps per wave instead of 4 (16 x 16 tiles, up to 4 channels).  A kernel that is not built, or does not fit the
+ * up to 8 K steps per wave instead of 4 (16 x 16 tiles, up to 4 channels),
+ * kind 5 = the MFMA kernel with three column waves (tile 16*mb x 48*nb;
+ * int8 activations read in place, up to 4 channels).  A kernel that is not built, or does not fit the
  * call, makes the next GEMM call fail with RNSMX_EINVAL.  Not
  * thread-safe; results never depend on it.  No counterpart in the reference
  * (cuBLAS picks its own kernels there).
@@ -221,7 +223,7 @@ int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb,
 /*
  * The GEMM kernel the fused entry points would launch for an M x N x K
  * product with `channels` moduli: kind (1 stream, 2 MFMA, 3 LDS-staged,
- * 4 stream with 8-step chunks),
+ * 4 stream with 8-step chunks, 5 MFMA with 48-column tiles),
  * tile blocks mb, nb and ks, in the meaning of rnsmx_set_gemm_override
  * (whose setting, when one is active, is what it reports).  raw_a != 0:
  * int8 activations read in place, as the fused entry points do for int8

@@ -66,7 +66,8 @@ struct GemmArgs {
 };
 
 // kStreamWide: the stream kernel with chunks of up to 8 K steps (long K).
-enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kLds = 3, kStreamWide = 4 };
+// kMfma3: the MFMA kernel with three column waves (48*nb-column tiles).
+enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kLds = 3, kStreamWide = 4, kMfma3 = 5 };
 
 // ks: waves splitting K (stream kernel) or ring depth, 0 = automatic (MFMA kernel).
 struct GemmChoice {
@@ -853,25 +854,28 @@ constexpr int mfma_ac_of(int rcap, int mb, bool araw) {
   return (chunks + 255) / 256;
 }
 
-template <int RCAP, int MB, int NB, int P, bool ARAW>
-__global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
+// NWV: waves (column groups of 16*NB) per workgroup, 4 or 3.
+template <int RCAP, int MB, int NB, int P, bool ARAW, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgs args) {
   KGemmArgs &g = kernel_args<GemmArgs>();
   prefetch_kernel_args<static_cast<int>(sizeof(GemmArgs))>();
   constexpr int BM = 16 * MB, BNW = 16 * NB;
   constexpr int AP = ARAW ? 1 : RCAP;
   constexpr int PLANE = BM * kLdsRow;
   constexpr int ACH = AP * BM * 4;  // 16-byte A chunks per K step
-  constexpr int AC = mfma_ac_of(RCAP, MB, ARAW);
+  constexpr int NT = 64 * NWV;
+  static_assert(NWV == 3 || NWV == 4, "3 or 4 column waves");
+  constexpr int AC = (ACH + NT - 1) / NT;
   // one spare 16-byte slot takes the stores of threads without an A chunk
   __shared__ __attribute__((aligned(16))) int8_t As[2][AP * PLANE + 16];
   __shared__ int64_t red[4];
   __shared__ int bcast;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c_act = active_channels<RCAP>(g, red, &bcast, 256);
+  const int c_act = active_channels<RCAP>(g, red, &bcast, NT);
   int mt, nt;
   tile_of(g.tiles_m, g.tiles_n, mt, nt);
-  const int m0 = mt * BM, n0 = nt * (4 * BNW) + wave * BNW;
+  const int m0 = mt * BM, n0 = nt * (NWV * BNW) + wave * BNW;
   const int nk = g.kp >> 6;
 
   // A staging: chunk q -> plane p, row, 16-byte part
@@ -880,7 +884,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(const GemmArgs args) {
   bool aon[AC];
   static_for<AC>([&](auto II) {
     constexpr int i = decltype(II)::value;
-    const int q = tid + 256 * i;
+    const int q = tid + NT * i;
     const bool inside = q < ACH;
     const int qq = inside ? q : 0;
     const int p = qq / (BM * 4), w = qq % (BM * 4), row = w >> 2, part = w & 3;
@@ -1276,17 +1280,24 @@ bool launch_stream(GemmArgs g, int mb, int nb, int ks, int ucap, hipStream_t st)
 // i.e. all of K = 768 in flight, 12.1 us against 11.0 us with 3).  NBSEL: the tile widths this
 // instantiation covers (0 all, 1 or 2 only NB = NBSEL).
 template <int RCAP, bool ARAW, int NBSEL>
-bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, hipStream_t st) {
+bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, int nwv, hipStream_t st) {
 #define RNSMX_MFMA_P(MB_, NB_, P_)                                                          \
-  if (p == P_) {                                                                            \
+  if (p == P_ && nwv == 4) {                                                                \
     hipLaunchKernelGGL((mfma_kernel<RCAP, MB_, NB_, P_, ARAW>), grid, dim3(256), 0, st, g); \
     return true;                                                                            \
+  }
+#define RNSMX_MFMA_P3(MB_, NB_, P_)                                                              \
+  if constexpr (ARAW) {                                                                          \
+    if (p == P_ && nwv == 3) {                                                                   \
+      hipLaunchKernelGGL((mfma_kernel<RCAP, MB_, NB_, P_, ARAW, 3>), grid, dim3(192), 0, st, g); \
+      return true;                                                                               \
+    }                                                                                            \
   }
 #define RNSMX_MFMA(MB_, NB_, PDEF, ...)                                    \
   if constexpr (NBSEL == 0 || NBSEL == NB_) {                              \
     if (mb == MB_ && nb == NB_) {                                          \
       g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                       \
-      g.tiles_n = (g.n + 64 * NB_ - 1) / (64 * NB_);                       \
+      g.tiles_n = (g.n + 16 * nwv * NB_ - 1) / (16 * nwv * NB_);           \
       const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));       \
       const int p = p_req > 0 ? p_req : PDEF;                              \
       __VA_ARGS__                                                          \
@@ -1294,9 +1305,9 @@ bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, hipStream_t st) {
     }                                                                      \
   }
   if constexpr (RCAP <= 4) {
-    RNSMX_MFMA(2, 1, 3, RNSMX_MFMA_P(2, 1, 3) RNSMX_MFMA_P(2, 1, 4))
-    RNSMX_MFMA(4, 1, 3, RNSMX_MFMA_P(4, 1, 3) RNSMX_MFMA_P(4, 1, 4))
-    RNSMX_MFMA(3, 1, 3, RNSMX_MFMA_P(3, 1, 3) RNSMX_MFMA_P(3, 1, 4))
+    RNSMX_MFMA(2, 1, 3, RNSMX_MFMA_P(2, 1, 3) RNSMX_MFMA_P(2, 1, 4) RNSMX_MFMA_P3(2, 1, 4))
+    RNSMX_MFMA(4, 1, 3, RNSMX_MFMA_P(4, 1, 3) RNSMX_MFMA_P(4, 1, 4) RNSMX_MFMA_P3(4, 1, 3) RNSMX_MFMA_P3(4, 1, 4))
+    RNSMX_MFMA(3, 1, 3, RNSMX_MFMA_P(3, 1, 3) RNSMX_MFMA_P(3, 1, 4) RNSMX_MFMA_P3(3, 1, 4))
     RNSMX_MFMA(2, 2, 3, RNSMX_MFMA_P(2, 2, 3) RNSMX_MFMA_P(2, 2, 4))
     RNSMX_MFMA(4, 2, 3, RNSMX_MFMA_P(4, 2, 3) RNSMX_MFMA_P(4, 2, 4))
     RNSMX_MFMA(8, 2, 3, RNSMX_MFMA_P(8, 2, 3) RNSMX_MFMA_P(8, 2, 4))
@@ -1311,6 +1322,7 @@ bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, hipStream_t st) {
   }
 #undef RNSMX_MFMA
 #undef RNSMX_MFMA_P
+#undef RNSMX_MFMA_P3
   return false;
 }
 
@@ -1347,10 +1359,12 @@ bool launch_gemm_part(const GemmArgs &g, bool araw, const GemmChoice &c, hipStre
     const int ucap = c.kind == kStreamWide ? 8 : 4;
     return araw ? launch_stream<RCAP, true>(g, c.mb, c.nb, c.ks, ucap, st)
                 : launch_stream<RCAP, false>(g, c.mb, c.nb, c.ks, ucap, st);
-  } else if constexpr (PART == 1 || PART == 2) {
-    return launch_mfma<RCAP, true, PART>(g, c.mb, c.nb, c.ks, st);
   } else {
-    return launch_mfma<RCAP, false, 0>(g, c.mb, c.nb, c.ks, st);
+    const int nwv = c.kind == kMfma3 ? 3 : 4;
+    if constexpr (PART == 1 || PART == 2)
+      return launch_mfma<RCAP, true, PART>(g, c.mb, c.nb, c.ks, nwv, st);
+    else
+      return launch_mfma<RCAP, false, 0>(g, c.mb, c.nb, c.ks, nwv, st);
   }
 }
 

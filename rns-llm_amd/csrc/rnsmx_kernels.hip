@@ -345,8 +345,8 @@ static int stream_ks_cap(int rcap, int mb, int nb) {
 // least 2048 (at K = 768 the MFMA kernel's 64 x 64 tiles measured faster)
 // and its tiles alone give every CU a workgroup; otherwise the MFMA kernel:
 // 128 x 128 tiles once they give >= 1024 workgroups (their weight reuse then
-// pays for one wave per SIMD), else 32, 48 or 64 x 64 tiles, the height
-// that leaves the fewest rows on any CU.
+// pays for one wave per SIMD), else 32, 48 or 64 x 64 (or x 48) tiles,
+// the one that leaves the fewest rows on any CU.
 static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   const int rcap = rcap_for(g.mods.channels);
   const int nk = g.kp / 64;
@@ -396,10 +396,10 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
     c.nb = 2;
     return c;
   }
-  // 32, 48 or 64 x 64 tiles: among the heights that give at most 512
-  // workgroups, the one with the fewest rows per CU, counted as rounds of
-  // 256 workgroups times the tile height, the taller on a tie; 64 rows when
-  // none does (more tiles then re-read every weight column more often).
+  // 32, 48 or 64 rows x 64 (or 48) columns: among the tiles that give at
+  // most 512 workgroups, the one with the fewest rows per CU, counted as
+  // rounds of 256 workgroups times the tile height; 64 x 64 when none does
+  // (more tiles then re-read every weight column more often).
   // Swept on MI355X at K = 768 (N = 768-4608, M = 96-448), K = 2048 and
   // K = 4096 (N = 12288, M = 16-256), this picks the fastest height at
   // every shape: C2 M=256 (N=2304) 48 rows, 216 tiles, 9.9 us against 11.0
@@ -408,21 +408,39 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   // 12.6-12.9); N=4608 M=256 48 rows (13.6 against 15.2 and 15.7); C5
   // M=128 64 rows (62 us against 68 with 32 rows, 768 tiles); C5 M=32 32
   // rows (38 against 42).  The 48-row tile is built for up to 4 channels.
+  // At K <= 1024 tiles of 48 columns (three waves) are candidates too
+  // (raw int8 activations, up to 4 channels): on a tie in rows per CU the
+  // choice that fits one round of 256 workgroups with the most of them wins
+  // (C2 M=128 32 x 48, 192 tiles, 8.3 us against 8.8 with 32 x 64; N=1536
+  // M=256 8.5 against 9.0; K=1024 N=3072 M=256 64 x 48, 12.9 against 13.5),
+  // then the taller, then the wider tile.  48 x 48 and 64 x 48 never beat
+  // 48 x 64 on the headline (10.9 against 9.9 us).
   c.mb = 4;
-  int64_t best_rows = -1;
-  for (int mb = 4; mb >= 2; --mb) {
-    if (mb == 3 && rcap > 4) continue;
-    const int64_t t = tiles(16 * mb, 64);
-    if (t > 512) continue;
-    const int64_t rows = (t + 255) / 256 * (16 * mb);
-    if (best_rows < 0 || rows < best_rows) {
-      best_rows = rows;
-      c.mb = mb;
+  int best_w = 4;
+  int64_t best_rows = -1, best_fill = 0;
+  for (int w = 4; w >= 3; --w) {
+    if (w == 3 && !(araw && rcap <= 4 && nk <= 16)) continue;
+    for (int mb = 4; mb >= 2; --mb) {
+      if (mb == 3 && rcap > 4) continue;
+      const int64_t t = tiles(16 * mb, 16 * w);
+      if (t > 512) continue;
+      const int64_t rows = (t + 255) / 256 * (16 * mb);
+      const int64_t fill = t <= 256 ? t : 0;  // workgroups of a single round
+      const bool better = best_rows < 0 || rows < best_rows ||
+                          (rows == best_rows && fill > best_fill) ||
+                          (rows == best_rows && fill == best_fill && mb > c.mb);
+      if (better) {
+        best_rows = rows;
+        best_fill = fill;
+        c.mb = mb;
+        best_w = w;
+      }
     }
   }
   // a ring of 4 K steps measured 1-3 % faster than 3 for 32- and 48-row
-  // tiles (and slower for 64-row ones)
-  if (c.mb < 4) c.ks = 4;
+  // tiles and for three-wave tiles (and slower for 64 x 64 ones)
+  if (best_w == 3) c.kind = kMfma3;
+  if (c.mb < 4 || best_w == 3) c.ks = 4;
   return c;
 }
 
@@ -906,8 +924,9 @@ int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb, int32_t ks
     g_override = GemmChoice{kAuto, 0, 0, 0};
     return RNSMX_OK;
   }
-  if (kind != kStream && kind != kMfma && kind != kLds && kind != kStreamWide)
-    return fail(RNSMX_EINVAL, "kind must be 0 (auto), 1 (stream), 2 (mfma), 3 (lds) or 4 (wide stream)");
+  if (kind != kStream && kind != kMfma && kind != kLds && kind != kStreamWide && kind != kMfma3)
+    return fail(RNSMX_EINVAL,
+                "kind must be 0 (auto), 1 (stream), 2 (mfma), 3 (lds), 4 (wide stream) or 5 (3-wave mfma)");
   if (kind != kLds && (mb < 1 || nb < 1)) return fail(RNSMX_EINVAL, "tile blocks must be positive");
   g_override = GemmChoice{kind, mb, nb, ks};
   return RNSMX_OK;

@@ -14,7 +14,10 @@ DEV = "cuda"
 DENSE4 = (255, 253, 251, 247)
 
 SHAPES = [
-    (128, 768, 2304),    # MFMA: 576 stream tiles of 32 x 16 would be too many
+    (128, 768, 2304),    # MFMA 32 x 48 tiles: 576 stream tiles of 32 x 16 would be too many
+    (256, 768, 1536),    # MFMA 32 x 48 tiles (256 of them)
+    (256, 768, 3072),    # MFMA 64 x 48 tiles
+    (250, 1024, 3070),   # MFMA 64 x 48 tiles, ragged M and N
     (96, 768, 2304),     # stream: 432 tiles
     (128, 768, 768),     # stream: 192 tiles
     (64, 768, 4608),     # stream (M <= 64, K <= 1024)

@@ -112,6 +112,18 @@ def test_wide_stream_kernel_instances(backend, override, r, ks):
     run_case(backend, mods, 7, 150, 37, dtype=torch.int16, seed=ks + 1)
 
 
+@pytest.mark.parametrize("r,mb,p", [(r, mb, p) for r in (3, 4) for mb, p in ((2, 4), (3, 4), (4, 3), (4, 4))])
+def test_three_wave_mfma_kernel_instances(backend, override, r, mb, p):
+    # 48-column tiles: ragged N around multiples of 48 and 16, several trips
+    # round the ring, the last partly past K
+    override(5, mb, 1, p)
+    mods = SETS[r]
+    run_case(backend, mods, 16 * mb * 2 + 9, 336, 48 * 2 + 11, seed=r * 100 + mb)
+    run_case(backend, mods, 16 * mb + 5, 64 * (2 * p + 1) + 16, 48 + 3, seed=p)
+    run_case(backend, mods, 16 * mb + 3, 768, 2304, seed=r)
+    run_case(backend, mods, 3, 320, 90, seed=7, adaptive=True)
+
+
 @pytest.mark.parametrize("r,mb,nb,p", mfma_cases())
 def test_mfma_kernel_instances(backend, override, r, mb, nb, p):
     override(2, mb, nb, p)

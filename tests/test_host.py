@@ -49,13 +49,17 @@ def gemm_plan(m, n, k, channels=4, raw_a=1):
 
 
 # (M, N, K, channels) -> (kind, mb, nb, ks): kind 1 stream, 2 MFMA, 3 LDS-staged,
-# 4 stream with 8-step chunks
+# 4 stream with 8-step chunks, 5 MFMA with 48-column tiles
 PLANS = [
     ((1, 2304, 768, 4), (1, 1, 1, 3)),       # decode: stream, 3 waves split 12 K steps
     ((64, 2304, 768, 4), (1, 1, 1, 3)),      # stream up to 64 rows at short K
     ((96, 2304, 768, 4), (1, 2, 1, 3)),      # stream: 432 tiles of 32 x 16
     ((128, 768, 768, 4), (1, 2, 1, 3)),      # stream: 192 tiles
-    ((128, 2304, 768, 4), (2, 2, 1, 4)),     # 576 stream tiles: MFMA, 32 rows (144 tiles)
+    ((128, 2304, 768, 4), (5, 2, 1, 4)),     # 576 stream tiles: MFMA, 32 x 48 (192 tiles)
+    ((256, 1536, 768, 4), (5, 2, 1, 4)),     # 32 x 48 fills 256 CUs (32 x 64: 192)
+    ((256, 3072, 768, 4), (5, 4, 1, 4)),     # 64 x 48, 256 tiles, ties 64 x 64 on rows
+    ((256, 3072, 1024, 4), (5, 4, 1, 4)),
+    ((128, 2304, 768, 6), (2, 2, 1, 4)),     # 48-column tiles only up to 4 channels
     ((224, 2304, 768, 4), (2, 2, 1, 4)),     # 252 tiles of 32 rows: one round
     ((256, 2304, 768, 4), (2, 3, 1, 4)),     # headline: 216 tiles of 48 rows
     ((320, 2304, 768, 4), (2, 3, 1, 4)),     # 252 tiles of 48 rows
