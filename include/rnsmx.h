@@ -11,6 +11,12 @@
  *   - Every call that launches work is asynchronous on `stream` and never
  *     synchronises, allocates, or frees memory.  Scratch memory is always
  *     caller-owned (`workspace`, sized by the *_workspace_bytes queries).
+ *   - A workspace starts with RNSMX_SPLIT_TICKETS 32-bit arrival counters of
+ *     the K split over workgroups (rnsmx_plan_t.splits).  For
+ *     rnsmx_matmul_prepared_fused they must be zero when the workspace is
+ *     first used (allocate it zero-filled); every call leaves them zero, for
+ *     any shape, so one workspace serves any sequence of calls.  Calls that
+ *     share a workspace must not overlap (keep one per stream).
  *   - Return value: RNSMX_OK (0) on success, otherwise an RNSMX_E* code and a
  *     thread-local message readable through rnsmx_last_error().
  *   - Integer results are exact: bit-identical to A.astype(int64) @ B for any
@@ -28,6 +34,9 @@ extern "C" {
 
 #define RNSMX_MAX_CHANNELS 10
 #define RNSMX_K_ALIGN 64 /* K padding of residue planes, bytes */
+/* Arrival counters at the start of every workspace (64 KiB): a K split runs
+ * only when its (tile, wave) count fits. */
+#define RNSMX_SPLIT_TICKETS 16384
 
 enum rnsmx_status {
   RNSMX_OK = 0,
@@ -67,6 +76,30 @@ typedef struct rnsmx_moduli {
   uint32_t qk8[RNSMX_MAX_CHANNELS];    /* 2^8 * qinv_i mod m_i                */
 } rnsmx_moduli_t;
 
+/*
+ * Kernel plan of one GEMM launch.  kind 0 = the library's automatic choice
+ * (the other fields are then ignored); 1 = stream kernel (tile 16*mb x
+ * 16*nb, ks waves splitting K inside a workgroup), 2 = MFMA kernel (tile
+ * 16*mb x 64*nb, ks = K steps of loads in flight, 0 = the tile's default),
+ * 3 = LDS-staged kernel (256 x 64 tiles; int8 activations, 4-channel
+ * capacity, K a multiple of 256; mb, nb, ks ignored), 4 = the stream kernel
+ * loading chunks of up to 8 K steps per wave (16 x 16 tiles, up to 4
+ * channels), 5 = the MFMA kernel with three column waves (tile 16*mb x
+ * 48*nb; int8 activations read in place, up to 4 channels).
+ * splits: workgroups splitting K per output tile (0 or 1 = none; up to 4
+ * channels, and for the stream kernel ks = 1): each reduces its partial
+ * sums to residues, and the last to finish a tile reconstructs it.  A plan
+ * that names a kernel that is not built, or does not fit the call, makes the
+ * call fail with RNSMX_EINVAL.  Results never depend on the plan.  No
+ * counterpart in the reference (cuBLAS picks its own kernels there); for
+ * tuning and for tests that run every kernel on the same inputs.
+ */
+typedef struct rnsmx_plan {
+  int32_t kind;
+  int32_t mb, nb, ks;
+  int32_t splits;
+} rnsmx_plan_t;
+
 /* Thread-local text of the last error (empty string when none). */
 const char *rnsmx_last_error(void);
 
@@ -104,7 +137,8 @@ int32_t rnsmx_encode_centered(const void *values_dev, int32_t dtype,
                               int64_t *row_l1_dev, int32_t *absmax_dev,
                               void *stream);
 
-/* Bytes of workspace rnsmx_matmul_centered_fused_out needs. */
+/* Bytes of workspace rnsmx_matmul_centered_fused_out needs (its counters
+ * are cleared by the call itself, so any buffer of this size serves). */
 int64_t rnsmx_fused_workspace_bytes(int64_t m, int64_t k, int64_t n,
                                     int32_t channels);
 
@@ -146,9 +180,12 @@ int32_t rnsmx_prepare_weight(const void *b_nk_dev, int32_t dtype, int32_t n,
                              int8_t *packed_dev, int32_t *absmax_dev,
                              void *stream);
 
-/* Bytes of workspace rnsmx_matmul_prepared_fused needs for M rows. */
-int64_t rnsmx_prepared_workspace_bytes(int64_t m, int64_t k,
-                                       int32_t channels);
+/* Bytes of workspace rnsmx_matmul_prepared_fused needs for an M x N x K
+ * product with `channels` moduli under `plan` (NULL: the automatic plan),
+ * whatever the activation dtype. */
+int64_t rnsmx_prepared_workspace_bytes(int64_t m, int64_t k, int64_t n,
+                                       int32_t channels,
+                                       const rnsmx_plan_t *plan);
 
 /* Epilogue selector of rnsmx_matmul_prepared_fused. */
 typedef struct rnsmx_epilogue {
@@ -173,7 +210,9 @@ typedef struct rnsmx_adaptive {
  * adaptive.min_channels > 0 the GEMM picks, on the device and without any
  * host synchronisation, the shortest moduli prefix c >= min_channels with
  * 2 * max_i(sum_k |a_ik|) * max|B| < prod(prefix); if none fits it uses the
- * full set and sets meta[3] = 1.
+ * full set and sets meta[3] = 1.  plan: NULL for the automatic kernel
+ * choice.  The workspace's counters must be zero at its first use (see
+ * the conventions above).
  * Replaces matmul_prepared_fused (cuda_backend.py:514-539) and
  * matmul_prepared_adaptive_fused (cuda_backend.py:577-622, whose selector
  * synchronises at :591).
@@ -183,14 +222,15 @@ int32_t rnsmx_matmul_prepared_fused(
     const int8_t *packed_dev, const rnsmx_moduli_t *mods,
     const int16_t *lut_dev, int32_t lut_channels,
     const rnsmx_adaptive_t *adaptive, const rnsmx_epilogue_t *epilogue,
-    void *workspace_dev, int64_t workspace_bytes, void *out_dev,
-    void *stream);
+    const rnsmx_plan_t *plan, void *workspace_dev, int64_t workspace_bytes,
+    void *out_dev, void *stream);
 
 /*
  * GEMM stage of rnsmx_matmul_prepared_fused on activations already encoded
  * by rnsmx_encode_centered into a_res_dev [R][M][a_ld] (a_ld a multiple of
  * RNSMX_K_ALIGN, zero bytes in [K, a_ld)), against a prepared weight.  Same
- * epilogue options, no adaptive prefix (all channels).  Lets a caller
+ * epilogue options, no adaptive prefix (all channels), no workspace (so no
+ * K split over workgroups).  Lets a caller
  * encode once and reuse the residues (e.g. one activation against several
  * weights) and times the GEMM kernel on its own.
  * Replaces the cuBLAS + fused_reduce_garner half of _C.matmul_centered_fused_out
@@ -203,37 +243,16 @@ int32_t rnsmx_matmul_residues_prepared(
     const rnsmx_epilogue_t *epilogue, void *out_dev, void *stream);
 
 /*
- * Process-wide override of the GEMM kernel choice, for tuning sweeps and
- * for tests that run every kernel family on the same inputs.  kind 0
- * restores the automatic choice; kind 1 = stream kernel (tile 16*mb x 16*nb,
- * ks waves splitting K), kind 2 = MFMA kernel (tile 16*mb x 64*nb, ks =
- * K steps of loads in flight, 0 = automatic), kind 3 = LDS-staged kernel
- * (256 x 64 tiles; int8 activations, 4-channel capacity, K a multiple of
- * 256; mb, nb, ks ignored), kind 4 = the stream kernel loading chunks of
- * up to 8 K steps per wave instead of 4 (16 x 16 tiles, up to 4 channels),
- * kind 5 = the MFMA kernel with three column waves (tile 16*mb x 48*nb;
- * int8 activations read in place, up to 4 channels).  A kernel that is not built, or does not fit the
- * call, makes the next GEMM call fail with RNSMX_EINVAL.  Not
- * thread-safe; results never depend on it.  No counterpart in the reference
- * (cuBLAS picks its own kernels there).
- */
-int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb,
-                                int32_t ks);
-
-/*
- * The GEMM kernel the fused entry points would launch for an M x N x K
- * product with `channels` moduli: kind (1 stream, 2 MFMA, 3 LDS-staged,
- * 4 stream with 8-step chunks, 5 MFMA with 48-column tiles),
- * tile blocks mb, nb and ks, in the meaning of rnsmx_set_gemm_override
- * (whose setting, when one is active, is what it reports).  raw_a != 0:
- * int8 activations read in place, as the fused entry points do for int8
- * sources with K a multiple of 16 whose accumulators fit int32; 0: residue
- * planes.  Host code only (no GPU call, no stream).  No counterpart in the
- * reference (cuBLAS picks its own kernels there); for tests and tuning.
+ * The plan rnsmx_matmul_prepared_fused chooses by itself for an M x N x K
+ * product with `channels` moduli (kind 1-5, tile, ks, splits as in
+ * rnsmx_plan_t).  raw_a != 0: int8 activations read in place, as the fused
+ * entry points do for int8 sources with K a multiple of 16 whose
+ * accumulators fit int32; 0: residue planes.  Host code only (no GPU call,
+ * no stream).  No counterpart in the reference (cuBLAS picks its own
+ * kernels there); for tests and tuning.
  */
 int32_t rnsmx_gemm_plan(int64_t m, int64_t n, int64_t k, int32_t channels,
-                        int32_t raw_a, int32_t *kind, int32_t *mb,
-                        int32_t *nb, int32_t *ks);
+                        int32_t raw_a, rnsmx_plan_t *out);
 
 /* 32-bit scratch words rnsmx_quantize_symmetric needs (per-block maxima). */
 #define RNSMX_QUANT_SCRATCH 1025

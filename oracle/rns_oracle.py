@@ -24,14 +24,18 @@ How each function is pinned (tests/test_oracle.py):
     12-bit case (``:40-46``).
   * adaptive prefix: ``tests/test_reference.py:69-81`` (bound 5e6 -> 3
     channels); the 3-channel capacity 8,096,632 recorded in
-    ``results/v0.5/adaptive_channels.json:20``; brute force over every prefix.
+    ``results/v0.5/adaptive_channels.json:20``; brute force over every prefix;
+    ``adaptive_select`` on hand-built activations whose largest row L1
+    differs from their largest column L1 (the reference sums each row,
+    ``cuda_backend.py:591``), with the bound, prefix and capacity worked out
+    by hand.
   * compact LUT: every entry equals b * 256**p mod m and byte decomposition
     reproduces ``%`` for sampled 32-bit values.
 """
 from __future__ import annotations
 
 from math import gcd, prod
-from typing import Iterable, Sequence
+from typing import Iterable
 
 import numpy as np
 
@@ -368,21 +372,3 @@ def adaptive_matmul(a, b, moduli, *, min_channels=3, lut_channels=2):
     prefix = tuple(moduli)[:c]
     out = rns_matmul_centered(a, b, prefix, lut_channels=min(lut_channels, c))
     return out, {"channels": c, "bound": bound, "capacity": cap}
-
-
-# ---------------------------------------------------------------------------
-# Fused QKV / continuous batching (integer level)
-# ---------------------------------------------------------------------------
-def fused_qkv_weight(wq, wk, wv) -> np.ndarray:
-    """B [K, Nq+Nk+Nv] from three [K, N*] blocks, q, k, v order
-    (``layers/rns_qkv.py:75-78``, expressed on B = W^T)."""
-    return np.concatenate([wq, wk, wv], axis=1)
-
-
-def split_rows(merged, rows: Sequence[int]):
-    """Per-request row views of a merged output (``cuda_backend.py:695-700``)."""
-    out, off = [], 0
-    for r in rows:
-        out.append(merged[off:off + r])
-        off += r
-    return out

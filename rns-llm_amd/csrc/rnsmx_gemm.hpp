@@ -50,6 +50,12 @@ struct GemmArgs {
   int32_t tiles_m, tiles_n;  // output tile grid (set at launch)
   int32_t threads;           // workgroup size (set at launch; read here rather than
                              // from the hidden arguments, a cache line of its own)
+  // K split over workgroups (split_exchange): every output tile is computed
+  // by `splits` workgroups, split s taking K steps [s * kchunk, (s + 1) *
+  // kchunk) (the last one the rest); splits = 1, kchunk = kp / 64 otherwise
+  int32_t splits, kchunk;
+  uint32_t *tickets;  // one arrival counter per (tile, wave), zero between calls
+  int8_t *xchg;       // partial residues, [tile * waves + wave][split][MI * NJ][4 words][64 lanes] x 4 bytes
   // adaptive prefix
   int32_t min_channels;  // 0: all channels
   const int64_t *row_l1;
@@ -69,9 +75,18 @@ struct GemmArgs {
 // kMfma3: the MFMA kernel with three column waves (48*nb-column tiles).
 enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kLds = 3, kStreamWide = 4, kMfma3 = 5 };
 
-// ks: waves splitting K (stream kernel) or ring depth, 0 = automatic (MFMA kernel).
+// ks: waves splitting K (stream kernel) or ring depth, 0 = automatic (MFMA
+// kernel); splits: workgroups splitting K (1 = none).
 struct GemmChoice {
-  int kind, mb, nb, ks;
+  int kind, mb, nb, ks, splits;
+};
+
+// Geometry of one launch: output tiles, waves per workgroup, and the 16-byte
+// accumulator chunks per lane of one wave's block (the exchange unit of a
+// K split).
+struct GemmGrid {
+  int64_t tiles;
+  int waves, chunks;
 };
 
 // The kernels are instantiated in parts, one translation unit each
@@ -608,19 +623,176 @@ __device__ __forceinline__ i32x4 select16(bool keep, i32x4 v) {
   return keep ? v : zero;
 }
 
-// Workgroup -> output tile.  Workgroups are handed to the 8 XCDs round-robin
-// (workgroup b runs on XCD b % 8), and each XCD has its own L2.  Tiles are
-// numbered M-block fastest, so giving every XCD one contiguous run of tile
-// numbers keeps the workgroups that read the same weight columns on the
-// same L2.  The map is a bijection on [0, tiles) for any tile count.
-__device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int &mt, int &nt) {
-  const int total = tiles_m * tiles_n;
+// Workgroup -> (output tile, K split).  Workgroups are handed to the 8 XCDs
+// round-robin (workgroup b runs on XCD b % 8), and each XCD has its own L2.
+// Work units are numbered split-major, then M-block fastest, so giving
+// every XCD one contiguous run of unit numbers keeps the workgroups that
+// read the same weight columns (and K range) on the same L2.  The map is a
+// bijection on [0, tiles * splits) for any count.
+__device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int splits, int &mt, int &nt, int &split) {
+  const int tiles = tiles_m * tiles_n;
+  const int total = tiles * splits;
   const int b = blockIdx.x;
   const int xcd = b & 7, local = b >> 3;
   const int base = total >> 3, rem = total & 7;
   const int t = xcd * base + min(xcd, rem) + local;
-  mt = t % tiles_m;
-  nt = t / tiles_m;
+  split = t / tiles;
+  const int u = t - split * tiles;
+  mt = u % tiles_m;
+  nt = u / tiles_m;
+}
+
+// The K range of one split, in 64-byte steps from ks0: nk steps (at least
+// one: the launcher sizes kchunk so every split has work), and the A bytes
+// per row that lie inside the true K from ks0 on (a_k in GemmArgs, less the
+// bytes before the split).
+struct KRange {
+  int ks0, nk, a_k;
+};
+
+__device__ __forceinline__ KRange k_range(KGemmArgs &g, int split) {
+  KRange r;
+  r.ks0 = split * g.kchunk;
+  r.nk = min(g.kchunk, (g.kp >> 6) - r.ks0);
+  r.a_k = g.a_k - r.ks0 * 64;
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// Residue exchange of a K split.  The S workgroups of one output tile hold
+// int32 partial sums over disjoint K ranges; the channel-c accumulator of
+// the whole K is their sum, so its residue mod m_c is the sum of the
+// partials' residues mod m_c (the K split is exact in RNS, whatever the
+// split).  Each wave reduces its partial sums to canonical residues (one
+// byte per channel, so up to four channels pack into one 32-bit word per
+// element), writes them to its slot of the exchange area, and takes a
+// ticket on its (tile, wave) counter.  The wave that draws the last ticket
+// adds the other splits' residues to its own partial sums (each an int32
+// congruent to the whole accumulator afterwards, which is all the Garner
+// epilogue needs), returns the counter to zero for the next call, and
+// finishes the tile; the others are done.  No wave waits for another, so
+// the protocol needs neither co-residency nor a spin loop.
+//
+// Visibility across XCDs (each has its own L2): the residues are written
+// and read with agent-scope atomic accesses (writes through to, and reads
+// from, the device-coherent level, not a possibly stale L2 copy), and the
+// writer's stores complete (vmcnt 0) before its ticket increment issues;
+// the reader's loads issue only after its ticket returned.  This gives the
+// release/acquire order of the handoff without an L2 writeback or
+// invalidate, which would also flush or drop the weight columns other
+// workgroups on the same XCD are still reading.
+// ---------------------------------------------------------------------------
+// One 16-byte exchange word group of a lane, stored word-major: word q of
+// lane l sits at byte 256 q + 4 l of its 1 KB chunk, so each of the four
+// 32-bit agent-scope stores (or loads) of a wave covers 256 contiguous
+// bytes (whole cache lines: written through, a partly covered line would
+// be merged at the memory side).
+__device__ __forceinline__ void store_coherent(int8_t *p, i32x4 v) {
+  static_for<4>([&](auto Q) {
+    constexpr int q = decltype(Q)::value;
+    __hip_atomic_store(reinterpret_cast<uint32_t *>(p + 256 * q), static_cast<uint32_t>(v[q]), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  });
+}
+
+__device__ __forceinline__ i32x4 load_coherent(const int8_t *p) {
+  i32x4 v;
+  static_for<4>([&](auto Q) {
+    constexpr int q = decltype(Q)::value;
+    v[q] = static_cast<int32_t>(__hip_atomic_load(reinterpret_cast<uint32_t *>(const_cast<int8_t *>(p + 256 * q)),
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  });
+  return v;
+}
+
+// s_waitcnt vmcnt(0) alone (expcnt and lgkmcnt left at their maxima), with
+// compiler barriers so no memory access moves across it.
+__device__ __forceinline__ void wait_vm_all() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));
+  asm volatile("" ::: "memory");
+}
+
+// The tiles built with the exchange (the host splits K only for these):
+// up to 4 channels, and few enough accumulators that the exchange code does
+// not raise the kernel's register count (and so lower its occupancy, split
+// or not): stream tiles of one or two 16 x 16 blocks down a column, MFMA
+// tiles of one column block per wave; the LDS kernel always.
+constexpr bool stream_splits(int rcap, int mb, int nb) { return rcap <= 4 && nb == 1 && mb <= 2; }
+constexpr bool mfma_splits(int rcap, int mb, int nb) { return rcap <= 4 && nb == 1; }
+
+// One wave's part of the exchange, for a (16 MI) x (16 NJ) block of
+// accumulators per channel (RCAP <= 4).  slot = tile * waves + wave.
+// Returns true in the wave that finishes the tile, whose acc then holds
+// sums congruent to the whole-K accumulators.
+template <int RCAP, int MI, int NJ>
+__device__ __forceinline__ bool split_exchange(KGemmArgs &g, const Epi<RCAP> &e, i32x4 (&acc)[RCAP][MI][NJ],
+                                               int64_t slot, int split) {
+  static_assert(RCAP <= 4, "one byte per channel in a 32-bit word");
+  constexpr int CH = MI * NJ;  // 1 KB chunks per wave and split
+  const int lane = threadIdx.x & 63;
+  const int S = g.splits;
+  int8_t *base = g.xchg + slot * S * CH * 1024 + lane * 4;
+  // canonical residues of this split's partial sums
+  static_for<MI>([&](auto I) {
+    constexpr int i = decltype(I)::value;
+    static_for<NJ>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      i32x4 w;
+      static_for<4>([&](auto T) {
+        constexpr int t = decltype(T)::value;
+        uint32_t packed = 0;
+        static_for<RCAP>([&](auto C) {
+          constexpr int c = decltype(C)::value;
+          packed |= (reduce_acc<RCAP>(e, c, acc[c][i][j][t]) & 0xFFu) << (8 * c);
+        });
+        w[t] = static_cast<int32_t>(packed);
+      });
+      store_coherent(base + (static_cast<int64_t>(split) * CH + i * NJ + j) * 1024, w);
+    });
+  });
+  wait_vm_all();
+  uint32_t old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(g.tickets + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __builtin_amdgcn_readfirstlane(old);
+  if (old != static_cast<uint32_t>(S - 1)) return false;
+  // the last ticket: every other split's residues are in place.  They are
+  // read G splits at a time, every load of a group issued before the first
+  // is used (own split and splits past S read a valid slot and are masked).
+  asm volatile("" ::: "memory");
+  constexpr int G = CH >= 4 ? 1 : 4 / CH;  // at most 4 chunks (16 registers) in flight, or one split
+  for (int s0 = 0; s0 < S; s0 += G) {
+    i32x4 w[G][MI][NJ];
+    static_for<G>([&](auto U) {
+      constexpr int u = decltype(U)::value;
+      const int s = min(s0 + u, S - 1);
+      static_for<MI>([&](auto I) {
+        static_for<NJ>([&](auto J) {
+          constexpr int i = decltype(I)::value, j = decltype(J)::value;
+          w[u][i][j] = load_coherent(base + (static_cast<int64_t>(s) * CH + i * NJ + j) * 1024);
+        });
+      });
+    });
+    static_for<G>([&](auto U) {
+      constexpr int u = decltype(U)::value;
+      const bool use = s0 + u < S && s0 + u != split;
+      static_for<MI>([&](auto I) {
+        static_for<NJ>([&](auto J) {
+          constexpr int i = decltype(I)::value, j = decltype(J)::value;
+          static_for<4>([&](auto T) {
+            constexpr int t = decltype(T)::value;
+            const uint32_t word = use ? static_cast<uint32_t>(w[u][i][j][t]) : 0u;
+            static_for<RCAP>([&](auto C) {
+              constexpr int c = decltype(C)::value;
+              acc[c][i][j][t] += static_cast<int32_t>(byte_of(word, c));
+            });
+          });
+        });
+      });
+    });
+  }
+  if (lane == 0) __hip_atomic_store(g.tickets + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
 }
 
 // ---------------------------------------------------------------------------
@@ -658,10 +830,11 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nthreads = g.threads, ks_n = nthreads >> 6;
   const int c_act = active_channels<RCAP>(g, red, &bcast, nthreads);
-  int mt, nt;
-  tile_of(g.tiles_m, g.tiles_n, mt, nt);
+  int mt, nt, split;
+  tile_of(g.tiles_m, g.tiles_n, g.splits, mt, nt, split);
   const int m0 = mt * BM, n0 = nt * BN;
-  const int nk = g.kp >> 6;
+  const KRange kr = k_range(g, split);
+  const int nk = kr.nk, a_k = kr.a_k;
   const int kofs = (lane >> 4) * 16;
 
   const int8_t *ap[MB];
@@ -669,13 +842,13 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
   static_for<MB>([&](auto I) {
     constexpr int i = decltype(I)::value;
     const int row = min(m0 + i * 16 + (lane & 15), g.m - 1);
-    ap[i] = g.a + static_cast<int64_t>(row) * g.a_ld;
+    ap[i] = g.a + static_cast<int64_t>(row) * g.a_ld + kr.ks0 * 64;
   });
   const int nblk = (g.n + 15) >> 4;
   static_for<NB>([&](auto J) {
     constexpr int j = decltype(J)::value;
     const int jb = min(nt * NB + j, nblk - 1);
-    bp[j] = g.b + static_cast<int64_t>(jb) * g.b_ld + lane * 16;
+    bp[j] = g.b + static_cast<int64_t>(jb) * g.b_ld + kr.ks0 * 1024 + lane * 16;
   });
   int64_t boff[RCAP], aoff[AP];
   static_for<RCAP>([&](auto C) { boff[decltype(C)::value] = plane_off(decltype(C)::value, c_act, g.b_cs); });
@@ -693,8 +866,8 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
       constexpr int u = decltype(UU)::value;
       const int ks = min(q + u, nk - 1);
       const int ka = ks * 64 + kofs;
-      const bool av = (q + u < nk) && (ka < g.a_k);
-      const int kac = min(ka, g.a_k - 16);
+      const bool av = (q + u < nk) && (ka < a_k);
+      const int kac = min(ka, a_k - 16);
       static_for<AP>([&](auto PP) {
         constexpr int p = decltype(PP)::value;
         static_for<MB>([&](auto I) {
@@ -756,6 +929,12 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
   }
 
   if (ks_n == 1) {
+    // a K split over workgroups (one wave each): only the last to finish
+    // this tile goes on
+    if constexpr (stream_splits(RCAP, MB, NB)) {
+      if (g.splits > 1 && !split_exchange<RCAP, MB, NB>(g, e, acc, mt + static_cast<int64_t>(nt) * g.tiles_m, split))
+        return;
+    }
     const int64_t idx0 = static_cast<int64_t>(m0 + 4 * (lane >> 4)) * e.out_ld + n0 + (lane & 15);
     ColScale cs[NB];
     static_for<NB>([&](auto J) { cs[J] = cs4[decltype(J)::value]; });
@@ -873,10 +1052,11 @@ __global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgs args) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c_act = active_channels<RCAP>(g, red, &bcast, NT);
-  int mt, nt;
-  tile_of(g.tiles_m, g.tiles_n, mt, nt);
+  int mt, nt, split;
+  tile_of(g.tiles_m, g.tiles_n, g.splits, mt, nt, split);
   const int m0 = mt * BM, n0 = nt * (NWV * BNW) + wave * BNW;
-  const int nk = g.kp >> 6;
+  const KRange kr = k_range(g, split);
+  const int nk = kr.nk, a_k = kr.a_k;
 
   // A staging: chunk q -> plane p, row, 16-byte part
   const int8_t *asrc[AC];
@@ -889,7 +1069,7 @@ __global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgs args) {
     const int qq = inside ? q : 0;
     const int p = qq / (BM * 4), w = qq % (BM * 4), row = w >> 2, part = w & 3;
     const int grow = min(m0 + row, g.m - 1);
-    asrc[i] = g.a + plane_off(p, c_act, g.a_cs) + static_cast<int64_t>(grow) * g.a_ld;
+    asrc[i] = g.a + plane_off(p, c_act, g.a_cs) + static_cast<int64_t>(grow) * g.a_ld + kr.ks0 * 64;
     alds[i] = inside ? p * PLANE + a_chunk_off(row, part) : AP * PLANE;
     apart[i] = part * 16;
     aon[i] = inside && (ARAW || p < c_act);
@@ -899,7 +1079,7 @@ __global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgs args) {
   static_for<NB>([&](auto J) {
     constexpr int j = decltype(J)::value;
     const int jb = min((n0 >> 4) + j, nblk - 1);
-    bp[j] = g.b + static_cast<int64_t>(jb) * g.b_ld + lane * 16;
+    bp[j] = g.b + static_cast<int64_t>(jb) * g.b_ld + kr.ks0 * 1024 + lane * 16;
   });
   int64_t boff[RCAP];
   static_for<RCAP>([&](auto C) { boff[decltype(C)::value] = plane_off(decltype(C)::value, c_act, g.b_cs); });
@@ -914,8 +1094,8 @@ __global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgs args) {
     static_for<AC>([&](auto II) {
       constexpr int i = decltype(II)::value;
       const int ka = kc * 64 + apart[i];
-      const bool keep = aon[i] && ks < nk && ka < g.a_k;
-      ra[s][i] = select16(keep, load16(asrc[i] + min(ka, g.a_k - 16)));
+      const bool keep = aon[i] && ks < nk && ka < a_k;
+      ra[s][i] = select16(keep, load16(asrc[i] + min(ka, a_k - 16)));
     });
     static_for<RCAP>([&](auto C) {
       constexpr int c = decltype(C)::value;
@@ -993,6 +1173,11 @@ __global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgs args) {
   for (int ks0 = 0; ks0 < steps - P; ks0 += P) trip(ks0, std::true_type{});
   trip(steps - P, std::false_type{});
 
+  if constexpr (mfma_splits(RCAP, MB, NB)) {
+    if (g.splits > 1 &&
+        !split_exchange<RCAP, MB, NB>(g, e, acc, (mt + static_cast<int64_t>(nt) * g.tiles_m) * NWV + wave, split))
+      return;
+  }
   register_epilogue<RCAP, MB, NB>(g, e, c_act, acc, m0, n0, m_lim, n_lim, cs);
 }
 
@@ -1060,10 +1245,11 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int c_act = active_channels<RCAP>(g, red, &bcast, 64 * NW);
-  int mt, nt;
-  tile_of(g.tiles_m, g.tiles_n, mt, nt);
+  int mt, nt, split;
+  tile_of(g.tiles_m, g.tiles_n, g.splits, mt, nt, split);
   const int m0 = mt * kLdsBM, n0 = nt * kLdsBN;
-  const int nk = g.kp >> 6;
+  const KRange kr = k_range(g, split);
+  const int nk = kr.nk;  // a multiple of the stage count (the launcher sizes kchunk so)
 
   // Direct-to-LDS sources.  A is loaded two K steps at a time, as whole
   // 128-byte row segments: block b (8 rows, 1 KB) of the pair of steps
@@ -1092,10 +1278,10 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
     constexpr int u = decltype(U)::value;
     const int q = wave + NW * u, c = q / (kLdsBN / 16);
     const int jb = min((n0 >> 4) + q % (kLdsBN / 16), nblk - 1);
-    bbase[u] = g.b + plane_off(c, c_act, g.b_cs) + static_cast<int64_t>(jb) * g.b_ld;
+    bbase[u] = g.b + plane_off(c, c_act, g.b_cs) + static_cast<int64_t>(jb) * g.b_ld + kr.ks0 * 1024;
   });
   const uint32_t boff = static_cast<uint32_t>(lane * 16);
-  const int8_t *abase = g.a;
+  const int8_t *abase = g.a + kr.ks0 * 64;
   const uint32_t sbase = __builtin_amdgcn_readfirstlane(
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t *)(smem))) +
       wave * 1024);
@@ -1244,6 +1430,9 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
   // the loads issued for steps past K land before the workgroup ends
   wait_vmcnt<0>();
 
+  if (g.splits > 1 &&
+      !split_exchange<RCAP, MI, NJ>(g, e, acc, (mt + static_cast<int64_t>(nt) * g.tiles_m) * NW + wave, split))
+    return;
   register_epilogue<RCAP, MI, NJ>(g, e, c_act, acc, rw0, cw0, m_lim, n_lim, cs);
 }
 
@@ -1256,7 +1445,7 @@ bool launch_stream(GemmArgs g, int mb, int nb, int ks, int ucap, hipStream_t st)
   if (mb == MB_ && nb == NB_ && ucap == UCAP_) {                                            \
     g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                                          \
     g.tiles_n = (g.n + 16 * NB_ - 1) / (16 * NB_);                                          \
-    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));                          \
+    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n * g.splits));               \
     const size_t lds = ks > 1 ? static_cast<size_t>(RCAP) * 256 * MB_ * NB_ * 4 : 0;         \
     g.threads = 64 * ks;                                                                    \
     hipLaunchKernelGGL((stream_kernel<RCAP, MB_, NB_, ARAW, UCAP_>), grid, dim3(64 * ks), lds, st, g); \
@@ -1298,7 +1487,7 @@ bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, int nwv, hipStream_t st)
     if (mb == MB_ && nb == NB_) {                                          \
       g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                       \
       g.tiles_n = (g.n + 16 * nwv * NB_ - 1) / (16 * nwv * NB_);           \
-      const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));       \
+      const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n * g.splits)); \
       const int p = p_req > 0 ? p_req : PDEF;                              \
       __VA_ARGS__                                                          \
       return false;                                                        \
@@ -1335,6 +1524,28 @@ inline bool lds_kernel_fits(const GemmArgs &g, bool araw, int rcap) {
   return araw && rcap == 4 && g.a_k == g.kp && g.kp % (64 * kLdsStages) == 0 && a_offsets_fit;
 }
 
+// Tiles, waves per workgroup and accumulator chunks per lane of a choice
+// for an m x n output (the launchers derive the same tile grid).
+inline GemmGrid gemm_grid(const GemmChoice &c, int64_t m, int64_t n) {
+  GemmGrid r{};
+  auto cdiv = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
+  if (c.kind == kStream || c.kind == kStreamWide) {
+    r.tiles = cdiv(m, 16 * c.mb) * cdiv(n, 16 * c.nb);
+    r.waves = c.ks < 1 ? 1 : c.ks;
+    r.chunks = c.mb * c.nb;
+  } else if (c.kind == kLds) {
+    r.tiles = cdiv(m, kLdsBM) * cdiv(n, kLdsBN);
+    r.waves = 8;
+    r.chunks = (kLdsBM / 16 / 4) * (kLdsBN / 16 / 2);
+  } else {
+    const int nwv = c.kind == kMfma3 ? 3 : 4;
+    r.tiles = cdiv(m, 16 * c.mb) * cdiv(n, 16 * nwv * c.nb);
+    r.waves = nwv;
+    r.chunks = c.mb * c.nb;
+  }
+  return r;
+}
+
 template <int RCAP>
 bool launch_lds(GemmArgs g, bool araw, hipStream_t st) {
   if constexpr (RCAP != 4) {
@@ -1343,7 +1554,7 @@ bool launch_lds(GemmArgs g, bool araw, hipStream_t st) {
     if (!lds_kernel_fits(g, araw, RCAP)) return false;
     g.tiles_m = (g.m + kLdsBM - 1) / kLdsBM;
     g.tiles_n = (g.n + kLdsBN - 1) / kLdsBN;
-    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));
+    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n * g.splits));
     hipLaunchKernelGGL((lds_kernel<RCAP, 8>), grid, dim3(512), 0, st, g);
     return true;
   }

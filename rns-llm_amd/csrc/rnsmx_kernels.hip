@@ -264,9 +264,15 @@ __global__ __launch_bounds__(256) void decode_garner_kernel(const DecodeArgs a) 
 // ---------------------------------------------------------------------------
 // src [R][K][N] (the reference layout) -> the fragment-major layout of
 // encode_frag_kernel, zero padded: one thread per 16-byte fragment slot.
+// Also clears the first `ntickets` split counters of the workspace (the
+// drop-in op's workspace may hold anything before the call).
 __global__ __launch_bounds__(256) void transpose_frag_kernel(const int8_t *__restrict__ src, int64_t k,
                                                              int64_t n, int64_t n16, int64_t nk,
-                                                             int64_t total, int8_t *__restrict__ dst) {
+                                                             int64_t total, int8_t *__restrict__ dst,
+                                                             uint32_t *__restrict__ tickets, int64_t ntickets) {
+  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < ntickets;
+       q += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    tickets[q] = 0;
   for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < total;
        q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int lane = static_cast<int>(q & 63);
@@ -321,9 +327,6 @@ static int32_t check_launch(const char *what) {
   return RNSMX_OK;
 }
 
-// Process-wide override of the kernel choice (rnsmx_set_gemm_override).
-static GemmChoice g_override = {kAuto, 0, 0, 0};
-
 static constexpr int kStreamLdsMax = 65536;
 
 // Up to this many raw int8 rows, the adaptive prefix's row norms are summed
@@ -374,6 +377,7 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
     c.kind = wide ? kStreamWide : kStream;
     const int u = stream_u_of(rcap, araw, c.mb, c.nb, wide ? 8 : 4);
     c.ks = std::min(stream_ks_cap(rcap, c.mb, c.nb), std::max(1, (nk + u - 1) / u));
+    c.splits = 1;
     return c;
   }
   // The LDS kernel's 256 x 64 tiles run one workgroup per CU (128 KB of
@@ -384,6 +388,7 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   const int64_t lds_tiles = tiles(kLdsBM, kLdsBN);
   const int64_t rounds = (lds_tiles + 255) / 256;
   const bool full_rounds = 8 * lds_tiles >= 7 * 256 * rounds;
+  c.splits = 1;
   if (g.m > 128 && lds_kernel_fits(g, araw, rcap) && lds_tiles >= 256 && (g.kp >= 2048 || full_rounds)) {
     c.kind = kLds;
     return c;
@@ -444,10 +449,122 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   return c;
 }
 
-// Launches the GEMM for `g`.  araw: A is one int8 matrix for all channels.
-static int32_t launch_gemm(const GemmArgs &g, bool araw, hipStream_t st) {
+// ---------------------------------------------------------------------------
+// K split over workgroups (split_exchange in rnsmx_gemm.hpp)
+// ---------------------------------------------------------------------------
+// Bytes of the arrival counters at the start of every workspace.
+static constexpr int64_t kTicketBytes = int64_t{RNSMX_SPLIT_TICKETS} * 4;
+
+// Steps per split for `splits` workgroups over nk K steps (the LDS kernel
+// runs whole trips of its stages), and the split count that leaves no
+// split empty.
+static void split_steps(const GemmChoice &c, int nk, int &splits, int &kchunk) {
+  const int unit = c.kind == kLds ? kLdsStages : 1;
+  const int s = std::max(1, std::min(c.splits, nk / unit));
+  kchunk = ((nk + s - 1) / s + unit - 1) / unit * unit;
+  splits = (nk + kchunk - 1) / kchunk;
+}
+
+// Whether `c` may split K: a tile built with the exchange (stream_splits,
+// mfma_splits: up to 4 channels, one residue byte per channel in the
+// exchange word), one wave per stream workgroup (the waves of a larger one
+// already meet in LDS), and every (tile, wave) counter inside the
+// workspace's fixed counter block.
+static bool split_fits(const GemmChoice &c, const GemmArgs &g) {
   const int rcap = rcap_for(g.mods.channels);
-  GemmChoice c = g_override.kind != kAuto ? g_override : choose_gemm(g, araw);
+  const GemmGrid gr = gemm_grid(c, g.m, g.n);
+  bool built;
+  if (c.kind == kStream || c.kind == kStreamWide)
+    built = stream_splits(rcap, c.mb, c.nb) && c.ks == 1;
+  else if (c.kind == kLds)
+    built = rcap <= 4;
+  else
+    built = mfma_splits(rcap, c.mb, c.nb);
+  return built && gr.tiles * gr.waves <= RNSMX_SPLIT_TICKETS;
+}
+
+// Exchange-area bytes of a choice (0 without a split).
+static int64_t xchg_bytes(const GemmChoice &c, const GemmArgs &g) {
+  if (c.splits <= 1) return 0;
+  int splits, kchunk;
+  split_steps(c, g.kp / 64, splits, kchunk);
+  if (splits <= 1) return 0;
+  const GemmGrid gr = gemm_grid(c, g.m, g.n);
+  return round_up(gr.tiles * gr.waves * splits * gr.chunks * 1024, 256);
+}
+
+// The automatic split count for a choice of kernel and tile, from sweeps on
+// MI355X.  A split pays only where the K loop of each tile is long and the
+// grid leaves CUs idle: every split adds a fixed cost per workgroup (entry,
+// first loads, a second epilogue-sized pass over the residues) and an
+// exchange of R bytes per output element through the device-coherent level.
+// Measured (us, 4 channels, automatic kernel unsplit -> split):
+//   M=1    N=768  K=16384  57.3 -> 15.6 (8 splits)   M=256 N=256 K=8192  48.3 -> 16.4 (8)
+//   M=16   N=512  K=8192   30.2 -> 10.2 (8)          M=512 N=512 K=8192  46.5 -> 25.6 (4)
+//   M=256  N=768  K=4096   25.9 -> 17.9 (4)          M=128 N=4096 K=16384 104.5 -> 94.6 (2)
+//   M=2048 N=768  K=16384 148 -> 128 (2)
+// and it loses on the BASELINE shapes: C2 M=256 (216 tiles, 12 K steps)
+// 10.3 -> 15.9 (2), C3 M=1 4.3 -> 5.5, C5 M=64 (192 tiles, 64 steps) 44.8
+// -> 48.2, C5 M=512 (384 LDS tiles) 107 -> 127 (and 114 even with the
+// exchange data left out: the extra workgroups' fixed cost alone).
+// A split stream kernel runs one wave per workgroup, against the unsplit
+// one's four waves sharing K through LDS; at decode (M=1) the one-wave
+// split wins from 4 splits (N=768: K=4096 9.35 -> 8.33, K=8192 16.4 ->
+// 11.1, K=16384 28.7 -> 15.7; N=256 K=4096 7.07 -> 6.53) and never with 2
+// (N=768 K=2048 7.39 against 9.76).
+// Rule: under 128 tiles, the largest power of two up to 8 that keeps at
+// least 16 K steps per split and at most 512 workgroups (for the stream
+// kernel only when that is 4 or more); 128-511 tiles of the MFMA or LDS
+// kernel, 2 splits once K >= 8192; otherwise none.
+static int choose_splits(const GemmChoice &c, const GemmArgs &g) {
+  const int nk = g.kp / 64;
+  const int64_t tiles = gemm_grid(c, g.m, g.n).tiles;
+  const bool stream = c.kind == kStream || c.kind == kStreamWide;
+  int s = 1;
+  if (tiles < 128) {
+    const int64_t cap = std::min<int64_t>(std::min<int64_t>(8, 512 / tiles), nk / 16);
+    while (2 * s <= cap) s *= 2;
+    if (stream && s < 4) s = 1;
+  } else if (!stream && tiles < 512 && nk >= 128) {
+    s = 2;
+  }
+  return s;
+}
+
+// The automatic plan: kernel and tile (choose_gemm), then the split.  A
+// stream choice that splits over workgroups runs one wave per workgroup.
+static GemmChoice auto_plan(const GemmArgs &g, bool araw, bool allow_split) {
+  GemmChoice c = choose_gemm(g, araw);
+  if (!allow_split || rcap_for(g.mods.channels) > 4) return c;
+  GemmChoice t = c;
+  if (t.kind == kStream || t.kind == kStreamWide) t.ks = 1;
+  t.splits = choose_splits(c, g);
+  if (t.splits > 1 && split_fits(t, g)) return t;
+  return c;
+}
+
+static int32_t plan_from(const rnsmx_plan_t *plan, const GemmArgs &g, bool araw, bool allow_split,
+                         GemmChoice &c) {
+  if (plan == nullptr || plan->kind == kAuto) {
+    c = auto_plan(g, araw, allow_split);
+    return RNSMX_OK;
+  }
+  const int k = plan->kind;
+  if (k != kStream && k != kMfma && k != kLds && k != kStreamWide && k != kMfma3)
+    return fail(RNSMX_EINVAL, "plan kind must be 0 (auto), 1 (stream), 2 (mfma), 3 (lds), 4 (wide stream) or 5 (3-wave mfma)");
+  if (k != kLds && (plan->mb < 1 || plan->nb < 1)) return fail(RNSMX_EINVAL, "tile blocks must be positive");
+  c = GemmChoice{k, plan->mb, plan->nb, plan->ks, std::max(1, plan->splits)};
+  if (c.splits > 1 && (!allow_split || !split_fits(c, g)))
+    return fail(RNSMX_EINVAL, "this plan cannot split K over workgroups (channels, stream waves, or counters)");
+  return RNSMX_OK;
+}
+
+// Launches the GEMM for `g` with choice `c`.  araw: A is one int8 matrix for
+// all channels.  tickets / xchg: the split counters and exchange area (only
+// read when c splits K).
+static int32_t launch_gemm(GemmArgs g, bool araw, const GemmChoice &c, uint32_t *tickets, int8_t *xchg,
+                           hipStream_t st) {
+  const int rcap = rcap_for(g.mods.channels);
   if (c.kind == kStream || c.kind == kStreamWide) {
     const int cap = stream_ks_cap(rcap, c.mb, c.nb);
     if (c.ks < 1 || c.ks > cap) {
@@ -455,7 +572,19 @@ static int32_t launch_gemm(const GemmArgs &g, bool araw, hipStream_t st) {
       return RNSMX_EINVAL;
     }
   }
-  bool ok = false;
+  g.splits = 1;
+  g.kchunk = g.kp / 64;
+  g.tickets = tickets;
+  g.xchg = xchg;
+  if (c.splits > 1) {
+    if (c.kind == kLds && !lds_kernel_fits(g, araw, rcap)) {
+      set_error("no GEMM kernel for kind %d, tile %d x %d, %d channels", c.kind, c.mb, c.nb, g.mods.channels);
+      return RNSMX_EINVAL;
+    }
+    split_steps(c, g.kp / 64, g.splits, g.kchunk);
+    if (g.splits > 1 && (tickets == nullptr || xchg == nullptr))
+      return fail(RNSMX_EINVAL, "a K split needs the workspace's counters and exchange area");
+  }
   using PartFn = bool (*)(const GemmArgs &, bool, const GemmChoice &, hipStream_t);
 #define RNSMX_PARTS(R)                                                                      \
   {                                                                                         \
@@ -466,8 +595,7 @@ static int32_t launch_gemm(const GemmArgs &g, bool araw, hipStream_t st) {
                                               RNSMX_PARTS(10)};
 #undef RNSMX_PARTS
   const int ri = rcap == 3 ? 0 : rcap == 4 ? 1 : rcap == 6 ? 2 : 3;
-  ok = parts[ri][gemm_part_of(c, araw)](g, araw, c, st);
-  if (!ok) {
+  if (!parts[ri][gemm_part_of(c, araw)](g, araw, c, st)) {
     set_error("no GEMM kernel for kind %d, tile %d x %d, %d channels", c.kind, c.mb, c.nb,
               g.mods.channels);
     return RNSMX_EINVAL;
@@ -660,14 +788,44 @@ int32_t rnsmx_encode_centered(const void *values_dev, int32_t dtype, int64_t row
   return launch_encode_rows(dtype, e, st);
 }
 
+// The fields of GemmArgs the kernel choice reads, for an M x N x K product
+// (raw int8 activations read in place with row stride K, or residue planes
+// padded to kp).
+static GemmArgs plan_args(int64_t m, int64_t n, int64_t k, int32_t channels, bool araw) {
+  GemmArgs g{};
+  g.m = static_cast<int32_t>(m);
+  g.n = static_cast<int32_t>(n);
+  g.kp = static_cast<int32_t>(round_up(std::max<int64_t>(k, 1), RNSMX_K_ALIGN));
+  g.a_k = araw ? static_cast<int32_t>(k) : g.kp;
+  g.a_ld = araw ? k : g.kp;
+  g.mods.channels = channels;
+  return g;
+}
+
+// Drop-in op workspace: [split counters][A padded to kp (when needed)]
+// [B repacked fragment-major][split exchange].
+struct FusedLayout {
+  int64_t a_pad, b_nk, xchg, total;
+};
+
+static FusedLayout fused_layout(int64_t m, int64_t kp, int64_t n, int32_t channels, int64_t xchg) {
+  FusedLayout l{};
+  l.a_pad = kTicketBytes;
+  l.b_nk = l.a_pad + round_up(channels * m * kp, 256);
+  l.xchg = l.b_nk + round_up(channels * ((n + 15) / 16) * 16 * kp, 256);
+  l.total = l.xchg + xchg;
+  return l;
+}
+
 int64_t rnsmx_fused_workspace_bytes(int64_t m, int64_t k, int64_t n, int32_t channels) {
-  if (m < 0 || k < 0 || n < 0 || channels < 1) return -1;
+  if (m < 0 || k < 0 || n < 0 || channels < 1 || channels > RNSMX_MAX_CHANNELS) return -1;
   const int64_t kp = round_up(std::max<int64_t>(k, 1), RNSMX_K_ALIGN);
-  // room for a padded copy of A (used when K % 16 != 0 or A is not 16-byte
-  // aligned) followed by B repacked to [R][N][kp]
-  const int64_t a = round_up(channels * m * kp, 256);
-  const int64_t b = round_up(channels * ((n + 15) / 16) * 16 * kp, 256);
-  return a + b;
+  int64_t xchg = 0;
+  if (m > 0 && n > 0 && m <= INT32_MAX && n <= INT32_MAX) {
+    const GemmArgs g = plan_args(m, n, k, channels, false);
+    xchg = xchg_bytes(auto_plan(g, false, true), g);
+  }
+  return fused_layout(m, kp, n, channels, xchg).total;
 }
 
 int32_t rnsmx_matmul_centered_fused_out(const int8_t *a_dev, const int8_t *b_dev, int32_t m, int32_t k,
@@ -693,14 +851,19 @@ int32_t rnsmx_matmul_centered_fused_out(const int8_t *a_dev, const int8_t *b_dev
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int R = mods->channels;
   const int64_t kp = round_up(k, RNSMX_K_ALIGN);
+  GemmArgs g = plan_args(m, n, k, R, false);
+  g.mods = *mods;
+  const GemmChoice c = auto_plan(g, false, true);
+  const FusedLayout l = fused_layout(m, kp, n, R, xchg_bytes(c, g));
   int8_t *ws = static_cast<int8_t *>(workspace_dev);
+  uint32_t *tickets = reinterpret_cast<uint32_t *>(ws);
   const int8_t *a_use = a_dev;
   int64_t a_ld = k, a_k = k;
-  int8_t *b_nk = ws + round_up(R * static_cast<int64_t>(m) * kp, 256);
+  int8_t *b_nk = ws + l.b_nk;
   if (k % 16 != 0 || !aligned16(a_dev)) {
     // rows of 16-byte chunks are read straight from the caller's planes
     // otherwise (chunks past K load as zero)
-    int8_t *a_pad = ws;
+    int8_t *a_pad = ws + l.a_pad;
     const int64_t total = R * static_cast<int64_t>(m) * kp;
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 16384));
     hipLaunchKernelGGL(pad_rows_kernel, dim3(blocks), dim3(256), 0, st, a_dev, static_cast<int64_t>(m),
@@ -713,12 +876,13 @@ int32_t rnsmx_matmul_centered_fused_out(const int8_t *a_dev, const int8_t *b_dev
   const int64_t n16 = (n + 15) / 16, nk = kp / 64;
   {
     const int64_t total = R * n16 * nk * 64;
+    const GemmGrid gr = gemm_grid(c, m, n);
+    const int64_t ntickets = c.splits > 1 ? gr.tiles * gr.waves : 0;
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 16384));
     hipLaunchKernelGGL(transpose_frag_kernel, dim3(blocks), dim3(256), 0, st, b_dev, static_cast<int64_t>(k),
-                       static_cast<int64_t>(n), n16, nk, total, b_nk);
+                       static_cast<int64_t>(n), n16, nk, total, b_nk, tickets, ntickets);
     if (int32_t rc = check_launch("transpose_frag")) return rc;
   }
-  GemmArgs g{};
   g.a = a_use;
   g.a_ld = a_ld;
   g.a_cs = a_ld * m;
@@ -726,15 +890,11 @@ int32_t rnsmx_matmul_centered_fused_out(const int8_t *a_dev, const int8_t *b_dev
   g.b = b_nk;
   g.b_ld = kp * 16;
   g.b_cs = kp * 16 * n16;
-  g.m = m;
-  g.n = n;
-  g.kp = static_cast<int32_t>(kp);
   g.min_channels = 0;
   g.out = out_dev;
   g.out_ld = n;
   g.out_dtype = RNSMX_INT64;
-  g.mods = *mods;
-  return launch_gemm(g, false, st);
+  return launch_gemm(g, false, c, tickets, ws + l.xchg, st);
 }
 
 int32_t rnsmx_prepare_weight(const void *b_nk_dev, int32_t dtype, int32_t n, int32_t k,
@@ -771,18 +931,50 @@ int32_t rnsmx_prepare_weight(const void *b_nk_dev, int32_t dtype, int32_t n, int
 
 }
 
-int64_t rnsmx_prepared_workspace_bytes(int64_t m, int64_t k, int32_t channels) {
-  if (m < 0 || k < 0 || channels < 1) return -1;
+// Prepared-path workspace: [split counters][activation residue planes
+// (only when A is not read in place)][row L1 norms][split exchange].  Only
+// the counters sit at a fixed place; the rest is rewritten by every call.
+struct PreparedLayout {
+  int64_t a_res, row_l1, xchg, total;
+};
+
+static PreparedLayout prepared_layout(bool araw, int64_t m, int64_t kp, int32_t channels, int64_t xchg) {
+  PreparedLayout l{};
+  l.a_res = kTicketBytes;
+  l.row_l1 = l.a_res + (araw ? 0 : round_up(channels * m * kp, 256));
+  l.xchg = l.row_l1 + round_up(8 * m, 256);
+  l.total = l.xchg + xchg;
+  return l;
+}
+
+// Workspace bytes of one prepared-path call shape and plan, for A read in
+// place (araw) or as residue planes.
+static int64_t prepared_need(bool araw, int64_t m, int64_t k, int64_t n, int32_t channels,
+                             const rnsmx_plan_t *plan) {
   const int64_t kp = round_up(std::max<int64_t>(k, 1), RNSMX_K_ALIGN);
-  return round_up(channels * m * kp, 256) + round_up(8 * m, 256);
+  int64_t xchg = 0;
+  if (m > 0 && n > 0) {
+    const GemmArgs g = plan_args(m, n, k, channels, araw);
+    GemmChoice c{};
+    if (plan_from(plan, g, araw, true, c) == RNSMX_OK) xchg = xchg_bytes(c, g);
+  }
+  return prepared_layout(araw, m, kp, channels, xchg).total;
+}
+
+int64_t rnsmx_prepared_workspace_bytes(int64_t m, int64_t k, int64_t n, int32_t channels,
+                                       const rnsmx_plan_t *plan) {
+  if (m < 0 || k < 0 || n < 0 || channels < 1 || channels > RNSMX_MAX_CHANNELS || m > INT32_MAX ||
+      n > INT32_MAX || k > INT32_MAX - 63)
+    return -1;
+  return std::max(prepared_need(true, m, k, n, channels, plan), prepared_need(false, m, k, n, channels, plan));
 }
 
 int32_t rnsmx_matmul_prepared_fused(const void *a_dev, int32_t a_dtype, int32_t m, int32_t k, int32_t n,
                                     const int8_t *packed_dev, const rnsmx_moduli_t *mods,
                                     const int16_t *lut_dev, int32_t lut_channels,
                                     const rnsmx_adaptive_t *adaptive, const rnsmx_epilogue_t *epilogue,
-                                    void *workspace_dev, int64_t workspace_bytes, void *out_dev,
-                                    void *stream) {
+                                    const rnsmx_plan_t *plan, void *workspace_dev, int64_t workspace_bytes,
+                                    void *out_dev, void *stream) {
   clear_error();
   if (!mods || mods->channels < 1) return fail(RNSMX_EINVAL, "moduli are not initialised");
   if (m < 0 || k < 1 || n < 0) return fail(RNSMX_EINVAL, "bad GEMM shape");
@@ -804,23 +996,28 @@ int32_t rnsmx_matmul_prepared_fused(const void *a_dev, int32_t a_dtype, int32_t 
   if (min_ch != 0 && !adaptive->w_absmax_dev) return fail(RNSMX_EINVAL, "adaptive needs max|B|");
   if (m == 0 || n == 0) return RNSMX_OK;
   if (!a_dev || !packed_dev || !out_dev || !workspace_dev) return fail(RNSMX_EINVAL, "null tensor pointer");
-  const int64_t need = rnsmx_prepared_workspace_bytes(m, k, mods->channels);
-  if (workspace_bytes < need) {
-    set_error("workspace too small: %lld < %lld bytes", static_cast<long long>(workspace_bytes),
-              static_cast<long long>(need));
-    return RNSMX_ESPACE;
-  }
+  if (!aligned16(a_dev)) return fail(RNSMX_EINVAL, "activations must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int R = mods->channels;
   const int64_t kp = round_up(k, RNSMX_K_ALIGN);
-  int8_t *a_res = static_cast<int8_t *>(workspace_dev);
-  int64_t *row_l1 = reinterpret_cast<int64_t *>(a_res + round_up(R * static_cast<int64_t>(m) * kp, 256));
-  if (!aligned16(a_dev)) return fail(RNSMX_EINVAL, "activations must be 16-byte aligned");
 
   // int8 activations with 16-byte rows feed the MFMA directly (they are
   // their own representatives mod every m_c); the encoder then only runs for
   // the adaptive row L1 norms.  Other sources are encoded to residue planes.
   const bool araw = a_dtype == RNSMX_INT8 && k % 16 == 0 && raw_accumulator_fits(*mods, k);
+  GemmArgs g = plan_args(m, n, k, R, araw);
+  g.mods = *mods;
+  GemmChoice c{};
+  if (int32_t rc = plan_from(plan, g, araw, true, c)) return rc;
+  const PreparedLayout l = prepared_layout(araw, m, kp, R, xchg_bytes(c, g));
+  if (workspace_bytes < l.total) {
+    set_error("workspace too small: %lld < %lld bytes", static_cast<long long>(workspace_bytes),
+              static_cast<long long>(l.total));
+    return RNSMX_ESPACE;
+  }
+  int8_t *ws = static_cast<int8_t *>(workspace_dev);
+  int8_t *a_res = ws + l.a_res;
+  int64_t *row_l1 = reinterpret_cast<int64_t *>(ws + l.row_l1);
   // With a few raw rows the GEMM workgroups sum the adaptive row norms
   // themselves (each reads the rows: a few KB from L2), which saves the
   // encoder launch: C5 adaptive M=1 44 -> 39 us.
@@ -838,24 +1035,16 @@ int32_t rnsmx_matmul_prepared_fused(const void *a_dev, int32_t a_dtype, int32_t 
   if (!araw || (min_ch != 0 && !l1_in_gemm))
     if (int32_t rc = launch_encode_rows(a_dtype, e, st)) return rc;
 
-  GemmArgs g{};
   if (araw) {
     g.a = static_cast<const int8_t *>(a_dev);
-    g.a_ld = k;
     g.a_cs = 0;
-    g.a_k = k;
   } else {
     g.a = a_res;
-    g.a_ld = kp;
     g.a_cs = kp * m;
-    g.a_k = static_cast<int32_t>(kp);
   }
   g.b = packed_dev;
   g.b_ld = kp * 16;
   g.b_cs = kp * 16 * ((n + 15) / 16);
-  g.m = m;
-  g.n = n;
-  g.kp = static_cast<int32_t>(kp);
   g.min_channels = min_ch;
   g.row_l1 = l1_in_gemm ? nullptr : row_l1;
   g.w_absmax = min_ch != 0 ? adaptive->w_absmax_dev : nullptr;
@@ -866,8 +1055,7 @@ int32_t rnsmx_matmul_prepared_fused(const void *a_dev, int32_t a_dtype, int32_t 
   g.a_scale = epilogue ? epilogue->a_scale_dev : nullptr;
   g.w_scale = epilogue ? epilogue->w_scale_dev : nullptr;
   g.bias = epilogue ? epilogue->bias_dev : nullptr;
-  g.mods = *mods;
-  return launch_gemm(g, araw, st);
+  return launch_gemm(g, araw, c, reinterpret_cast<uint32_t *>(ws), ws + l.xchg, st);
 }
 
 int32_t rnsmx_matmul_residues_prepared(const int8_t *a_res_dev, int64_t a_ld, int32_t m, int32_t k,
@@ -915,47 +1103,27 @@ int32_t rnsmx_matmul_residues_prepared(const int8_t *a_res_dev, int64_t a_ld, in
   g.w_scale = epilogue ? epilogue->w_scale_dev : nullptr;
   g.bias = epilogue ? epilogue->bias_dev : nullptr;
   g.mods = *mods;
-  return launch_gemm(g, false, static_cast<hipStream_t>(stream));
+  return launch_gemm(g, false, auto_plan(g, false, false), nullptr, nullptr, static_cast<hipStream_t>(stream));
 }
 
-int32_t rnsmx_set_gemm_override(int32_t kind, int32_t mb, int32_t nb, int32_t ks) {
+int32_t rnsmx_gemm_plan(int64_t m, int64_t n, int64_t k, int32_t channels, int32_t raw_a, rnsmx_plan_t *out) {
   clear_error();
-  if (kind == kAuto) {
-    g_override = GemmChoice{kAuto, 0, 0, 0};
-    return RNSMX_OK;
-  }
-  if (kind != kStream && kind != kMfma && kind != kLds && kind != kStreamWide && kind != kMfma3)
-    return fail(RNSMX_EINVAL,
-                "kind must be 0 (auto), 1 (stream), 2 (mfma), 3 (lds), 4 (wide stream) or 5 (3-wave mfma)");
-  if (kind != kLds && (mb < 1 || nb < 1)) return fail(RNSMX_EINVAL, "tile blocks must be positive");
-  g_override = GemmChoice{kind, mb, nb, ks};
-  return RNSMX_OK;
-}
-
-int32_t rnsmx_gemm_plan(int64_t m, int64_t n, int64_t k, int32_t channels, int32_t raw_a,
-                        int32_t *kind, int32_t *mb, int32_t *nb, int32_t *ks) {
-  clear_error();
-  if (kind == nullptr || mb == nullptr || nb == nullptr || ks == nullptr)
-    return fail(RNSMX_EINVAL, "gemm plan needs four output pointers");
+  if (out == nullptr) return fail(RNSMX_EINVAL, "gemm plan needs an output");
   if (m < 1 || n < 1 || k < 1 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX - 63)
     return fail(RNSMX_EINVAL, "gemm plan needs 1 <= M, N, K < 2^31");
   if (channels < 2 || channels > RNSMX_MAX_CHANNELS)
     return fail(RNSMX_EINVAL, "gemm plan needs 2..10 channels");
-  // the fields choose_gemm reads, as the fused entry points fill them:
-  // raw int8 activations are read in place (row stride K), residue planes
-  // are padded to kp
-  GemmArgs g{};
-  g.m = static_cast<int32_t>(m);
-  g.n = static_cast<int32_t>(n);
-  g.kp = static_cast<int32_t>((k + 63) / 64 * 64);
-  g.a_k = raw_a ? static_cast<int32_t>(k) : g.kp;
-  g.a_ld = raw_a ? k : g.kp;
-  g.mods.channels = channels;
-  const GemmChoice c = g_override.kind != kAuto ? g_override : choose_gemm(g, raw_a != 0);
-  *kind = c.kind;
-  *mb = c.mb;
-  *nb = c.nb;
-  *ks = c.ks;
+  const GemmArgs g = plan_args(m, n, k, channels, raw_a != 0);
+  GemmChoice c = auto_plan(g, raw_a != 0, true);
+  if (c.splits > 1) {
+    int kchunk;
+    split_steps(c, g.kp / 64, c.splits, kchunk);
+  }
+  out->kind = c.kind;
+  out->mb = c.mb;
+  out->nb = c.nb;
+  out->ks = c.ks;
+  out->splits = c.splits;
   return RNSMX_OK;
 }
 

@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 MAX_CHANNELS = 10
 K_ALIGN = 64
+SPLIT_TICKETS = 16384  # RNSMX_SPLIT_TICKETS: 32-bit counters at the start of a workspace
 
 OK, EINVAL, ERANGE, ELAUNCH, ESPACE = 0, 1, 2, 3, 4
 
@@ -34,7 +35,6 @@ EXPORTED_SYMBOLS = (
     "rnsmx_prepared_workspace_bytes",
     "rnsmx_matmul_prepared_fused",
     "rnsmx_matmul_residues_prepared",
-    "rnsmx_set_gemm_override",
     "rnsmx_gemm_plan",
     "rnsmx_quantize_symmetric",
     "rnsmx_decode_garner",
@@ -70,6 +70,35 @@ class Epilogue(ctypes.Structure):
     ]
 
 
+class Plan(ctypes.Structure):
+    """Mirror of ``rnsmx_plan_t``: kind 0 = automatic; 1 stream, 2 MFMA,
+    3 LDS-staged, 4 wide stream, 5 three-wave MFMA; tile blocks, ks, and
+    the number of workgroups splitting K."""
+
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("mb", ctypes.c_int32),
+        ("nb", ctypes.c_int32),
+        ("ks", ctypes.c_int32),
+        ("splits", ctypes.c_int32),
+    ]
+
+    def as_tuple(self) -> tuple[int, int, int, int, int]:
+        return (self.kind, self.mb, self.nb, self.ks, self.splits)
+
+
+def make_plan(plan) -> "Plan | None":
+    """A ``Plan`` from a (kind, mb, nb, ks[, splits]) tuple; None stays None."""
+    if plan is None or isinstance(plan, Plan):
+        return plan
+    fields = tuple(int(v) for v in plan)
+    if len(fields) == 4:
+        fields += (1,)
+    if len(fields) != 5:
+        raise ValueError("a plan is (kind, mb, nb, ks) or (kind, mb, nb, ks, splits)")
+    return Plan(*fields)
+
+
 class Adaptive(ctypes.Structure):
     """Mirror of ``rnsmx_adaptive_t``."""
 
@@ -96,22 +125,20 @@ _SIGNATURES = {
         _I32, [_P, _P, _I32, _I32, _I32, ctypes.POINTER(Moduli), _P, _I32, _P, _I64, _P, _P]),
     "rnsmx_prepare_weight": (
         _I32, [_P, _I32, _I32, _I32, ctypes.POINTER(Moduli), _P, _P, _P]),
-    "rnsmx_prepared_workspace_bytes": (_I64, [_I64, _I64, _I32]),
+    "rnsmx_prepared_workspace_bytes": (_I64, [_I64, _I64, _I64, _I32, ctypes.POINTER(Plan)]),
     "rnsmx_matmul_prepared_fused": (
         _I32, [_P, _I32, _I32, _I32, _I32, _P, ctypes.POINTER(Moduli), _P, _I32,
-               ctypes.POINTER(Adaptive), ctypes.POINTER(Epilogue), _P, _I64, _P, _P]),
+               ctypes.POINTER(Adaptive), ctypes.POINTER(Epilogue), ctypes.POINTER(Plan),
+               _P, _I64, _P, _P]),
     "rnsmx_matmul_residues_prepared": (
         _I32, [_P, _I64, _I32, _I32, _I32, _P, ctypes.POINTER(Moduli), _P, _I32,
                ctypes.POINTER(Epilogue), _P, _P]),
-    "rnsmx_set_gemm_override": (_I32, [_I32, _I32, _I32, _I32]),
-    "rnsmx_gemm_plan": (_I32, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _I32, _I32,
-                                ctypes.POINTER(_I32), ctypes.POINTER(_I32),
-                                ctypes.POINTER(_I32), ctypes.POINTER(_I32)]),
+    "rnsmx_gemm_plan": (_I32, [_I64, _I64, _I64, _I32, _I32, ctypes.POINTER(Plan)]),
     "rnsmx_quantize_symmetric": (_I32, [_P, _I32, _I64, _I32, _P, _P, _P, _P]),
     "rnsmx_decode_garner": (_I32, [_P, _I64, ctypes.POINTER(Moduli), _P, _P]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class NativeError(RuntimeError):

@@ -333,11 +333,13 @@ class HipRNSBackend:
     # ------------------------------------------------------------------
     def create_workspace(self, *, device: torch.device, channels: int, m: int, n: int,
                          k: int | None = None) -> RNSWorkspace:
-        scratch_bytes = 0
+        # zero-filled: the library's K-split arrival counters at its start
+        # must be zero at first use (every call leaves them zero)
+        scratch_bytes = _native.SPLIT_TICKETS * 4
         if k is not None:
-            scratch_bytes = int(self._lib.rnsmx_prepared_workspace_bytes(m, k, channels))
+            scratch_bytes = self._prepared_workspace_bytes(m, k, n, channels, None)
         return RNSWorkspace(
-            accumulators=torch.empty((max(scratch_bytes, 0),), dtype=torch.uint8, device=device),
+            accumulators=torch.zeros((max(scratch_bytes, 0),), dtype=torch.uint8, device=device),
             output=torch.empty((m, n), dtype=torch.int64, device=device),
             channels=channels,
             m=m,
@@ -352,11 +354,14 @@ class HipRNSBackend:
         if workspace.accumulators.device != device or workspace.output.device != device:
             raise ValueError("workspace device does not match operation")
 
-    def _prepared_workspace_bytes(self, m: int, k: int, channels: int) -> int:
-        key = (m, k, channels)
+    def _prepared_workspace_bytes(self, m: int, k: int, n: int, channels: int, plan) -> int:
+        key = (m, k, n, channels, None if plan is None else plan.as_tuple())
         nbytes = self._ws_bytes.get(key)
         if nbytes is None:
-            nbytes = int(self._lib.rnsmx_prepared_workspace_bytes(m, k, channels))
+            nbytes = int(self._lib.rnsmx_prepared_workspace_bytes(
+                m, k, n, channels, None if plan is None else ctypes.byref(plan)))
+            if nbytes < 0:
+                raise ValueError("bad workspace shape")
             self._ws_bytes[key] = nbytes
         return nbytes
 
@@ -365,7 +370,8 @@ class HipRNSBackend:
         if nbytes < 0:
             raise ValueError("bad workspace size")
         if workspace.accumulators.numel() < nbytes:
-            workspace.accumulators = torch.empty(
+            # zero-filled for the arrival counters (see create_workspace)
+            workspace.accumulators = torch.zeros(
                 (nbytes,), dtype=torch.uint8, device=workspace.output.device)
         return workspace.accumulators
 
@@ -538,19 +544,21 @@ class HipRNSBackend:
                               lut_channels: int = 0, workspace: RNSWorkspace | None = None,
                               out: torch.Tensor | None = None, a_scale: torch.Tensor | None = None,
                               w_scale: torch.Tensor | None = None,
-                              bias: torch.Tensor | None = None) -> torch.Tensor:
+                              bias: torch.Tensor | None = None, plan=None) -> torch.Tensor:
         """a [M, K] int8/16/32 x prepared B -> exact int64 [M, N]
         (``cuda_backend.py:514-539``), returned as ``workspace.output``.
 
         With ``out`` (float32/float16/bfloat16 [M, N]) plus ``a_scale`` [1]
         and ``w_scale`` [N] (and optional ``bias`` [N], all float32), the
         epilogue instead writes ``((float)x * a_scale) * w_scale + bias`` in
-        ``out``'s dtype, the float chain of ``RNSLinear.forward``."""
+        ``out``'s dtype, the float chain of ``RNSLinear.forward``.
+        ``plan`` (kind, mb, nb, ks[, splits]) forces a kernel for this call
+        (tuning and tests; results do not depend on it)."""
         return self._prepared_call(a, prepared_weight, lut_channels, workspace, None,
-                                   out, a_scale, w_scale, bias)
+                                   out, a_scale, w_scale, bias, plan)
 
     def _prepared_call(self, a, prepared, lut_channels, workspace, adaptive, out,
-                       a_scale, w_scale, bias):
+                       a_scale, w_scale, bias, plan=None):
         self._check_activation(a, prepared)
         if lut_channels not in (0, 1, 2):
             raise ValueError("lut_channels must be 0, 1 or 2")
@@ -561,7 +569,8 @@ class HipRNSBackend:
         if workspace is None:
             workspace = self.create_workspace(device=device, channels=channels, m=m, n=n, k=k)
         self._check_workspace(workspace, channels=channels, m=m, n=n, device=device)
-        scratch = self._scratch(workspace, self._prepared_workspace_bytes(m, k, channels))
+        plan = _native.make_plan(plan)
+        scratch = self._scratch(workspace, self._prepared_workspace_bytes(m, k, n, channels, plan))
         epi = None
         target = workspace.output
         if out is not None:
@@ -587,8 +596,8 @@ class HipRNSBackend:
         _native.check(self._lib.rnsmx_matmul_prepared_fused(
             _aligned(a).data_ptr(), _native.dtype_code(a.dtype), m, k, n,
             prepared.packed.data_ptr(), consts.native_ref, consts.compact_lut.data_ptr(),
-            lut_channels, adaptive, epi, scratch.data_ptr(), scratch.numel(),
-            target.data_ptr(), _stream_handle(device)))
+            lut_channels, adaptive, epi, None if plan is None else ctypes.byref(plan),
+            scratch.data_ptr(), scratch.numel(), target.data_ptr(), _stream_handle(device)))
         return target
 
     def encode_activations(self, a: torch.Tensor, prepared_weight: PreparedRNSWeight,
@@ -697,7 +706,7 @@ class HipRNSBackend:
                                        *, lut_channels: int = 2,
                                        workspace_by_channels: dict | None = None,
                                        return_metadata: bool = False, out=None, a_scale=None,
-                                       w_scale=None, bias=None):
+                                       w_scale=None, bias=None, plan=None):
         """Adaptive prefix chosen on the device (no host synchronisation).
         The full-set workspace is used for every prefix; the output is exact
         whenever the bound fits the full set, and the metadata reports the
@@ -711,7 +720,7 @@ class HipRNSBackend:
                                     meta.data_ptr())
         self._stats["adaptive_selections"] += 1
         result = self._prepared_call(a, full, lut_channels, workspace, ctypes.byref(adaptive),
-                                     out, a_scale, w_scale, bias)
+                                     out, a_scale, w_scale, bias, plan)
         if return_metadata:
             return result, AdaptiveMetadata(meta, prepared.full_moduli)
         return result

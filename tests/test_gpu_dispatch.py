@@ -3,8 +3,10 @@ stream vs MFMA (M <= 16; M <= 64 unless K > 1024 with over 1024 stream
 tiles; M <= 128 with at most 512 stream tiles), the LDS kernel's K >= 2048 gate and its
 full-round rule below it (256 tiles of 256 x 64 vs 2.25 rounds), ragged N
 and K, K that the LDS kernel cannot take (K % 256 != 0), and the MFMA
-kernel's tile height (32, 48 or 64 rows, fewest rows per CU).  Every output
-must equal the exact product."""
+kernel's tile height (32, 48 or 64 rows, fewest rows per CU), and the K
+split over workgroups for few tiles and long K (and none where it loses:
+the BASELINE shapes).  Every output must equal the exact product, on two
+calls in a row (the split's arrival counters return to zero)."""
 import pytest
 import torch
 
@@ -42,6 +44,15 @@ SHAPES = [
     (250, 768, 2290),    # 48 x 64 tiles with ragged M and N
     (384, 768, 2304),    # MFMA 64 x 64 tiles: 216 (48 rows would need 288)
     (256, 768, 4608),    # no height fits one round: 48 rows (2 rounds) ties 32 (3)
+    (4096, 768, 768),    # C4 out_proj: MFMA 64 x 64 tiles
+    # K split over workgroups
+    (1, 16384, 768),     # decode: 8 one-wave splits
+    (3, 4096, 770),      # decode: 4 splits, ragged N
+    (1, 2048, 768),      # 2 splits would be the cap: 4 waves in one workgroup instead
+    (256, 8192, 256),    # MFMA 32 x 64, 8 splits
+    (250, 4096, 760),    # MFMA, 4 splits, ragged M and N
+    (512, 8192, 512),    # 128 tiles, K >= 8192: 2 splits
+    (2048, 16384, 768),  # 384 tiles of 64 x 64, 2 splits
 ]
 
 
@@ -51,6 +62,8 @@ def test_auto_choice_is_exact(backend, m, k, n):
     w = torch.randint(-127, 128, (n, k), generator=gen, device=DEV, dtype=torch.int8)
     a = torch.randint(-127, 128, (m, k), generator=gen, device=DEV, dtype=torch.int8)
     prepared = backend.prepare_weight_nk(w, DENSE4)
-    out = backend.matmul_prepared_fused(a, prepared)
+    ws = backend.create_workspace(device=torch.device(DEV), channels=4, m=m, n=n, k=k)
     want = a.double() @ w.double().t()  # exact: integer sums below 2^53
-    assert torch.equal(out.double(), want)
+    for _ in range(2):
+        out = backend.matmul_prepared_fused(a, prepared, workspace=ws)
+        assert torch.equal(out.double(), want)

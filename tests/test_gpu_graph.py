@@ -39,9 +39,11 @@ def capture(fn):
     return graph, result
 
 
-# (m, k, n): the stream kernel (decode), the MFMA kernel (C2 headline shape)
-# and the LDS-staged kernel (256 full-round tiles)
-@pytest.mark.parametrize("m,k,n", [(1, 768, 2304), (256, 768, 2304), (1024, 1024, 4096)])
+# (m, k, n): the stream kernel (decode), the MFMA kernel (C2 headline shape),
+# the LDS-staged kernel (256 full-round tiles), and K split over workgroups
+# (stream and MFMA: their arrival counters must return to zero every replay)
+@pytest.mark.parametrize("m,k,n", [(1, 768, 2304), (256, 768, 2304), (1024, 1024, 4096),
+                                   (1, 8192, 768), (256, 8192, 256)])
 def test_graph_replays_fused_gemm(backend, m, k, n):
     gen = torch.Generator(device=DEV).manual_seed(m + k)
     w = torch.randint(-127, 128, (n, k), generator=gen, device=DEV, dtype=torch.int8)

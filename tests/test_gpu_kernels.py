@@ -1,8 +1,9 @@
-"""Every GEMM kernel instance, forced through rnsmx_set_gemm_override, on
-ragged shapes: raw int8 activations (one A matrix shared by all channels)
-and residue-plane activations (int16 sources, K not a multiple of 16), full
-and adaptive channel prefixes, integer and float epilogues.  Each output must
-equal the exact int64 product (or the CPU oracle) bit for bit."""
+"""Every GEMM kernel instance, forced through a per-call plan, on ragged
+shapes: raw int8 activations (one A matrix shared by all channels) and
+residue-plane activations (int16 sources, K not a multiple of 16), full and
+adaptive channel prefixes, integer and float epilogues, with and without K
+split over workgroups.  Each output must equal the exact int64 product (or
+the CPU oracle) bit for bit."""
 import numpy as np
 import pytest
 import torch
@@ -42,24 +43,16 @@ def mfma_cases():
             for p in depths]
 
 
-@pytest.fixture
-def override(backend):
-    lib = backend._lib
-
-    def set_(kind, mb=0, nb=0, ks=0):
-        _native.check(lib.rnsmx_set_gemm_override(kind, mb, nb, ks))
-
-    yield set_
-    _native.check(lib.rnsmx_set_gemm_override(0, 0, 0, 0))
-
-
 def amax_for(mods, k):
     # largest int8 magnitude whose worst-case product the set still holds
     half = (np.prod(np.array(mods, dtype=object)) - 1) // 2
     return int(min(127, max(1, int((half // k) ** 0.5))))
 
 
-def run_case(backend, mods, m, k, n, dtype=torch.int8, seed=0, adaptive=False, out_dtype=None):
+def run_case(backend, mods, m, k, n, dtype=torch.int8, seed=0, adaptive=False, out_dtype=None,
+             plan=None, repeat=1):
+    """One product through the plan; with repeat > 1 the same call runs
+    again on one workspace (the K-split counters must return to zero)."""
     gen = torch.Generator().manual_seed(seed)
     amax = amax_for(mods, k)
     if adaptive:
@@ -69,22 +62,29 @@ def run_case(backend, mods, m, k, n, dtype=torch.int8, seed=0, adaptive=False, o
     want = ro.exact_matmul(a.numpy(), b.numpy())
     if adaptive:
         prepared = backend.prepare_weight_adaptive(b.to(DEV), mods, min_channels=2)
-        out, meta = backend.matmul_prepared_adaptive_fused(a.to(DEV), prepared, lut_channels=1,
-                                                          return_metadata=True)
-        assert meta["channels"] < len(mods)
-        np.testing.assert_array_equal(out.cpu().numpy(), want)
+        ws = {len(mods): backend.create_workspace(device=torch.device(DEV), channels=len(mods),
+                                                  m=m, n=n, k=k)}
+        for _ in range(repeat):
+            out, meta = backend.matmul_prepared_adaptive_fused(a.to(DEV), prepared, lut_channels=1,
+                                                              workspace_by_channels=ws,
+                                                              return_metadata=True, plan=plan)
+            assert meta["channels"] < len(mods)
+            np.testing.assert_array_equal(out.cpu().numpy(), want)
         return
     prepared = backend.prepare_weight(b.to(DEV), mods)
     if out_dtype is None:
-        out = backend.matmul_prepared_fused(a.to(DEV), prepared, lut_channels=min(2, len(mods)))
-        np.testing.assert_array_equal(out.cpu().numpy(), want)
+        ws = backend.create_workspace(device=torch.device(DEV), channels=len(mods), m=m, n=n, k=k)
+        for _ in range(repeat):
+            out = backend.matmul_prepared_fused(a.to(DEV), prepared, lut_channels=min(2, len(mods)),
+                                                workspace=ws, plan=plan)
+            np.testing.assert_array_equal(out.cpu().numpy(), want)
         return
     a_scale = torch.tensor([0.0123], dtype=torch.float32)
     w_scale = torch.rand((n,), generator=gen, dtype=torch.float32) * 0.01
     bias = torch.randn((n,), generator=gen, dtype=torch.float32)
     out = torch.empty((m, n), dtype=out_dtype, device=DEV)
     backend.matmul_prepared_fused(a.to(DEV), prepared, out=out, a_scale=a_scale.to(DEV),
-                                  w_scale=w_scale.to(DEV), bias=bias.to(DEV))
+                                  w_scale=w_scale.to(DEV), bias=bias.to(DEV), plan=plan)
     # the op order of RNSLinear's output chain, on the CPU (IEEE f32, no FMA)
     ref = ((torch.from_numpy(want).float() * a_scale.view(1, 1)) * w_scale.unsqueeze(0) + bias)
     bits = torch.int32 if out_dtype == torch.float32 else torch.int16
@@ -92,83 +92,81 @@ def run_case(backend, mods, m, k, n, dtype=torch.int8, seed=0, adaptive=False, o
 
 
 @pytest.mark.parametrize("r,mb,nb,ks", stream_cases())
-def test_stream_kernel_instances(backend, override, r, mb, nb, ks):
-    override(1, mb, nb, ks)
+def test_stream_kernel_instances(backend, r, mb, nb, ks):
+    plan = (1, mb, nb, ks)
     mods = SETS[r]
     # raw int8 A (K % 16 == 0), K tail inside the last 64-byte step
-    run_case(backend, mods, 16 * mb * 2 + 3, 208, 16 * nb * 3 + 5, seed=r * 1000 + mb * 10 + nb)
+    run_case(backend, mods, 16 * mb * 2 + 3, 208, 16 * nb * 3 + 5, seed=r * 1000 + mb * 10 + nb, plan=plan)
     # residue-plane A: K % 16 != 0 and int16 sources
-    run_case(backend, mods, 16 * mb + 1, 100, 16 * nb + 7, seed=ks)
-    run_case(backend, mods, 7, 150, 37, dtype=torch.int16, seed=ks + 1)
+    run_case(backend, mods, 16 * mb + 1, 100, 16 * nb + 7, seed=ks, plan=plan)
+    run_case(backend, mods, 7, 150, 37, dtype=torch.int16, seed=ks + 1, plan=plan)
 
 
 @pytest.mark.parametrize("r,ks", [(r, ks) for r in (3, 4) for ks in (1, 2, 4)])
-def test_wide_stream_kernel_instances(backend, override, r, ks):
+def test_wide_stream_kernel_instances(backend, r, ks):
     # 8-step chunks: several chunks per wave, the last past K
-    override(4, 1, 1, ks)
+    plan = (4, 1, 1, ks)
     mods = SETS[r]
-    run_case(backend, mods, 19, 64 * (8 * ks * 2 + 3) + 16, 16 * 3 + 5, seed=r * 10 + ks)
-    run_case(backend, mods, 5, 208, 21, seed=ks)
-    run_case(backend, mods, 7, 150, 37, dtype=torch.int16, seed=ks + 1)
+    run_case(backend, mods, 19, 64 * (8 * ks * 2 + 3) + 16, 16 * 3 + 5, seed=r * 10 + ks, plan=plan)
+    run_case(backend, mods, 5, 208, 21, seed=ks, plan=plan)
+    run_case(backend, mods, 7, 150, 37, dtype=torch.int16, seed=ks + 1, plan=plan)
 
 
 @pytest.mark.parametrize("r,mb,p", [(r, mb, p) for r in (3, 4) for mb, p in ((2, 4), (3, 4), (4, 3), (4, 4))])
-def test_three_wave_mfma_kernel_instances(backend, override, r, mb, p):
+def test_three_wave_mfma_kernel_instances(backend, r, mb, p):
     # 48-column tiles: ragged N around multiples of 48 and 16, several trips
     # round the ring, the last partly past K
-    override(5, mb, 1, p)
+    plan = (5, mb, 1, p)
     mods = SETS[r]
-    run_case(backend, mods, 16 * mb * 2 + 9, 336, 48 * 2 + 11, seed=r * 100 + mb)
-    run_case(backend, mods, 16 * mb + 5, 64 * (2 * p + 1) + 16, 48 + 3, seed=p)
-    run_case(backend, mods, 16 * mb + 3, 768, 2304, seed=r)
-    run_case(backend, mods, 3, 320, 90, seed=7, adaptive=True)
+    run_case(backend, mods, 16 * mb * 2 + 9, 336, 48 * 2 + 11, seed=r * 100 + mb, plan=plan)
+    run_case(backend, mods, 16 * mb + 5, 64 * (2 * p + 1) + 16, 48 + 3, seed=p, plan=plan)
+    run_case(backend, mods, 16 * mb + 3, 768, 2304, seed=r, plan=plan)
+    run_case(backend, mods, 3, 320, 90, seed=7, adaptive=True, plan=plan)
 
 
 @pytest.mark.parametrize("r,mb,nb,p", mfma_cases())
-def test_mfma_kernel_instances(backend, override, r, mb, nb, p):
-    override(2, mb, nb, p)
+def test_mfma_kernel_instances(backend, r, mb, nb, p):
+    plan = (2, mb, nb, p)
     mods = SETS[r]
-    run_case(backend, mods, 16 * mb * 2 + 9, 336, 64 * nb * 2 + 11, seed=r * 100 + mb)
+    run_case(backend, mods, 16 * mb * 2 + 9, 336, 64 * nb * 2 + 11, seed=r * 100 + mb, plan=plan)
     # several trips round the load ring, the last one partly past K
-    run_case(backend, mods, 16 * mb + 5, 64 * (2 * p + 1) + 16, 64 * nb + 3, seed=p)
-    run_case(backend, mods, 16 * mb + 3, 100, 64 * nb + 1, seed=r)
-    run_case(backend, mods, 40, 150, 70, dtype=torch.int16, seed=r + 1)
+    run_case(backend, mods, 16 * mb + 5, 64 * (2 * p + 1) + 16, 64 * nb + 3, seed=p, plan=plan)
+    run_case(backend, mods, 16 * mb + 3, 100, 64 * nb + 1, seed=r, plan=plan)
+    run_case(backend, mods, 40, 150, 70, dtype=torch.int16, seed=r + 1, plan=plan)
 
 
 @pytest.mark.parametrize("m,k,n", [(256 * 2 + 37, 256, 64 * 3 + 5), (300, 512, 100), (17, 1024, 64),
                                    (256, 768, 2304)])
-def test_lds_kernel(backend, override, m, k, n):
+def test_lds_kernel(backend, m, k, n):
     # 256 x 64 tiles, four stages of direct-to-LDS loads: ragged M and N,
     # one and several trips round the stages
-    override(3)
-    run_case(backend, DENSE4, m, k, n, seed=m + k)
+    run_case(backend, DENSE4, m, k, n, seed=m + k, plan=(3, 0, 0, 0))
 
 
-def test_lds_kernel_rejects_unfit_shapes(backend, override):
-    override(3)
+def test_lds_kernel_rejects_unfit_shapes(backend):
+    lds = (3, 0, 0, 0)
     prepared = backend.prepare_weight(torch.ones((320, 16), dtype=torch.int8, device=DEV), DENSE4)
     with pytest.raises(ValueError, match="no GEMM kernel"):  # K not a multiple of 256
-        backend.matmul_prepared_fused(torch.ones((4, 320), dtype=torch.int8, device=DEV), prepared)
+        backend.matmul_prepared_fused(torch.ones((4, 320), dtype=torch.int8, device=DEV), prepared, plan=lds)
     prepared = backend.prepare_weight(torch.ones((256, 16), dtype=torch.int8, device=DEV), SETS[3])
     with pytest.raises(ValueError, match="no GEMM kernel"):  # 3-channel capacity
-        backend.matmul_prepared_fused(torch.ones((4, 256), dtype=torch.int8, device=DEV), prepared)
+        backend.matmul_prepared_fused(torch.ones((4, 256), dtype=torch.int8, device=DEV), prepared, plan=lds)
 
 
 @pytest.mark.parametrize("kind,mb,nb,ks,k", [(1, 1, 1, 4, 320), (1, 1, 2, 2, 320), (1, 2, 1, 1, 320),
                                              (2, 8, 2, 0, 320), (2, 2, 1, 0, 320), (3, 0, 0, 0, 512)])
-def test_kernel_adaptive_prefix(backend, override, kind, mb, nb, ks, k):
-    override(kind, mb, nb, ks)
-    run_case(backend, DENSE4, 50, k, 90, seed=5, adaptive=True)
+def test_kernel_adaptive_prefix(backend, kind, mb, nb, ks, k):
+    plan = (kind, mb, nb, ks)
+    run_case(backend, DENSE4, 50, k, 90, seed=5, adaptive=True, plan=plan)
     # up to 4 raw rows: the row norms are summed inside the GEMM
-    run_case(backend, DENSE4, 3, k, 90, seed=6, adaptive=True)
+    run_case(backend, DENSE4, 3, k, 90, seed=6, adaptive=True, plan=plan)
 
 
 @pytest.mark.parametrize("kind,mb,nb,ks", [(1, 1, 2, 2), (1, 4, 1, 4), (1, 2, 1, 1), (2, 8, 2, 0), (2, 2, 1, 0),
                                            (3, 0, 0, 0)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
-def test_kernel_float_epilogue(backend, override, kind, mb, nb, ks, out_dtype):
-    override(kind, mb, nb, ks)
-    run_case(backend, DENSE4, 45, 256, 77, seed=9, out_dtype=out_dtype)
+def test_kernel_float_epilogue(backend, kind, mb, nb, ks, out_dtype):
+    run_case(backend, DENSE4, 45, 256, 77, seed=9, out_dtype=out_dtype, plan=(kind, mb, nb, ks))
 
 
 def test_prepared_residues_view_matches_encode(backend):
@@ -183,8 +181,70 @@ def test_prepared_residues_view_matches_encode(backend):
 
 
 @pytest.mark.parametrize("kind,mb,nb,ks", [(2, 3, 3, 0), (2, 8, 2, 8)])
-def test_override_rejects_unbuilt_tile(backend, override, kind, mb, nb, ks):
-    override(kind, mb, nb, ks)
+def test_plan_rejects_unbuilt_tile(backend, kind, mb, nb, ks):
     prepared = backend.prepare_weight(torch.ones((64, 16), dtype=torch.int8, device=DEV), DENSE4)
     with pytest.raises(ValueError, match="no GEMM kernel"):
-        backend.matmul_prepared_fused(torch.ones((4, 64), dtype=torch.int8, device=DEV), prepared)
+        backend.matmul_prepared_fused(torch.ones((4, 64), dtype=torch.int8, device=DEV), prepared,
+                                      plan=(kind, mb, nb, ks))
+
+
+# --------------------------------------------------------------------------
+# K split over workgroups: partial sums reduced to residues, exchanged, and
+# reconstructed by the last workgroup of each tile
+# --------------------------------------------------------------------------
+SPLIT_PLANS = [
+    # (kind, mb, nb, ks, splits)
+    (1, 1, 1, 1, 2), (1, 1, 1, 1, 3), (1, 1, 1, 1, 12), (1, 2, 1, 1, 4), (1, 2, 1, 1, 5),
+    (4, 1, 1, 1, 3),
+    (2, 2, 1, 4, 2), (2, 3, 1, 4, 2), (2, 4, 1, 3, 3), (2, 4, 1, 4, 5), (2, 2, 1, 3, 2),
+    (5, 2, 1, 4, 2), (5, 3, 1, 4, 3), (5, 4, 1, 4, 2),
+]
+
+
+@pytest.mark.parametrize("plan", SPLIT_PLANS, ids=lambda p: "k%d_%dx%d_ks%d_s%d" % p)
+@pytest.mark.parametrize("r", [3, 4])
+def test_split_k_instances(backend, plan, r):
+    mods = SETS[r]
+    kind, mb, nb = plan[0], plan[1], plan[2]
+    cols = 48 * nb if kind == 5 else (16 * nb if kind in (1, 4) else 64 * nb)
+    # ragged M and N; K with a tail inside the last step and several steps
+    # per split; each call twice on one workspace (the counters reset)
+    run_case(backend, mods, 16 * mb * 2 + 3, 64 * 13 + 16, cols * 3 + 5, seed=r + mb, plan=plan, repeat=2)
+    # more splits than K steps: the split count shrinks to the steps
+    run_case(backend, mods, 16 * mb + 1, 160, cols + 7, seed=r * 7, plan=plan)
+    # residue-plane activations (int16 sources)
+    if kind != 5:
+        run_case(backend, mods, 9, 200, cols + 3, dtype=torch.int16, seed=r + 2, plan=plan)
+
+
+@pytest.mark.parametrize("m,k,n,splits", [(512 + 37, 1024, 64 * 5 + 3, 2), (300, 2048, 100, 3),
+                                          (256, 4096, 64, 4), (17, 512, 64, 2)])
+def test_split_k_lds_kernel(backend, m, k, n, splits):
+    # whole trips of four stages per split
+    run_case(backend, DENSE4, m, k, n, seed=m + splits, plan=(3, 0, 0, 0, splits), repeat=2)
+
+
+@pytest.mark.parametrize("plan", [(1, 1, 1, 1, 4), (2, 3, 1, 4, 2), (5, 2, 1, 4, 2), (3, 0, 0, 0, 2)])
+def test_split_k_adaptive_prefix(backend, plan):
+    k = 512
+    run_case(backend, DENSE4, 50, k, 90, seed=15, adaptive=True, plan=plan, repeat=2)
+    run_case(backend, DENSE4, 3, k, 90, seed=16, adaptive=True, plan=plan)
+
+
+@pytest.mark.parametrize("plan", [(1, 1, 1, 1, 3), (2, 4, 1, 3, 2), (3, 0, 0, 0, 2)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_split_k_float_epilogue(backend, plan, out_dtype):
+    run_case(backend, DENSE4, 45, 512, 77, seed=19, out_dtype=out_dtype, plan=plan)
+
+
+def test_split_k_rejects_unfit_plans(backend):
+    prepared = backend.prepare_weight(torch.ones((256, 40), dtype=torch.int8, device=DEV), SETS[6])
+    with pytest.raises(ValueError, match="cannot split"):  # more than 4 channels
+        backend.matmul_prepared_fused(torch.ones((4, 256), dtype=torch.int8, device=DEV), prepared,
+                                      plan=(2, 2, 1, 3, 2))
+    prepared = backend.prepare_weight(torch.ones((256, 40), dtype=torch.int8, device=DEV), DENSE4)
+    a = torch.ones((4, 256), dtype=torch.int8, device=DEV)
+    # stream workgroups of several waves; tiles built without the exchange
+    for plan in ((1, 1, 1, 2, 2), (1, 1, 2, 1, 2), (1, 4, 1, 1, 2), (2, 4, 2, 3, 2), (2, 8, 2, 3, 2)):
+        with pytest.raises(ValueError, match="cannot split"):
+            backend.matmul_prepared_fused(a, prepared, plan=plan)

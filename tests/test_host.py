@@ -43,41 +43,52 @@ def test_abi_struct_layout_matches_header():
 
 
 def gemm_plan(m, n, k, channels=4, raw_a=1):
-    out = [ctypes.c_int32() for _ in range(4)]
-    _native.check(_native.lib().rnsmx_gemm_plan(m, n, k, channels, raw_a, *[ctypes.byref(v) for v in out]))
-    return tuple(v.value for v in out)
+    out = _native.Plan()
+    _native.check(_native.lib().rnsmx_gemm_plan(m, n, k, channels, raw_a, ctypes.byref(out)))
+    return out.as_tuple()
 
 
-# (M, N, K, channels) -> (kind, mb, nb, ks): kind 1 stream, 2 MFMA, 3 LDS-staged,
-# 4 stream with 8-step chunks, 5 MFMA with 48-column tiles
+# (M, N, K, channels) -> (kind, mb, nb, ks, splits): kind 1 stream, 2 MFMA,
+# 3 LDS-staged, 4 stream with 8-step chunks, 5 MFMA with 48-column tiles;
+# splits: workgroups sharing each output tile's K range
 PLANS = [
-    ((1, 2304, 768, 4), (1, 1, 1, 3)),       # decode: stream, 3 waves split 12 K steps
-    ((64, 2304, 768, 4), (1, 1, 1, 3)),      # stream up to 64 rows at short K
-    ((96, 2304, 768, 4), (1, 2, 1, 3)),      # stream: 432 tiles of 32 x 16
-    ((128, 768, 768, 4), (1, 2, 1, 3)),      # stream: 192 tiles
-    ((128, 2304, 768, 4), (5, 2, 1, 4)),     # 576 stream tiles: MFMA, 32 x 48 (192 tiles)
-    ((256, 1536, 768, 4), (5, 2, 1, 4)),     # 32 x 48 fills 256 CUs (32 x 64: 192)
-    ((256, 3072, 768, 4), (5, 4, 1, 4)),     # 64 x 48, 256 tiles, ties 64 x 64 on rows
-    ((256, 3072, 1024, 4), (5, 4, 1, 4)),
-    ((128, 2304, 768, 6), (2, 2, 1, 4)),     # 48-column tiles only up to 4 channels
-    ((224, 2304, 768, 4), (2, 2, 1, 4)),     # 252 tiles of 32 rows: one round
-    ((256, 2304, 768, 4), (2, 3, 1, 4)),     # headline: 216 tiles of 48 rows
-    ((320, 2304, 768, 4), (2, 3, 1, 4)),     # 252 tiles of 48 rows
-    ((384, 2304, 768, 4), (2, 4, 1, 0)),     # 64 rows (216 tiles) tie 32 rows (2 rounds)
-    ((256, 4608, 768, 4), (2, 3, 1, 4)),     # no height fits one round: 48 rows (2 rounds)
-    ((256, 2304, 768, 6), (2, 4, 1, 0)),     # no 48-row tile past 4 channels
-    ((4096, 2304, 768, 4), (2, 4, 1, 0)),    # C4 QKV: over 512 tiles at every height
-    ((1, 12288, 4096, 4), (4, 1, 1, 4)),     # C5 decode: stream with 8-step chunks
-    ((16, 12288, 4096, 4), (4, 1, 1, 4)),    # long K, 16 rows: stream, 8-step chunks
-    ((16, 2048, 2048, 4), (1, 1, 1, 4)),     # K = 2048: 4-step chunks
-    ((1, 12288, 4096, 6), (1, 1, 1, 4)),     # 8-step chunks only up to 4 channels
-    ((32, 12288, 4096, 4), (2, 2, 1, 4)),    # long K, wide N: MFMA, 32 rows
-    ((48, 12288, 4096, 4), (2, 3, 1, 4)),
-    ((64, 12288, 4096, 4), (2, 4, 1, 0)),
-    ((128, 12288, 4096, 4), (2, 4, 1, 0)),   # 32 rows would need 768 tiles
-    ((512, 12288, 4096, 4), (3, 0, 0, 0)),   # LDS-staged, 256 x 64 tiles
-    ((2048, 12288, 4096, 4), (3, 0, 0, 0)),
-    ((2048, 12288, 4096, 6), (2, 4, 1, 0)),  # the LDS kernel holds at most 4 channels
+    ((1, 2304, 768, 4), (1, 1, 1, 3, 1)),       # decode: stream, 3 waves split 12 K steps
+    ((64, 2304, 768, 4), (1, 1, 1, 3, 1)),      # stream up to 64 rows at short K
+    ((96, 2304, 768, 4), (1, 2, 1, 3, 1)),      # stream: 432 tiles of 32 x 16
+    ((128, 768, 768, 4), (1, 2, 1, 3, 1)),      # stream: 192 tiles
+    ((128, 2304, 768, 4), (5, 2, 1, 4, 1)),     # 576 stream tiles: MFMA, 32 x 48 (192 tiles)
+    ((256, 1536, 768, 4), (5, 2, 1, 4, 1)),     # 32 x 48 fills 256 CUs (32 x 64: 192)
+    ((256, 3072, 768, 4), (5, 4, 1, 4, 1)),     # 64 x 48, 256 tiles, ties 64 x 64 on rows
+    ((256, 3072, 1024, 4), (5, 4, 1, 4, 1)),
+    ((128, 2304, 768, 6), (2, 2, 1, 4, 1)),     # 48-column tiles only up to 4 channels
+    ((224, 2304, 768, 4), (2, 2, 1, 4, 1)),     # 252 tiles of 32 rows: one round
+    ((256, 2304, 768, 4), (2, 3, 1, 4, 1)),     # headline: 216 tiles of 48 rows
+    ((320, 2304, 768, 4), (2, 3, 1, 4, 1)),     # 252 tiles of 48 rows
+    ((384, 2304, 768, 4), (2, 4, 1, 0, 1)),     # 64 rows (216 tiles) tie 32 rows (2 rounds)
+    ((256, 4608, 768, 4), (2, 3, 1, 4, 1)),     # no height fits one round: 48 rows (2 rounds)
+    ((256, 2304, 768, 6), (2, 4, 1, 0, 1)),     # no 48-row tile past 4 channels
+    ((4096, 2304, 768, 4), (2, 4, 1, 0, 1)),    # C4 QKV: over 512 tiles at every height
+    ((1, 12288, 4096, 4), (4, 1, 1, 4, 1)),     # C5 decode: stream with 8-step chunks
+    ((16, 12288, 4096, 4), (4, 1, 1, 4, 1)),    # long K, 16 rows: stream, 8-step chunks
+    ((16, 2048, 2048, 4), (1, 1, 1, 4, 1)),     # K = 2048: 4-step chunks
+    ((1, 12288, 4096, 6), (1, 1, 1, 4, 1)),     # 8-step chunks only up to 4 channels
+    ((32, 12288, 4096, 4), (2, 2, 1, 4, 1)),    # long K, wide N: MFMA, 32 rows
+    ((48, 12288, 4096, 4), (2, 3, 1, 4, 1)),
+    ((64, 12288, 4096, 4), (2, 4, 1, 0, 1)),
+    ((128, 12288, 4096, 4), (2, 4, 1, 0, 1)),   # 32 rows would need 768 tiles
+    ((512, 12288, 4096, 4), (3, 0, 0, 0, 1)),   # LDS-staged, 256 x 64 tiles
+    ((2048, 12288, 4096, 4), (3, 0, 0, 0, 1)),
+    ((2048, 12288, 4096, 6), (2, 4, 1, 0, 1)),  # the LDS kernel holds at most 4 channels
+    # K split over workgroups: few tiles and long K
+    ((1, 768, 16384, 4), (4, 1, 1, 1, 8)),    # decode: 8 one-wave workgroups per 16 x 16 tile
+    ((1, 768, 4096, 4), (4, 1, 1, 1, 4)),     # 16 K steps per split: 4 splits
+    ((1, 768, 2048, 4), (1, 1, 1, 4, 1)),     # 2 one-wave splits lose to 4 waves in one workgroup
+    ((1, 2304, 16384, 4), (4, 1, 1, 4, 1)),   # 144 stream tiles: no split
+    ((256, 256, 8192, 4), (2, 2, 1, 4, 8)),   # 32 tiles: 8 splits (256 workgroups)
+    ((256, 768, 4096, 4), (2, 2, 1, 4, 4)),   # 96 tiles: at most 512 workgroups -> 4
+    ((512, 512, 8192, 4), (2, 2, 1, 4, 2)),   # 128 tiles, K >= 8192: 2
+    ((2048, 768, 16384, 4), (2, 4, 1, 0, 2)),
+    ((256, 256, 8192, 6), (2, 2, 1, 4, 1)),   # the exchange holds at most 4 channels
 ]
 
 
@@ -90,14 +101,7 @@ def test_gemm_plan_rules(shape, plan):
     assert gemm_plan(m, n, k, channels) == plan
 
 
-def test_gemm_plan_reports_override_and_rejects_bad_shapes():
-    lib = _native.lib()
-    _native.check(lib.rnsmx_set_gemm_override(2, 2, 2, 3))
-    try:
-        assert gemm_plan(256, 2304, 768) == (2, 2, 2, 3)
-    finally:
-        _native.check(lib.rnsmx_set_gemm_override(0, 0, 0, 0))
-    assert gemm_plan(256, 2304, 768) == (2, 3, 1, 4)
+def test_gemm_plan_rejects_bad_shapes():
     # residue-plane activations (K not a multiple of 16): never the LDS kernel
     assert gemm_plan(2048, 12288, 4104, raw_a=0)[0] == 2
     for bad in ((0, 8, 8, 4), (8, 8, 8, 1), (8, 8, 8, 11)):
@@ -152,11 +156,20 @@ def test_native_moduli_errors(bad, exc):
 
 def test_workspace_bytes_queries():
     lib = _native.lib()
-    assert lib.rnsmx_prepared_workspace_bytes(256, 768, 4) >= 4 * 256 * 768 + 8 * 256
-    assert lib.rnsmx_prepared_workspace_bytes(1, 100, 3) >= 3 * 128 + 8
-    assert lib.rnsmx_fused_workspace_bytes(16, 768, 2304, 4) >= 4 * 2304 * 768
-    assert lib.rnsmx_fused_workspace_bytes(16, 100, 37, 3) >= 3 * 37 * 128 + 3 * 16 * 128
-    assert lib.rnsmx_prepared_workspace_bytes(-1, 5, 4) == -1
+    tickets = 4 * _native.SPLIT_TICKETS
+    # counters + residue planes of A (int16 sources) + row norms
+    assert lib.rnsmx_prepared_workspace_bytes(256, 768, 2304, 4, None) >= tickets + 4 * 256 * 768 + 8 * 256
+    assert lib.rnsmx_prepared_workspace_bytes(1, 100, 37, 3, None) >= tickets + 3 * 128 + 8
+    assert lib.rnsmx_fused_workspace_bytes(16, 768, 2304, 4) >= tickets + 4 * 2304 * 768
+    assert lib.rnsmx_fused_workspace_bytes(16, 100, 37, 3) >= tickets + 3 * 48 * 128 + 3 * 16 * 128
+    assert lib.rnsmx_prepared_workspace_bytes(-1, 5, 5, 4, None) == -1
+    # a K split adds its exchange area: R residue bytes per output element
+    # and split (a whole 16 x 16 block per wave)
+    one = _native.Plan(1, 1, 1, 1, 1)
+    four = _native.Plan(1, 1, 1, 1, 4)
+    base = lib.rnsmx_prepared_workspace_bytes(1, 768, 768, 4, ctypes.byref(one))
+    split = lib.rnsmx_prepared_workspace_bytes(1, 768, 768, 4, ctypes.byref(four))
+    assert split - base >= 4 * 16 * 768 * 4
 
 
 def test_c_abi_rejects_bad_arguments_without_gpu():
@@ -167,14 +180,21 @@ def test_c_abi_rejects_bad_arguments_without_gpu():
                                              None, 0, None, None)
     assert rc == _native.EINVAL and b"lut_channels" in lib.rnsmx_last_error()
     rc = lib.rnsmx_matmul_prepared_fused(None, _native.INT8, 4, 200_000, 4, None, ctypes.byref(c),
-                                         None, 0, None, None, None, 0, None, None)
+                                         None, 0, None, None, None, None, 0, None, None)
     assert rc == _native.ERANGE
     rc = lib.rnsmx_encode_centered(None, _native.INT64, 1, 4, 4, ctypes.byref(c), None, None,
                                    None, None)
     assert rc == _native.EINVAL
     # zero-size problems are accepted and launch nothing
     assert lib.rnsmx_matmul_prepared_fused(None, _native.INT8, 0, 64, 8, None, ctypes.byref(c),
-                                           None, 0, None, None, None, 0, None, None) == _native.OK
+                                           None, 0, None, None, None, None, 0, None, None) == _native.OK
+    # a plan that cannot split is rejected before any launch
+    bad = _native.Plan(1, 1, 1, 2, 2)
+    x = ctypes.c_int64(0)
+    rc = lib.rnsmx_matmul_prepared_fused(ctypes.addressof(x), _native.INT8, 4, 64, 8, ctypes.addressof(x),
+                                         ctypes.byref(c), None, 0, None, None, ctypes.byref(bad),
+                                         ctypes.addressof(x), 1 << 20, ctypes.addressof(x), None)
+    assert rc == _native.EINVAL and b"cannot split" in lib.rnsmx_last_error()
 
 
 # --------------------------------------------------------------------------
