@@ -225,6 +225,33 @@ int32_t rnsmx_matmul_prepared_fused(
     const rnsmx_plan_t *plan, void *workspace_dev, int64_t workspace_bytes,
     void *out_dev, void *stream);
 
+/* Bytes of the static scratch of rnsmx_matmul_prepared_fused_noalloc (16 MiB
+ * per GPU, held until the process ends). */
+#define RNSMX_NOALLOC_SCRATCH_BYTES (16 << 20)
+
+/*
+ * rnsmx_matmul_prepared_fused without a workspace argument: the call uses a
+ * library-owned static device array of RNSMX_NOALLOC_SCRATCH_BYTES per GPU
+ * instead, and allocates nothing (no hipMalloc, no hipFree, no allocating
+ * library call).  Same arguments, results and errors otherwise.  A call whose
+ * scratch need (rnsmx_prepared_workspace_bytes for its shape and activation
+ * type) exceeds the maximum fails with RNSMX_ESPACE before touching the GPU.
+ * The first call on each device resolves the array's address there and
+ * clears its counters with one small kernel on `stream`; make that call
+ * outside graph capture.  Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads) race and
+ * must be serialised by the caller.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation).
+ */
+int32_t rnsmx_matmul_prepared_fused_noalloc(
+    const void *a_dev, int32_t a_dtype, int32_t m, int32_t k, int32_t n,
+    const int8_t *packed_dev, const rnsmx_moduli_t *mods,
+    const int16_t *lut_dev, int32_t lut_channels,
+    const rnsmx_adaptive_t *adaptive, const rnsmx_epilogue_t *epilogue,
+    const rnsmx_plan_t *plan, void *out_dev, void *stream);
+
 /*
  * GEMM stage of rnsmx_matmul_prepared_fused on activations already encoded
  * by rnsmx_encode_centered into a_res_dev [R][M][a_ld] (a_ld a multiple of

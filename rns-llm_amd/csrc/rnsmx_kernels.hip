@@ -16,6 +16,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <mutex>
 
 #include "rnsmx_gemm.hpp"
 
@@ -306,6 +307,21 @@ __global__ __launch_bounds__(256) void pad_rows_kernel(const int8_t *__restrict_
     const int64_t col = q % ld, rr = q / ld;  // rr = c * rows + row
     dst[q] = col < k ? src[rr * k + col] : static_cast<int8_t>(0);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of rnsmx_matmul_prepared_fused_noalloc: one array per GPU, held
+// until the process ends.  Its first RNSMX_SPLIT_TICKETS words are the K
+// split's arrival counters, zero when the code object is loaded (the array
+// is zero-initialised device memory) and cleared again by a fill kernel at
+// the first call on each device; every call leaves them zero.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) int8_t scratch[RNSMX_NOALLOC_SCRATCH_BYTES];
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(uint32_t *p, int64_t words) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < words;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -1056,6 +1072,63 @@ int32_t rnsmx_matmul_prepared_fused(const void *a_dev, int32_t a_dtype, int32_t 
   g.w_scale = epilogue ? epilogue->w_scale_dev : nullptr;
   g.bias = epilogue ? epilogue->bias_dev : nullptr;
   return launch_gemm(g, araw, c, reinterpret_cast<uint32_t *>(ws), ws + l.xchg, st);
+}
+
+// Device address of `scratch` on the current device, resolved once per
+// device (each GPU holds its own copy of the array at its own address; the
+// host-side name is only a stand-in and is never passed to a kernel).  The
+// first resolution on a device also clears the counters on `st`.
+static int32_t static_scratch(hipStream_t st, int8_t **out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex lock;
+  static int8_t *ptr[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(RNSMX_ELAUNCH, "no current HIP device for the static scratch");
+  std::lock_guard<std::mutex> guard(lock);
+  if (ptr[dev] == nullptr) {
+    void *p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr) {
+      set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(err));
+      return RNSMX_ELAUNCH;
+    }
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(16), dim3(256), 0, st, static_cast<uint32_t *>(p),
+                       static_cast<int64_t>(RNSMX_SPLIT_TICKETS));
+    if (int32_t rc = check_launch("fill_zero")) return rc;
+    ptr[dev] = static_cast<int8_t *>(p);
+  }
+  *out = ptr[dev];
+  return RNSMX_OK;
+}
+
+int32_t rnsmx_matmul_prepared_fused_noalloc(const void *a_dev, int32_t a_dtype, int32_t m, int32_t k, int32_t n,
+                                            const int8_t *packed_dev, const rnsmx_moduli_t *mods,
+                                            const int16_t *lut_dev, int32_t lut_channels,
+                                            const rnsmx_adaptive_t *adaptive, const rnsmx_epilogue_t *epilogue,
+                                            const rnsmx_plan_t *plan, void *out_dev, void *stream) {
+  clear_error();
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (m > 0 && n > 0) {
+    // reject what cannot fit before touching the device
+    const int64_t need = rnsmx_prepared_workspace_bytes(m, k, n, mods ? mods->channels : 0, plan);
+    const bool raw = a_dtype == RNSMX_INT8 && k % 16 == 0;
+    const int64_t need_call =
+        mods && mods->channels >= 1 && mods->channels <= RNSMX_MAX_CHANNELS && k >= 1
+            ? prepared_need(raw && raw_accumulator_fits(*mods, k), m, k, n, mods->channels, plan)
+            : need;
+    if (need_call > RNSMX_NOALLOC_SCRATCH_BYTES) {
+      set_error("this call needs %lld bytes of scratch; the static scratch holds %lld (use "
+                "rnsmx_matmul_prepared_fused with a workspace)",
+                static_cast<long long>(need_call), static_cast<long long>(RNSMX_NOALLOC_SCRATCH_BYTES));
+      return RNSMX_ESPACE;
+    }
+  }
+  int8_t *ws = nullptr;
+  if (m > 0 && n > 0)
+    if (int32_t rc = static_scratch(st, &ws)) return rc;
+  return rnsmx_matmul_prepared_fused(a_dev, a_dtype, m, k, n, packed_dev, mods, lut_dev, lut_channels, adaptive,
+                                     epilogue, plan, ws, RNSMX_NOALLOC_SCRATCH_BYTES, out_dev, stream);
 }
 
 int32_t rnsmx_matmul_residues_prepared(const int8_t *a_res_dev, int64_t a_ld, int32_t m, int32_t k,

@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 MAX_CHANNELS = 10
 K_ALIGN = 64
 SPLIT_TICKETS = 16384  # RNSMX_SPLIT_TICKETS: 32-bit counters at the start of a workspace
+NOALLOC_SCRATCH_BYTES = 16 << 20  # RNSMX_NOALLOC_SCRATCH_BYTES
 
 OK, EINVAL, ERANGE, ELAUNCH, ESPACE = 0, 1, 2, 3, 4
 
@@ -34,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "rnsmx_prepare_weight",
     "rnsmx_prepared_workspace_bytes",
     "rnsmx_matmul_prepared_fused",
+    "rnsmx_matmul_prepared_fused_noalloc",
     "rnsmx_matmul_residues_prepared",
     "rnsmx_gemm_plan",
     "rnsmx_quantize_symmetric",
@@ -130,6 +132,9 @@ _SIGNATURES = {
         _I32, [_P, _I32, _I32, _I32, _I32, _P, ctypes.POINTER(Moduli), _P, _I32,
                ctypes.POINTER(Adaptive), ctypes.POINTER(Epilogue), ctypes.POINTER(Plan),
                _P, _I64, _P, _P]),
+    "rnsmx_matmul_prepared_fused_noalloc": (
+        _I32, [_P, _I32, _I32, _I32, _I32, _P, ctypes.POINTER(Moduli), _P, _I32,
+               ctypes.POINTER(Adaptive), ctypes.POINTER(Epilogue), ctypes.POINTER(Plan), _P, _P]),
     "rnsmx_matmul_residues_prepared": (
         _I32, [_P, _I64, _I32, _I32, _I32, _P, ctypes.POINTER(Moduli), _P, _I32,
                ctypes.POINTER(Epilogue), _P, _P]),

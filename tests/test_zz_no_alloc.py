@@ -1,0 +1,60 @@
+"""rnsmx_matmul_prepared_fused_noalloc (static scratch, no allocation) against
+rnsmx_matmul_prepared_fused (caller workspace) through the C ABI: two calls
+in a row, the second with a smaller input, each bit-identical to the
+workspace entry point and to the exact product; a call whose scratch need
+exceeds the static maximum is rejected before any launch."""
+import ctypes
+
+import pytest
+import torch
+
+from rns_llm_amd import _native
+from rns_llm_amd.backends.hip_backend import _stream_handle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+DENSE4 = (255, 253, 251, 247)
+
+
+def noalloc_call(backend, a, prepared, out, plan=None):
+    consts = backend._constants(a.device, prepared.moduli)
+    m, k = int(a.shape[0]), int(a.shape[1])
+    return backend._lib.rnsmx_matmul_prepared_fused_noalloc(
+        a.data_ptr(), _native.dtype_code(a.dtype), m, k, prepared.n, prepared.packed.data_ptr(),
+        consts.native_ref, consts.compact_lut.data_ptr(), 2, None, None,
+        None if plan is None else ctypes.byref(_native.make_plan(plan)), out.data_ptr(),
+        _stream_handle(a.device))
+
+
+def test_noalloc_matches_workspace_entry_on_two_calls(backend):
+    gen = torch.Generator(device=DEV).manual_seed(77)
+    # first: long K, few tiles (the automatic plan splits K 8 ways: counters
+    # and exchange area in the static scratch); second: smaller, int16
+    # activations (residue planes in the scratch), ragged shape
+    cases = [(256, 8192, 256, torch.int8, 127), (5, 200, 37, torch.int16, 127)]
+    for m, k, n, dtype, amax in cases:
+        w = torch.randint(-127, 128, (n, k), generator=gen, device=DEV, dtype=torch.int8)
+        a = torch.randint(-amax, amax + 1, (m, k), generator=gen, device=DEV, dtype=torch.int32).to(dtype)
+        prepared = backend.prepare_weight_nk(w, DENSE4)
+        want = backend.matmul_prepared_fused(a, prepared).clone()
+        out = torch.full((m, n), -1, dtype=torch.int64, device=DEV)
+        _native.check(noalloc_call(backend, a, prepared, out))
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+        assert torch.equal(out.double(), a.double() @ w.double().t())
+
+
+def test_noalloc_rejects_oversize_without_launch(backend):
+    # int16 activations need R * M * kp bytes of residue planes: 4 * 8192 *
+    # 1024 = 32 MiB > 16 MiB
+    m, k, n = 8192, 1024, 16
+    w = torch.ones((n, k), dtype=torch.int8, device=DEV)
+    prepared = backend.prepare_weight_nk(w, DENSE4)
+    a = torch.ones((m, k), dtype=torch.int16, device=DEV)
+    out = torch.zeros((m, n), dtype=torch.int64, device=DEV)
+    rc = noalloc_call(backend, a, prepared, out)
+    assert rc == _native.ESPACE
+    assert b"static scratch" in backend._lib.rnsmx_last_error()
+    torch.cuda.synchronize()
+    assert int(out.abs().sum()) == 0
