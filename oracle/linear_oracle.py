@@ -65,15 +65,20 @@ def quantize_activations(inputs: torch.Tensor, in_features: int, bits: int = 8):
     return quantize(flat, scale, bits).contiguous(), scale
 
 
-def linear_forward(inputs: torch.Tensor, weight: torch.Tensor, bias, bits: int = 8):
+def linear_forward(inputs: torch.Tensor, weight: torch.Tensor, bias, bits: int = 8, rows=None):
     """Full rns-mode ``RNSLinear.forward`` on the CPU; returns (output, int64
-    integer product)."""
+    integer product).  With ``rows`` (indices into the flattened [M, K]
+    input) the activation scale still comes from the whole input (it is per
+    tensor), but only those rows are multiplied and returned, as [len(rows),
+    N], so large layers can be checked on a sample of their rows."""
     out_features, in_features = weight.shape
     b, w_scale = prepare_weight(weight, bits)
     a, a_scale = quantize_activations(inputs, in_features, bits)
+    if rows is not None:
+        a = a[torch.as_tensor(rows, dtype=torch.long)]
     integer = torch.from_numpy(a.numpy().astype(np.int64) @ b.numpy().astype(np.int64))
     out = integer.float() * a_scale * w_scale.unsqueeze(0)
     if bias is not None:
         out = out + bias.detach().cpu().float()
-    shape = tuple(inputs.shape[:-1]) + (out_features,)
+    shape = (integer.shape[0], out_features) if rows is not None else tuple(inputs.shape[:-1]) + (out_features,)
     return out.reshape(shape).to(inputs.dtype), integer

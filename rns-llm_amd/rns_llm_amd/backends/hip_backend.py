@@ -16,13 +16,18 @@ Deliberate deviations (each keeps results bit-identical):
   * the workspace's ``accumulators`` tensor is byte scratch sized by the
     library (the fused kernel has no int32 round trip);
   * ``matmul_prepared_adaptive_fused`` selects the channel prefix on the
-    device; its metadata is a lazy mapping that synchronises (and raises
-    ``OverflowError`` when no prefix fits) only when read.
+    device whenever the weight's preparation proved that even the worst
+    activation of the call's dtype fits the full moduli set (the usual case:
+    the set was chosen for that range); its metadata is then a lazy mapping
+    read from the device, and the per-prefix counters are taken when it is
+    read.  Otherwise it takes the reference's synchronous selection and
+    raises ``OverflowError`` before computing, as the reference does.
 """
 from __future__ import annotations
 
 import ctypes
 import functools
+import itertools
 from collections import Counter
 from collections.abc import Mapping
 from dataclasses import dataclass, field
@@ -93,7 +98,10 @@ class RNSWorkspace:
 
 
 class PreparedAdaptiveRNSWeight:
-    """One encoded weight with every safe prefix variant (views, no copies)."""
+    """One encoded weight with every safe prefix variant (views, no copies).
+
+    ``max_abs_weight`` is read from the device once, at preparation (the
+    reference reads it there too, ``cuda_backend.py:569``)."""
 
     def __init__(self, variants: dict, full_moduli: tuple[int, ...],
                  absmax: torch.Tensor, min_channels: int):
@@ -101,14 +109,17 @@ class PreparedAdaptiveRNSWeight:
         self.full_moduli = full_moduli
         self.absmax = absmax
         self.min_channels = min_channels
-        self._max_abs_weight: int | None = None
+        self.max_abs_weight = int(absmax.item())
+        self.full_capacity = (prod(full_moduli) - 1) // 2
 
-    @property
-    def max_abs_weight(self) -> int:
-        """max |B| as a Python int (synchronises once, on first read)."""
-        if self._max_abs_weight is None:
-            self._max_abs_weight = int(self.absmax.item())
-        return self._max_abs_weight
+    def device_selection_is_safe(self, a_dtype: torch.dtype) -> bool:
+        """Whether no activation of this dtype can overflow the full set:
+        K * max|a| * max|B| <= (P - 1) / 2, i.e. 2 * bound < P for the
+        largest bound any input could have.  Then the device-side selection
+        always finds a prefix and no call can wrap."""
+        amax = _DTYPE_MAX_ABS.get(a_dtype)
+        k = self.variants[len(self.full_moduli)].k
+        return amax is not None and k * amax * self.max_abs_weight <= self.full_capacity
 
 
 @dataclass
@@ -121,17 +132,24 @@ class RNSRequestBatchWorkspace:
     k: int
 
 
+_DTYPE_MAX_ABS = {torch.int8: 128, torch.int16: 1 << 15, torch.int32: 1 << 31}
+
+
 class AdaptiveMetadata(Mapping):
-    """``{"channels", "bound", "capacity"}`` of one adaptive call, read lazily
-    from the device.  Reading it synchronises with the stream; when the
-    device found that even the full moduli set cannot hold the bound it
+    """``{"channels", "bound", "capacity"}`` of one device-selected adaptive
+    call, read lazily from the device.  Reading it synchronises with the
+    stream and, once, adds the call to the backend's per-prefix counters
+    ``adaptive_channels_{c}`` and ``fused_gemm_channels_{c}`` (the prefix is
+    known only on the device until then).  The device path is taken only
+    when overflow is impossible; should the device still flag one, reading
     raises ``OverflowError`` like ``minimal_prefix_channels``."""
 
     _KEYS = ("channels", "bound", "capacity")
 
-    def __init__(self, meta: torch.Tensor, full_moduli: tuple[int, ...]):
+    def __init__(self, meta: torch.Tensor, full_moduli: tuple[int, ...], stats: Counter | None = None):
         self.device_tensor = meta
         self._full = full_moduli
+        self._stats = stats
         self._host: dict | None = None
 
     def _load(self) -> dict:
@@ -141,6 +159,9 @@ class AdaptiveMetadata(Mapping):
                 raise OverflowError(
                     f"full moduli set cannot represent bound {bound}; capacity={capacity}")
             self._host = {"channels": channels, "bound": bound, "capacity": capacity}
+            if self._stats is not None:
+                self._stats[f"adaptive_channels_{channels}"] += 1
+                self._stats[f"fused_gemm_channels_{channels}"] += 1
         return self._host
 
     @property
@@ -231,12 +252,15 @@ class HipRNSBackend:
 
     @staticmethod
     def _validate_matrix(matrix: torch.Tensor, name: str, ndim: int) -> None:
-        if not matrix.is_cuda:
-            raise ValueError(f"{name} must be a GPU tensor")
-        if matrix.ndim != ndim:
-            raise ValueError(f"{name} must have rank {ndim}")
-        if not matrix.is_contiguous():
-            raise ValueError(f"{name} must be contiguous")
+        """The layout every native entry point reads: a dense row-major
+        device tensor of the expected rank."""
+        problems = [text for bad, text in ((not matrix.is_cuda, "on the GPU"),
+                                           (matrix.ndim != ndim, f"{ndim}-dimensional"),
+                                           (not matrix.is_contiguous(), "contiguous"))
+                    if bad]
+        if problems:
+            raise ValueError(f"{name} ({tuple(matrix.shape)}, {matrix.device}) must be "
+                             + " and ".join(problems))
 
     # ------------------------------------------------------------------
     # Encoding (cuda_backend.py:188-200)
@@ -349,10 +373,15 @@ class HipRNSBackend:
     @staticmethod
     def _check_workspace(workspace: RNSWorkspace, *, channels: int, m: int, n: int,
                          device: torch.device) -> None:
-        if (workspace.channels, workspace.m, workspace.n) != (channels, m, n):
-            raise ValueError("workspace shape does not match operation")
-        if workspace.accumulators.device != device or workspace.output.device != device:
-            raise ValueError("workspace device does not match operation")
+        """A workspace serves exactly the (channels, M, N) it was made for,
+        on one device (``cuda_backend.py:385-396``)."""
+        made_for = (workspace.channels, workspace.m, workspace.n)
+        if made_for != (channels, m, n):
+            raise ValueError(f"workspace made for (channels, M, N) = {made_for}, "
+                             f"used for {(channels, m, n)}")
+        devices = {workspace.accumulators.device, workspace.output.device}
+        if devices != {device}:
+            raise ValueError(f"workspace on {sorted(map(str, devices))}, operands on {device}")
 
     def _prepared_workspace_bytes(self, m: int, k: int, n: int, channels: int, plan) -> int:
         key = (m, k, n, channels, None if plan is None else plan.as_tuple())
@@ -558,7 +587,7 @@ class HipRNSBackend:
                                    out, a_scale, w_scale, bias, plan)
 
     def _prepared_call(self, a, prepared, lut_channels, workspace, adaptive, out,
-                       a_scale, w_scale, bias, plan=None):
+                       a_scale, w_scale, bias, plan=None, count_channels=True):
         self._check_activation(a, prepared)
         if lut_channels not in (0, 1, 2):
             raise ValueError("lut_channels must be 0, 1 or 2")
@@ -592,7 +621,8 @@ class HipRNSBackend:
         self._stats["encode_centered_calls"] += 1
         self._stats["encode_centered_values"] += int(a.numel())
         self._stats["fused_gemm_calls"] += 1
-        self._stats[f"fused_gemm_channels_{channels}"] += 1
+        if count_channels:
+            self._stats[f"fused_gemm_channels_{channels}"] += 1
         _native.check(self._lib.rnsmx_matmul_prepared_fused(
             _aligned(a).data_ptr(), _native.dtype_code(a.dtype), m, k, n,
             prepared.packed.data_ptr(), consts.native_ref, consts.compact_lut.data_ptr(),
@@ -707,22 +737,37 @@ class HipRNSBackend:
                                        workspace_by_channels: dict | None = None,
                                        return_metadata: bool = False, out=None, a_scale=None,
                                        w_scale=None, bias=None, plan=None):
-        """Adaptive prefix chosen on the device (no host synchronisation).
-        The full-set workspace is used for every prefix; the output is exact
-        whenever the bound fits the full set, and the metadata reports the
-        prefix that was used."""
-        full = prepared.variants[len(prepared.full_moduli)]
-        workspace = None
-        if workspace_by_channels is not None:
-            workspace = workspace_by_channels.get(len(prepared.full_moduli))
-        meta = torch.empty((4,), dtype=torch.int64, device=a.device)
-        adaptive = _native.Adaptive(prepared.min_channels, prepared.absmax.data_ptr(),
-                                    meta.data_ptr())
-        self._stats["adaptive_selections"] += 1
-        result = self._prepared_call(a, full, lut_channels, workspace, ctypes.byref(adaptive),
-                                     out, a_scale, w_scale, bias, plan)
+        """Adaptive channel prefix (``cuda_backend.py:602-622``).
+
+        When the weight's preparation proves that no activation of ``a``'s
+        dtype can exceed the full set (``device_selection_is_safe``), the
+        prefix is chosen on the device inside the one GEMM launch, with no
+        host synchronisation; the full-set workspace serves every prefix and
+        the metadata is an ``AdaptiveMetadata`` read on demand.  Otherwise
+        the selection is the reference's: the row bound is read on the host
+        (one synchronisation), ``OverflowError`` is raised before anything
+        is computed when no prefix holds it, and the chosen prefix runs as a
+        fixed-channel call; the metadata is then a plain dict."""
+        full_channels = len(prepared.full_moduli)
+        if prepared.device_selection_is_safe(a.dtype):
+            workspace = None if workspace_by_channels is None else workspace_by_channels.get(full_channels)
+            meta = torch.empty((4,), dtype=torch.int64, device=a.device)
+            adaptive = _native.Adaptive(prepared.min_channels, prepared.absmax.data_ptr(), meta.data_ptr())
+            self._stats["adaptive_selections"] += 1
+            result = self._prepared_call(a, prepared.variants[full_channels], lut_channels, workspace,
+                                         ctypes.byref(adaptive), out, a_scale, w_scale, bias, plan,
+                                         count_channels=False)
+            if return_metadata:
+                return result, AdaptiveMetadata(meta, prepared.full_moduli, self._stats)
+            return result
+        variant, bound = self.select_adaptive_variant(a, prepared)  # raises OverflowError
+        channels = len(variant.moduli)
+        workspace = None if workspace_by_channels is None else workspace_by_channels.get(channels)
+        result = self._prepared_call(a, variant, min(lut_channels, channels), workspace, None, out,
+                                     a_scale, w_scale, bias, plan)
         if return_metadata:
-            return result, AdaptiveMetadata(meta, prepared.full_moduli)
+            return result, {"channels": channels, "bound": bound,
+                            "capacity": (prod(variant.moduli) - 1) // 2}
         return result
 
     # ------------------------------------------------------------------
@@ -731,13 +776,15 @@ class HipRNSBackend:
     def create_request_batch_workspace(self, *, device: torch.device, dtype: torch.dtype,
                                        rows_per_request: Sequence[int], k: int, channels: int,
                                        n: int) -> RNSRequestBatchWorkspace:
-        rows = tuple(int(x) for x in rows_per_request)
-        if not rows or any(x <= 0 for x in rows):
-            raise ValueError("rows_per_request must contain positive sizes")
-        total = sum(rows)
+        """A staging buffer for the concatenated requests plus the fused
+        workspace of the merged product (``cuda_backend.py:624-645``)."""
+        rows = tuple(int(r) for r in rows_per_request)
+        if len(rows) == 0 or min(rows) < 1:
+            raise ValueError(f"every request needs at least one row, got {rows}")
+        merged = sum(rows)
         return RNSRequestBatchWorkspace(
-            activations=torch.empty((total, k), dtype=dtype, device=device),
-            fused=self.create_workspace(device=device, channels=channels, m=total, n=n, k=k),
+            activations=torch.empty((merged, k), dtype=dtype, device=device),
+            fused=self.create_workspace(device=device, channels=channels, m=merged, n=n, k=k),
             rows_per_request=rows,
             k=int(k),
         )
@@ -747,38 +794,38 @@ class HipRNSBackend:
                                        lut_channels: int = 2,
                                        workspace: RNSRequestBatchWorkspace | None = None,
                                        clone_outputs: bool = False) -> tuple[torch.Tensor, ...]:
-        """Concatenate requests along M, run one fused GEMM, split the rows."""
-        if not requests:
-            raise ValueError("requests must not be empty")
-        first = requests[0]
-        rows = tuple(int(x.shape[0]) for x in requests)
-        for index, t in enumerate(requests):
-            self._validate_matrix(t, f"requests[{index}]", 2)
-            if t.dtype != first.dtype or t.device != first.device:
-                raise ValueError("all requests must share dtype/device")
-            if int(t.shape[1]) != prepared_weight.k:
-                raise ValueError("request K does not match prepared weight")
+        """Continuous batching (``cuda_backend.py:647-703``): the requests'
+        rows are stacked into one activation matrix (a single concatenation
+        into the staging buffer), multiplied in one fused call, and handed
+        back as row views of the merged output (copies with
+        ``clone_outputs``)."""
+        if len(requests) == 0:
+            raise ValueError("no requests to batch")
+        for index, request in enumerate(requests):
+            self._validate_matrix(request, f"request {index}", 2)
+        kinds = {(r.dtype, r.device) for r in requests}
+        if len(kinds) != 1:
+            raise ValueError(f"requests mix dtypes/devices: {sorted(map(str, kinds))}")
+        widths = {int(r.shape[1]) for r in requests}
+        if widths != {prepared_weight.k}:
+            raise ValueError(f"request widths {sorted(widths)} differ from the weight's K = {prepared_weight.k}")
+        rows = tuple(int(r.shape[0]) for r in requests)
         if workspace is None:
+            (dtype, device), = kinds
             workspace = self.create_request_batch_workspace(
-                device=first.device, dtype=first.dtype, rows_per_request=rows,
-                k=prepared_weight.k, channels=len(prepared_weight.moduli), n=prepared_weight.n)
+                device=device, dtype=dtype, rows_per_request=rows, k=prepared_weight.k,
+                channels=len(prepared_weight.moduli), n=prepared_weight.n)
         if workspace.rows_per_request != rows or workspace.k != prepared_weight.k:
-            raise ValueError("request batch workspace does not match request shapes")
-        offset = 0
-        for t in requests:
-            workspace.activations[offset:offset + t.shape[0]].copy_(t)
-            offset += int(t.shape[0])
+            raise ValueError(f"batch workspace holds rows {workspace.rows_per_request} x K={workspace.k}, "
+                             f"requests are {rows} x K={prepared_weight.k}")
+        torch.cat(tuple(requests), dim=0, out=workspace.activations)
         merged = self.matmul_prepared_fused(workspace.activations, prepared_weight,
                                             lut_channels=lut_channels, workspace=workspace.fused)
-        outputs = []
-        offset = 0
-        for r in rows:
-            view = merged[offset:offset + r]
-            outputs.append(view.clone() if clone_outputs else view)
-            offset += r
+        bounds = list(itertools.accumulate(rows, initial=0))
+        views = tuple(merged[lo:hi] for lo, hi in zip(bounds, bounds[1:]))
         self._stats["continuous_batch_calls"] += 1
-        self._stats["continuous_batch_requests"] += len(requests)
-        return tuple(outputs)
+        self._stats["continuous_batch_requests"] += len(rows)
+        return tuple(v.clone() for v in views) if clone_outputs else views
 
     # ------------------------------------------------------------------
     # Convenience wrappers (cuda_backend.py:733-799)

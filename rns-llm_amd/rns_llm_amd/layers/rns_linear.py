@@ -240,10 +240,16 @@ class RNSLinear(nn.Module):
             epi = dict(out=out, a_scale=activation_scale.reshape(1), w_scale=self._weight_scale,
                        bias=bias)
             if self.adaptive_channels:
+                adaptive = self._adaptive_prepared_weight
+                device_safe = getattr(adaptive, "device_selection_is_safe", None)
+                if device_safe is not None and device_safe(quantized_a.dtype):
+                    # the prefix is chosen on the device: the full set's workspace serves all
+                    workspaces = {len(self.moduli): self._workspace(rows)}
+                else:
+                    workspaces = {c: self._workspace(rows, c) for c in adaptive.variants}
                 _, metadata = self.backend.matmul_prepared_adaptive_fused(
-                    quantized_a, self._adaptive_prepared_weight, lut_channels=self.lut_channels,
-                    workspace_by_channels={len(self.moduli): self._workspace(rows)},
-                    return_metadata=True, **epi)
+                    quantized_a, adaptive, lut_channels=self.lut_channels,
+                    workspace_by_channels=workspaces, return_metadata=True, **epi)
                 self.last_adaptive_metadata = metadata
             else:
                 self.backend.matmul_prepared_fused(

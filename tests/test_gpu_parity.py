@@ -280,17 +280,75 @@ def test_adaptive_adversarial_full_set_k4096(backend):
     assert meta["channels"] == 4 and meta["bound"] == 4096 * 127 * 127
 
 
-def test_adaptive_overflow_is_reported(backend):
-    # a two-channel set cannot hold full-range products: the device flags it
+@pytest.mark.parametrize("return_metadata", [False, True])
+def test_adaptive_overflow_raises_before_computing(backend, return_metadata):
+    # adaptive.py:36-41: callers must never silently wrap around.  A
+    # two-channel set cannot hold full-range int8 products, so preparation
+    # cannot prove the device selection safe: the call takes the
+    # reference's synchronous selection and raises before any launch.
     mods = (251, 241)
     gen = torch.Generator().manual_seed(5)
     b = rand_i8(gen, (64, 8))
     a = rand_i8(gen, (4, 64))
     adaptive = backend.prepare_weight_adaptive(b.to(DEV), mods, min_channels=2)
-    _, meta = backend.matmul_prepared_adaptive_fused(a.to(DEV), adaptive, return_metadata=True)
-    assert meta.overflow
+    assert not adaptive.device_selection_is_safe(torch.int8)
+    ws = backend.create_workspace(device=torch.device(DEV), channels=2, m=4, n=8, k=64)
+    ws.output.fill_(-7)
+    backend.reset_stats()
     with pytest.raises(OverflowError):
-        meta["channels"]
+        backend.matmul_prepared_adaptive_fused(a.to(DEV), adaptive, workspace_by_channels={2: ws},
+                                               return_metadata=return_metadata)
+    torch.cuda.synchronize()
+    assert bool((ws.output == -7).all())
+    assert backend.stats_snapshot().get("fused_gemm_calls", 0) == 0
+
+
+def test_rnslinear_adaptive_with_undersized_moduli_raises(backend):
+    layer = RNSLinear(64, 8, mode="rns", backend=backend, moduli=(251, 241), adaptive_channels=True,
+                      adaptive_min_channels=2).to(DEV).eval()
+    with torch.no_grad():
+        layer.weight.copy_(torch.linspace(-1, 1, 64 * 8).reshape(8, 64))
+    with pytest.raises(OverflowError):
+        layer(torch.ones((3, 64), device=DEV))
+
+
+def test_adaptive_synchronous_path_is_exact_and_counted(backend):
+    # a set too small for worst-case int8 products but large enough for
+    # these: the synchronous selection picks 3 of 4 channels, exactly as
+    # select_adaptive_variant + matmul_prepared_fused do in the reference
+    mods = (13, 11, 7, 5)
+    gen = torch.Generator().manual_seed(9)
+    b = rand_i8(gen, (64, 24), -2, 2)
+    a = rand_i8(gen, (5, 64), -2, 2)
+    adaptive = backend.prepare_weight_adaptive(b.to(DEV), mods, min_channels=2)
+    assert not adaptive.device_selection_is_safe(torch.int8)
+    backend.reset_stats()
+    out, meta = backend.matmul_prepared_adaptive_fused(a.to(DEV), adaptive, return_metadata=True)
+    np.testing.assert_array_equal(out.cpu().numpy(), exact(a, b))
+    c, bound, cap = ro.adaptive_select(a.numpy(), int(b.abs().max()), mods, min_channels=2)
+    assert dict(meta) == {"channels": c, "bound": bound, "capacity": cap}
+    stats = backend.stats_snapshot()
+    assert stats["adaptive_selections"] == 1 and stats[f"adaptive_channels_{c}"] == 1
+    assert stats["fused_gemm_calls"] == 1 and stats[f"fused_gemm_channels_{c}"] == 1
+
+
+def test_adaptive_device_path_counts_prefix_when_read(backend):
+    # the default dense set holds every int8 product at this K: the prefix
+    # is chosen on the device, and counted once, when the metadata is read
+    gen = torch.Generator().manual_seed(10)
+    b = rand_i8(gen, (256, 40), -40, 40)
+    a = rand_i8(gen, (6, 256), -8, 8)
+    adaptive = backend.prepare_weight_adaptive(b.to(DEV), DENSE4, min_channels=3)
+    assert adaptive.device_selection_is_safe(torch.int8)
+    backend.reset_stats()
+    out, meta = backend.matmul_prepared_adaptive_fused(a.to(DEV), adaptive, return_metadata=True)
+    stats = backend.stats_snapshot()
+    assert stats["adaptive_selections"] == 1 and stats["fused_gemm_calls"] == 1
+    assert not any(key.startswith(("fused_gemm_channels_", "adaptive_channels_")) for key in stats)
+    assert meta["channels"] == 3 and meta["channels"] == 3  # read twice, counted once
+    stats = backend.stats_snapshot()
+    assert stats["adaptive_channels_3"] == 1 and stats["fused_gemm_channels_3"] == 1
+    np.testing.assert_array_equal(out.cpu().numpy(), exact(a, b))
 
 
 def test_streams_have_independent_workspaces(backend):
@@ -420,6 +478,50 @@ def test_quantize_symmetric_matches_reference_chain(backend, dtype, shape, bits)
     # the scratch is left ready: a second call on the same stream agrees
     q2, scale2 = backend.quantize_symmetric(x.to(DEV), bits)
     assert torch.equal(q2, q) and torch.equal(scale2, scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [8, 12, 16])
+def test_oracle_quantization_matches_torch_gpu_ops(dtype, bits):
+    """The reference RNSLinear runs its activation quantization with torch on
+    the GPU (rns_linear.py:154-166, after flat = inputs.reshape(-1, K).float());
+    the oracle restates it on the CPU with the GPU's rounding of
+    ``tensor / 127.0``.  Pin that restatement against torch's own GPU ops:
+    10^5 tensors per dtype and bit width as the rows of one batch (amax per
+    row; the division is the same elementwise kernel as in the per-tensor
+    form), then 200 separate calls in the reference's exact per-tensor form.
+    A correctly rounded GPU division would fail the scale comparison."""
+    qmax = (1 << (bits - 1)) - 1
+    eps = torch.finfo(torch.float32).eps
+    gen = torch.Generator().manual_seed(1000 * bits + {torch.float32: 1, torch.float16: 2, torch.bfloat16: 3}[dtype])
+    rows, cols = 100_000, 16
+    span = 8 if dtype == torch.float16 else 40  # binades of the row magnitudes (fp16 must not overflow)
+    mag = torch.exp2(torch.randint(-span, span // 4 + 1, (rows, 1), generator=gen).float())
+    x = (torch.randn((rows, cols), generator=gen) * mag).to(dtype).float()
+    x[:64] = 0.0  # all-zero tensors: the eps clamp
+    xg = x.to(DEV)
+    s_gpu = torch.clamp(xg.abs().amax(dim=1, keepdim=True) / float(qmax), min=eps)
+    q_gpu = torch.clamp(torch.round(xg / s_gpu), -qmax, qmax)
+    s_or = linear_oracle.symmetric_scale(x, bits, dim=1)
+    q_or = linear_oracle.quantize(x, s_or, bits)
+    assert torch.equal(s_gpu.cpu().view(torch.int32), s_or.view(torch.int32))
+    assert torch.equal(q_gpu.cpu().to(q_or.dtype), q_or)
+    # float32 amax values on which a correctly rounded division differs from
+    # the reciprocal product for some entries (so the check can tell them apart)
+    a = (torch.rand((20_000, 1), generator=gen) + 1) * torch.exp2(
+        torch.randint(-30, 30, (20_000, 1), generator=gen).float())
+    s_or = linear_oracle.symmetric_scale(a, bits, dim=1)
+    assert not torch.equal(torch.clamp(a / float(qmax), min=eps).view(torch.int32), s_or.view(torch.int32))
+    s_gpu = torch.clamp(a.to(DEV) / float(qmax), min=eps)
+    assert torch.equal(s_gpu.cpu().view(torch.int32), s_or.view(torch.int32))
+    for i in range(200):
+        t = xg[97 * i: 97 * i + 1 + i % 6].reshape(-1, cols if i % 2 else 8)
+        s1 = torch.clamp(t.abs().amax(dim=None, keepdim=True) / float(qmax), min=eps)
+        q1 = torch.clamp(torch.round(t / s1), -qmax, qmax)
+        s1_or, = (linear_oracle.symmetric_scale(t.cpu(), bits),)
+        assert torch.equal(s1.cpu().view(torch.int32), s1_or.view(torch.int32))
+        assert torch.equal(q1.cpu().to(torch.int8 if bits == 8 else torch.int16),
+                           linear_oracle.quantize(t.cpu(), s1_or, bits))
 
 
 def test_quantize_symmetric_validation(backend):

@@ -305,3 +305,63 @@ def test_from_linears_validation():
         RNSQKVProjection.from_linears(q, k, nn.Linear(8, 16), mode="torch")
     with pytest.raises(TypeError):
         RNSQKVProjection.from_linears(q, k, nn.Identity(), mode="torch")
+
+
+def test_installed_fusion_owns_parameters_once():
+    from rns_llm_amd.layers import install_opt_qkv_fusion
+
+    class Attention(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.q_proj, self.k_proj, self.v_proj = make_linears()
+            self.out_proj = nn.Linear(16, 16)
+
+    attention = Attention()
+    q_w = attention.q_proj.weight.detach().clone()
+    coord = install_opt_qkv_fusion(attention, backend=None)
+    keys = set(attention.state_dict())
+    assert {"rns_qkv.projection.combined.weight", "rns_qkv.projection.combined.bias"} <= keys
+    assert not any(k.startswith(("q_proj", "k_proj", "v_proj")) for k in keys)
+    assert attention.rns_qkv is coord and [p.index for p in (attention.q_proj, attention.k_proj,
+                                                             attention.v_proj)] == [0, 1, 2]
+    # q, k, v stacked in that order along the output features
+    torch.testing.assert_close(coord.projection.combined.weight[:16], q_w, rtol=0, atol=0)
+    with pytest.raises(TypeError):
+        install_opt_qkv_fusion(attention, backend=None)  # q_proj is no longer nn.Linear
+
+
+def test_qkv_cache_recomputes_for_a_new_hidden_state():
+    q, k, v = make_linears()
+    projection = RNSQKVProjection.from_linears(q, k, v, mode="torch").eval()
+    coord = CachedRNSQKV(projection).eval()
+    qp, kp, vp = coord.slices()
+    x, y = torch.randn(2, 16), torch.randn(2, 16)
+    qp(x)
+    kp(y)  # another hidden state before the call finished: recompute
+    assert projection.compute_count == 2 and coord.cache_misses == 2 and coord.cache_hits == 0
+    vp(y)
+    qp(y)  # k, v and q of y served from one product
+    assert projection.compute_count == 2 and coord.cache_hits == 2
+    with pytest.raises(ValueError):
+        coord.forward_slice(x, 3)
+
+
+def test_replace_opt_attention_blocks_structure():
+    transformers = pytest.importorskip("transformers")
+    from rns_llm_amd.layers import replace_opt_attention_blocks
+
+    config = transformers.OPTConfig(hidden_size=16, num_attention_heads=2, ffn_dim=32,
+                                    num_hidden_layers=3, vocab_size=64, max_position_embeddings=32,
+                                    word_embed_proj_dim=16)
+    model = transformers.OPTForCausalLM(config).eval()
+    layers = model.model.decoder.layers
+    before = layers[0].self_attn.out_proj.weight.detach().clone()
+    replaced, coordinators = replace_opt_attention_blocks(model, backend=None, blocks=2)
+    assert replaced == [f"model.decoder.layers.{i}.self_attn.{part}" for i in (0, 1)
+                        for part in ("qkv_fused", "out_proj")]
+    assert len(coordinators) == 2
+    assert isinstance(layers[0].self_attn.out_proj, RNSLinear)
+    torch.testing.assert_close(layers[0].self_attn.out_proj.weight, before, rtol=0, atol=0)
+    assert isinstance(layers[2].self_attn.q_proj, nn.Linear)  # only the first two blocks
+    with pytest.raises(ValueError):
+        replace_opt_attention_blocks(model, backend=None, blocks=-1)

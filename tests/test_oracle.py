@@ -296,11 +296,66 @@ def test_quantize_is_half_to_even_and_clamped():
 
 
 def test_scale_uses_gpu_reciprocal_rounding():
-    # Measured on the MI355X (torch 2.10 ROCm): for this amax, torch on the GPU
-    # gives amax / 127.0 == amax * fl32(1/127) == 0x3B1BAAA0 (bits below), while
-    # a correctly rounded division gives the next float up.  RNSLinear runs on
-    # the GPU, so the oracle must produce the GPU value.
-    amax = torch.tensor([np.int32(1050309102)], dtype=torch.int32).view(torch.float32)
+    """The oracle's scale is amax * fl32(1/127) (the rounding of torch's GPU
+    ``tensor / 127.0``, which multiplies by the reciprocal of a CPU scalar),
+    not the correctly rounded quotient.  Known answer for one amax, worked
+    out with exact rational arithmetic: fl32(1/127) = 0x3C010204, the
+    product rounds to 0x3B1BA940, and the float nearest amax / 127 is the
+    next one up, 0x3B1BA941 (what the CPU division returns).  The GPU side
+    of the claim is tested against torch's own GPU ops in
+    tests/test_gpu_parity.py."""
+    from fractions import Fraction
+
+    def bits(t):
+        return int(t.view(torch.int32).item()) & 0xFFFFFFFF
+
+    def f32(b):
+        return torch.tensor([b], dtype=torch.int64).to(torch.int32).view(torch.float32)
+
+    amax = f32(1050309102)
+    inv = torch.tensor(1.0, dtype=torch.float32) / torch.tensor(127.0, dtype=torch.float32)
+    assert bits(inv.reshape(1)) == 0x3C010204
     s = linear_oracle.symmetric_scale(amax.reshape(1, 1))
-    assert s.view(torch.int32).item() != (amax / 127.0).view(torch.int32).item()
-    assert s.item() == (amax * (torch.tensor(1.0) / torch.tensor(127.0))).item()
+    assert bits(s) == 0x3B1BA940
+    # the correctly rounded quotient is the neighbour above, by exact arithmetic
+    exact = Fraction(float(amax.item())) / 127
+    lo, hi = Fraction(float(f32(0x3B1BA940).item())), Fraction(float(f32(0x3B1BA941).item()))
+    assert lo < exact < hi and hi - exact < exact - lo
+    assert bits((amax / 127.0).reshape(1)) == 0x3B1BA941
+    # and the product itself is the float nearest amax * fl32(1/127)
+    prod = Fraction(float(amax.item())) * Fraction(float(inv.item()))
+    assert abs(Fraction(float(s.item())) - prod) <= abs(Fraction(float(f32(0x3B1BA941).item())) - prod)
+
+
+def test_adaptive_select_sums_each_row():
+    """Known answers for ``adaptive_select`` (``cuda_backend.py:577-600``:
+    bound = max over rows of sum_k |a_ik|, times max|B|; the first prefix of
+    at least min_channels whose product exceeds twice the bound).  With
+    moduli (3, 5, 7, 11, 13) the prefix products are 3, 15, 105, 1155,
+    15015.  Case 1: row L1 36, column L1 at most 10, |B| <= 3: bound 108,
+    2 * 108 >= 105 so 4 channels (capacity (1155 - 1) / 2 = 577); summing
+    columns would give bound 30 and 3 channels.  Case 2: row L1 36 and 32,
+    total 68, |B| <= 10: bound 360, 4 channels; summing every element would
+    give 680 and 5 channels.  Case 3: no prefix holds the bound."""
+    mods = (3, 5, 7, 11, 13)
+    a1 = np.array([[9, -9, 9, -9], [1, 0, 0, 0]], dtype=np.int8)
+    assert ro.adaptive_select(a1, 3, mods, min_channels=2) == (4, 108, 577)
+    a2 = np.array([[9, 9, -9, 9], [8, -8, 8, 8]], dtype=np.int8)
+    assert ro.adaptive_select(a2, 10, mods, min_channels=2) == (4, 360, 577)
+    # the transposed operand and the whole-matrix sum give other answers
+    assert ro.adaptive_select(a1.T.copy(), 3, mods, min_channels=2)[0] == 3
+    assert ro.adaptive_select(a2.reshape(1, -1), 10, mods, min_channels=2)[0] == 5
+    with pytest.raises(OverflowError):
+        ro.adaptive_select(np.full((2, 64), 127, dtype=np.int8), 127, mods, min_channels=2)
+
+
+def test_linear_oracle_row_sample_equals_full_rows():
+    gen = torch.Generator().manual_seed(8)
+    w = torch.randn(24, 40, generator=gen) * 0.02
+    b = torch.randn(24, generator=gen)
+    x = torch.randn(5, 3, 40, generator=gen)
+    full, full_int = linear_oracle.linear_forward(x, w, b)
+    rows = [0, 7, 14]
+    part, part_int = linear_oracle.linear_forward(x, w, b, rows=rows)
+    assert torch.equal(part, full.reshape(-1, 24)[rows])
+    assert torch.equal(part_int, full_int[rows])
