@@ -10,12 +10,17 @@ modular reduction + Garner + signed correction, exact int64 output) with
 inputs resident in HBM.  The prepared weights rotate over copies totalling
 more than 512 MB so the 256 MB MALL cannot serve repeats.
 
-Timing: W untimed eager warmup steps, then the K timed steps are captured in
-one HIP graph (the launch cost of Python + ctypes per call is host time, not
-device throughput); the graph is replayed once untimed (upload), then once
-between synchronizations with HIP events on the launching stream.  The
-eager per-call latency (event pair around each call, host overhead
-included) is reported beside it as us_per_call_p50/p95.
+Timing: W untimed eager warmup steps plus eager calls until at least
+100 ms of them have run (the clocks ramp), then the K timed steps are
+captured in one HIP graph (the launch cost of Python + ctypes per call is
+host time, not device throughput); the graph is replayed once untimed
+(upload), a 512 MiB device copy then evicts the 256 MB MALL, and the graph
+is replayed once more between synchronizations with HIP events on the
+launching stream.  Every timed call reads a weight copy that is not in the
+MALL: the flushed ones first, and past `count` steps copies read `count`
+steps (> 512 MB) before.  The eager per-call latency (event pair around
+each call, host overhead included) is reported beside it as
+us_per_call_p50/p95.
 
 Printed JSON (one line): value = effective int8 TOPS = 2*R*M*K*N / t_step.
 roofline: the step is one GEMM kernel launch, so its duration is the
@@ -24,8 +29,11 @@ output) per launch / that duration.  traffic: HBM bytes per launch from two
 rocprofv3 --pmc child runs (FETCH_SIZE, WRITE_SIZE), each scaled by what
 the counter reads for a 64 MiB device copy in the same run (null when
 rocprofv3 is unavailable or fails).  cpu_baseline = the NumPy restatement
-of the reference CPU path on a bounded sample, 1 core; cpu_baseline_all_cores
-= the OpenMP C restatement on the full headline shape.  Extra rows cover the
+(oracle/) of the reference CPU pipeline on config C1 (M=128, K=N=768), 1
+core, min and median of >= 5 repeats after one warmup
+(benchmarks/reference_latency.py:7-11); cpu_baseline_torch = the torch-CPU
+restatement of TorchReferenceBackend.matmul_int8 on C1 at all host threads;
+cpu_baseline_all_cores = the OpenMP C restatement on C1.  Extra rows cover the
 other C2 token counts, C3 decode, C5 (OPT-6.7B QKV) shapes and C4 (a
 random-init OPT-125m forward with 4 RNS attention blocks: time, logit error,
 call counts).
@@ -54,6 +62,8 @@ DENSE4 = (255, 253, 251, 247)
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
 CALIB_BYTES = 64 << 20   # device copy used to scale the PMC byte counters
+FLUSH_BYTES = 256 << 20  # copied buffer to buffer (512 MiB touched) to evict the 256 MB MALL
+WARM_SECONDS = 0.1       # eager warmup time per row, beyond the W warmup steps
 GEMM_KERNELS = ("mfma_kernel", "stream_kernel", "lds_kernel")
 METRIC = "effective int8 TOPS + us/call, fused-QKV RNS GEMM+reconstruct, bit-exact"
 
@@ -128,9 +138,23 @@ def per_call(fn, iters):
     return statistics.median(samples), samples[min(len(samples) - 1, math.ceil(0.95 * len(samples)) - 1)]
 
 
+_FLUSH = []
+
+
+def mall_flush():
+    """Evict the MALL: a 256 MiB buffer-to-buffer device copy (512 MiB touched)."""
+    import torch
+
+    if not _FLUSH:
+        _FLUSH.extend([torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda"),
+                       torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")])
+    _FLUSH[1].copy_(_FLUSH[0])
+
+
 def graph_steps(fn, steps, warmup):
-    """W eager warmup steps, K steps captured in one graph, replayed once
-    untimed and once timed.  Returns (device ms per step, host ms per step)."""
+    """W eager warmup steps and at least WARM_SECONDS of eager calls, K steps
+    captured in one graph, replayed once untimed, the MALL flushed, then
+    replayed once timed.  Returns (device ms per step, host ms per step)."""
     import torch
 
     stream = torch.cuda.Stream()
@@ -138,6 +162,13 @@ def graph_steps(fn, steps, warmup):
     with torch.cuda.stream(stream):
         for i in range(warmup):
             fn(i)
+        t_end = time.perf_counter() + WARM_SECONDS
+        i = warmup
+        while time.perf_counter() < t_end:
+            fn(i)
+            i += 1
+            if i % 64 == 0:
+                torch.cuda.synchronize()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
@@ -147,6 +178,8 @@ def graph_steps(fn, steps, warmup):
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
+        mall_flush()
+        torch.cuda.synchronize()
         t0 = time.perf_counter()
         start.record(stream)
         graph.replay()
@@ -206,6 +239,8 @@ def measure_shape(backend, name, m, k, n_each, parts, steps, warmup, rotate_byte
     row = {
         "config": name, "m": m, "k": k, "n": n, "channels": r, "weight_copies": count,
         "adaptive": adaptive,
+        # every timed call reads one prepared weight that is not MALL-resident
+        "timed_weight_bytes": steps * len(DENSE4) * n * ((k + 63) // 64 * 64),
         "ms_per_step": ms, "host_ms_per_step": host_ms,
         "us_per_call_graph": ms * 1000.0, "us_per_call_p50": p50, "us_per_call_p95": p95,
         "eff_tops": ops / (ms * 1e-3) / 1e12, "useful_tops": ops / r / (ms * 1e-3) / 1e12,
@@ -305,59 +340,118 @@ def measure_traffic(args):
     return parts
 
 
+def host_description():
+    """CPU model, core count and threading settings of this host."""
+    model = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.lower().startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
+C1 = (128, 768, 768)  # BASELINE config 1: the reference CPU path's shape
+
+
+def c1_operands():
+    import numpy as np
+
+    rng = np.random.default_rng(1)
+    m, k, n = C1
+    return (rng.integers(-127, 128, (m, k)).astype(np.int8),
+            rng.integers(-127, 128, (k, n)).astype(np.int8))
+
+
+def repeat_timed(fn, repeats, seconds):
+    """One warmup, then at least `repeats` timed calls and at least `seconds`
+    of them (benchmarks/reference_latency.py:7-11); (min, median) seconds."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < repeats or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return min(times), statistics.median(times), len(times)
+
+
 def cpu_baseline(seconds):
-    """NumPy restatement of the reference CPU pipeline on a C2 sample."""
+    """The NumPy restatement of the reference CPU pipeline (centered encode
+    -> per-channel int64 matmul -> mod -> Garner, oracle/rns_oracle.py) on
+    C1, 1 core, checked exact first; the plain int64 A @ B beside it."""
     import numpy as np
 
     from oracle import rns_oracle
 
-    rng = np.random.default_rng(5)
-    m, k, n = 16, 768, 2304
-    a = rng.integers(-127, 128, (m, k)).astype(np.int8)
-    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
-    rns_oracle.rns_matmul_centered(a, b, DENSE4)  # warmup
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        rns_oracle.rns_matmul_centered(a, b, DENSE4)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
+    a, b = c1_operands()
+    if not np.array_equal(rns_oracle.rns_matmul_centered(a, b, DENSE4), rns_oracle.exact_matmul(a, b)):
+        raise SystemExit("cpu baseline: the NumPy pipeline is not exact")
+    t_min, t_med, reps = repeat_timed(lambda: rns_oracle.rns_matmul_centered(a, b, DENSE4), 5, seconds)
+    p_min, p_med, _ = repeat_timed(lambda: rns_oracle.exact_matmul(a, b), 5, 0.0)
+    m, k, n = C1
     ops = 2 * len(DENSE4) * m * k * n
     return {
-        "value": ops / t / 1e12, "unit": "effective int8 TOPS", "cores": 1, "kind": "port",
-        "sample": (f"C2 slice M={m}, K={k}, N={n}, R=4: NumPy int64 centered encode -> "
-                   f"per-channel matmul -> mod -> Garner (oracle/rns_oracle.py), median of "
-                   f"{len(times)} calls, {t * 1e3:.1f} ms/call; host {platform.processor() or platform.machine()}, "
-                   f"os.cpu_count()={os.cpu_count()}"),
+        "value": ops / t_med / 1e12, "unit": "effective int8 TOPS", "cores": 1, "kind": "port",
+        "sample": (f"C1 M={m}, K={k}, N={n}, R=4, int8 U[-127,127]: NumPy int64 centered encode -> "
+                   f"per-channel matmul -> mod -> Garner (oracle/rns_oracle.py), 1 core; {reps} calls "
+                   f"after 1 warmup: min {t_min * 1e3:.1f} ms, median {t_med * 1e3:.1f} ms "
+                   f"(value from the median); plain int64 A@B {p_med * 1e3:.1f} ms"),
+        "ms_min": t_min * 1e3, "ms_median": t_med * 1e3, "repeats": reps,
+        "plain_int64_matmul_ms_median": p_med * 1e3,
+        **host_description(),
+    }
+
+
+def cpu_baseline_torch(seconds):
+    """The torch-CPU restatement of TorchReferenceBackend.matmul_int8
+    (oracle/torch_cpu_oracle.py) on C1 at torch.get_num_threads() threads."""
+    import numpy as np
+    import torch
+
+    from oracle import torch_cpu_oracle
+    from oracle import rns_oracle
+
+    a, b = (torch.from_numpy(x) for x in c1_operands())
+    if not np.array_equal(torch_cpu_oracle.matmul_int8(a, b, DENSE4).numpy(),
+                          rns_oracle.exact_matmul(a.numpy(), b.numpy())):
+        raise SystemExit("cpu baseline: the torch-CPU pipeline is not exact")
+    t_min, t_med, reps = repeat_timed(lambda: torch_cpu_oracle.matmul_int8(a, b, DENSE4), 5, seconds)
+    m, k, n = C1
+    return {
+        "value": 2 * len(DENSE4) * m * k * n / t_med / 1e12, "unit": "effective int8 TOPS",
+        "cores": torch.get_num_threads(), "kind": "port",
+        "sample": (f"C1: torch CPU int64 encode -> per-channel matmul -> CRT decode "
+                   f"(oracle/torch_cpu_oracle.py), {torch.get_num_threads()} threads; {reps} calls: "
+                   f"min {t_min * 1e3:.1f} ms, median {t_med * 1e3:.1f} ms"),
+        "ms_min": t_min * 1e3, "ms_median": t_med * 1e3, "repeats": reps,
     }
 
 
 def cpu_baseline_all_cores(seconds):
-    """The OpenMP C restatement (oracle/rns_oracle.c) of the same centered
-    pipeline on the full headline shape, all host threads."""
+    """The OpenMP C restatement (oracle/rns_oracle.c) of the centered
+    pipeline on C1, all host threads."""
     import numpy as np
 
     from oracle import c_oracle
+    from oracle import rns_oracle
 
-    rng = np.random.default_rng(6)
-    m, k, n = 256, 768, 2304
-    a = rng.integers(-127, 128, (m, k)).astype(np.int8)
-    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
-    c_oracle.rns_matmul_centered(a, b, DENSE4)  # warmup (and build check)
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        c_oracle.rns_matmul_centered(a, b, DENSE4)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
+    a, b = c1_operands()
+    if not np.array_equal(c_oracle.rns_matmul_centered(a, b, DENSE4), rns_oracle.exact_matmul(a, b)):
+        raise SystemExit("cpu baseline: the C pipeline is not exact")
+    t_min, t_med, reps = repeat_timed(lambda: c_oracle.rns_matmul_centered(a, b, DENSE4), 5, seconds)
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    m, k, n = C1
     return {
-        "value": 2 * len(DENSE4) * m * k * n / t / 1e12, "unit": "effective int8 TOPS",
+        "value": 2 * len(DENSE4) * m * k * n / t_med / 1e12, "unit": "effective int8 TOPS",
         "cores": threads, "kind": "port",
-        "sample": (f"C2 M={m}, K={k}, N={n}, R=4: C restatement with OpenMP (oracle/rns_oracle.c), "
-                   f"median of {len(times)} calls, {t * 1e3:.1f} ms/call"),
+        "sample": (f"C1: C restatement with OpenMP (oracle/rns_oracle.c), {threads} threads; "
+                   f"{reps} calls: min {t_min * 1e3:.2f} ms, median {t_med * 1e3:.2f} ms"),
+        "ms_min": t_min * 1e3, "ms_median": t_med * 1e3, "repeats": reps,
     }
 
 
@@ -479,7 +573,7 @@ def main():
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--m", type=int, default=256)
     parser.add_argument("--rotate-mb", type=float, default=600.0)
-    parser.add_argument("--cpu-seconds", type=float, default=10.0)
+    parser.add_argument("--cpu-seconds", type=float, default=5.0)
     parser.add_argument("--no-extra", action="store_true", help="headline shape only")
     parser.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     parser.add_argument("--pmc-child", action="store_true",
@@ -545,7 +639,11 @@ def main():
             log(f"bench: C4 skipped ({exc})")
 
     cpu = cpu_baseline(args.cpu_seconds)
-    cpu_all = cpu_baseline_all_cores(min(args.cpu_seconds, 5.0))
+    cpu_torch = cpu_baseline_torch(min(args.cpu_seconds, 3.0))
+    cpu_all = cpu_baseline_all_cores(min(args.cpu_seconds, 2.0))
+    log(f"bench: CPU C1: NumPy 1 core {cpu['ms_median']:.0f} ms, torch {cpu_torch['cores']} threads "
+        f"{cpu_torch['ms_median']:.0f} ms, C/OpenMP {cpu_all['cores']} threads {cpu_all['ms_median']:.1f} ms "
+        f"({cpu['cpu_model']})")
     achieved = head["bytes_alg"] / (head["ms_per_step"] * 1e-3) / 1e9
     roofline = {
         "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -572,12 +670,16 @@ def main():
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (seeded N(0,0.02) weights, N(0,1) tokens, int8-quantized)",
-        "config": {"workload": "C2 fused OPT-125m QKV: M=256, K=768, N=2304, R=4 "
-                               "(255,253,251,247), int64 exact output, weights rotated over "
-                               f"{head['weight_copies']} copies (> 512 MB)",
-                   "m": args.m, "k": 768, "n": 2304, "channels": 4},
+        "config": {"workload": f"C2 fused OPT-125m QKV: M={args.m}, K=768, N=2304, R=4 "
+                               "(255,253,251,247), int64 exact output; weights rotated over "
+                               f"{head['weight_copies']} copies (> 512 MB) and the MALL flushed "
+                               "before the timed replay, so every timed call reads its weights "
+                               "from HBM",
+                   "m": args.m, "k": 768, "n": 2304, "channels": 4,
+                   "timed_weight_bytes": head["timed_weight_bytes"]},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_baseline_torch": cpu_torch,
         "cpu_baseline_all_cores": cpu_all,
         "rows": rows,
     }

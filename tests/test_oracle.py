@@ -359,3 +359,24 @@ def test_linear_oracle_row_sample_equals_full_rows():
     part, part_int = linear_oracle.linear_forward(x, w, b, rows=rows)
     assert torch.equal(part, full.reshape(-1, 24)[rows])
     assert torch.equal(part_int, full_int[rows])
+
+
+def test_torch_cpu_restatement_is_exact():
+    """oracle/torch_cpu_oracle.py (the reference's TorchReferenceBackend
+    path, timed as bench.py's all-cores CPU baseline) against the closed
+    form, the NumPy oracle's encoder and CRT decoder, and the reference's
+    known CRT answer (tests/test_torch_reference.py:6-13 shape)."""
+    from oracle import torch_cpu_oracle as tco
+
+    gen = torch.Generator().manual_seed(13)
+    a = torch.randint(-127, 128, (9, 40), generator=gen, dtype=torch.int8)
+    b = torch.randint(-127, 128, (40, 11), generator=gen, dtype=torch.int8)
+    mods = (255, 253, 251, 247)
+    np.testing.assert_array_equal(tco.matmul_int8(a, b, mods).numpy(), ro.exact_matmul(a.numpy(), b.numpy()))
+    np.testing.assert_array_equal(tco.encode(a, mods).numpy(), ro.encode_canonical(a.numpy(), mods))
+    res = ro.encode_canonical(ro.exact_matmul(a.numpy(), b.numpy()), mods)
+    np.testing.assert_array_equal(tco.decode(torch.from_numpy(res.astype(np.uint8)), mods).numpy(),
+                                  ro.decode_crt(res, mods))
+    big_p, coeffs = tco.crt_coefficients(mods)
+    assert big_p == 3_999_736_455
+    assert all(c % m == 1 and all(c % o == 0 for o in mods if o != m) for c, m in zip(coeffs, mods))
