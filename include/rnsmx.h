@@ -302,6 +302,31 @@ int32_t rnsmx_quantize_symmetric(const void *x_dev, int32_t x_dtype, int64_t cou
                                  int32_t quant_bits, int32_t *scratch_dev, float *scale_dev,
                                  void *q_dev, void *stream);
 
+/* Bytes of workspace rnsmx_linear_forward needs (-1 for a bad shape). */
+int64_t rnsmx_linear_workspace_bytes(int64_t rows, int64_t k, int64_t n,
+                                     int32_t channels, int32_t quant_bits);
+
+/*
+ * The device part of RNSLinear.forward in one call: per-tensor symmetric
+ * quantization of x_dev [rows][k] (float32, float16 or bfloat16, as
+ * rnsmx_quantize_symmetric), then the prepared-weight GEMM whose epilogue
+ * writes ((float)y * s_x) * w_scale[col] + bias[col] in x's dtype into
+ * out_dev [rows][n].  w_scale_dev [n] float32 (per output channel), bias_dev
+ * [n] float32 or NULL; adaptive as in rnsmx_matmul_prepared_fused.  The
+ * quantized activations, their scale and the GEMM scratch live in the
+ * workspace (rnsmx_linear_workspace_bytes; the counter rule of the
+ * conventions above applies).  Three launches, no host synchronisation.
+ * Replaces RNSLinear.forward's quantize -> backend -> dequantize chain
+ * (src/rns_llm/layers/rns_linear.py:238-275) on a prepared weight.
+ */
+int32_t rnsmx_linear_forward(const void *x_dev, int32_t x_dtype, int32_t rows,
+                             int32_t k, int32_t n, int32_t quant_bits,
+                             const int8_t *packed_dev, const rnsmx_moduli_t *mods,
+                             const float *w_scale_dev, const float *bias_dev,
+                             const rnsmx_adaptive_t *adaptive,
+                             void *workspace_dev, int64_t workspace_bytes,
+                             void *out_dev, void *stream);
+
 /*
  * Garner reconstruction of centered residues [R][count] int8 -> int64.
  * Replaces _C.decode_garner (csrc/rns_cuda.cu:818-885, kernel 416-440).

@@ -32,6 +32,7 @@
 #include <hip/hip_runtime.h>
 
 #include <climits>
+#include <cstring>
 
 #include "rnsmx_arith.hpp"
 #include "rnsmx_common.hpp"
@@ -40,7 +41,29 @@ namespace rnsmx {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-struct GemmArgs {
+// The GEMM's moduli constants for up to RCAP channels: the fields of
+// rnsmx_moduli_t the kernels read, sized for their channel capacity, so a
+// launch passes a few hundred bytes of arguments instead of the 10-channel
+// block (the runtime writes the argument block for every launch, and its
+// host cost grows with the size: 0.9 KB measured 1 us more per launch than
+// 16 bytes).
+template <int RCAP>
+struct GemmMods {
+  int32_t channels;
+  uint32_t moduli[RCAP];
+  uint32_t magic[RCAP];
+  uint32_t qinv[RCAP];
+  int32_t qk16[RCAP];
+  uint32_t qk8[RCAP];
+  uint32_t ucoef[RCAP][RCAP];
+  int64_t prefix[RCAP + 1];
+};
+
+// Arguments of one GEMM launch.  The host fills GemmArgs (with the full
+// moduli block); each kernel instantiation receives GemmArgsK<RCAP>, the
+// same fields with its compact constants (compact_args).
+template <typename Mods>
+struct GemmArgsOf {
   const int8_t *a;  // [R][M][a_ld] residue planes, or [M][a_ld] int8 (a_cs = 0)
   int64_t a_ld, a_cs;
   const int8_t *b;  // [R][N16][kp/64][1024] fragment-major
@@ -68,8 +91,32 @@ struct GemmArgs {
   const float *a_scale;
   const float *w_scale;
   const float *bias;
-  rnsmx_moduli_t mods;
+  Mods mods;  // last: every other field has the same offset in every instantiation
 };
+using GemmArgs = GemmArgsOf<rnsmx_moduli_t>;
+template <int RCAP>
+using GemmArgsK = GemmArgsOf<GemmMods<RCAP>>;
+
+// The kernel-side arguments of `g` for channel capacity RCAP (g.mods.channels
+// <= RCAP; unused channels are zero).
+template <int RCAP>
+inline GemmArgsK<RCAP> compact_args(const GemmArgs &g) {
+  static_assert(offsetof(GemmArgs, mods) == offsetof(GemmArgsK<RCAP>, mods), "shared leading fields");
+  GemmArgsK<RCAP> k{};
+  std::memcpy(static_cast<void *>(&k), static_cast<const void *>(&g), offsetof(GemmArgs, mods));
+  const rnsmx_moduli_t &f = g.mods;
+  k.mods.channels = f.channels;
+  for (int c = 0; c < RCAP && c < RNSMX_MAX_CHANNELS; ++c) {
+    k.mods.moduli[c] = static_cast<uint32_t>(f.moduli[c]);
+    k.mods.magic[c] = f.magic[c];
+    k.mods.qinv[c] = f.qinv[c];
+    k.mods.qk16[c] = f.qk16[c];
+    k.mods.qk8[c] = f.qk8[c];
+    for (int j = 0; j < RCAP && j < RNSMX_MAX_CHANNELS; ++j) k.mods.ucoef[j][c] = f.ucoef[j][c];
+  }
+  for (int c = 0; c <= RCAP && c <= RNSMX_MAX_CHANNELS; ++c) k.mods.prefix[c] = f.prefix[c];
+  return k;
+}
 
 // kStreamWide: the stream kernel with chunks of up to 8 K steps (long K).
 // kMfma3: the MFMA kernel with three column waves (48*nb-column tiles).
@@ -125,7 +172,8 @@ template <typename T>
 __device__ __forceinline__ RNSMX_KARG(T) & kernel_args() {
   return *(RNSMX_KARG(T) *)(__builtin_amdgcn_kernarg_segment_ptr());
 }
-typedef RNSMX_KARG(GemmArgs) KGemmArgs;
+template <int RCAP>
+using KArgs = RNSMX_KARG(GemmArgsK<RCAP>);
 
 // Touches the first BYTES of the argument block, one read per 64-byte line,
 // in one round at kernel entry.  The block is written for each launch, so
@@ -151,6 +199,8 @@ __device__ __forceinline__ void prefetch_kernel_args() {
 // GemmArgs through mods.channels: every field read before the first
 // operand loads of the GEMM kernels
 constexpr int kGemmHotArgBytes = static_cast<int>(offsetof(GemmArgs, mods) + sizeof(int32_t));
+template <int RCAP>
+constexpr int kGemmArgBytes = static_cast<int>(sizeof(GemmArgsK<RCAP>));
 
 __device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
 #pragma unroll
@@ -203,7 +253,7 @@ __device__ __forceinline__ int64_t prefix_at(const Mods &mods, int idx) {
 // the full set is used and meta[3] flags the overflow (the reference raises
 // OverflowError on the host, which a device-side selector cannot).
 template <int RCAP>
-__device__ __forceinline__ int active_channels(KGemmArgs &g, int64_t *red, int *bcast, int nthreads) {
+__device__ __forceinline__ int active_channels(KArgs<RCAP> &g, int64_t *red, int *bcast, int nthreads) {
   const int full = g.mods.channels;
   if (g.min_channels <= 0) return full;
   const int nw = nthreads >> 6;
@@ -309,7 +359,7 @@ __device__ __forceinline__ void fill_moduli(Epi<RCAP> &e, const Mods &mods, int 
 }
 
 template <int RCAP>
-__device__ __forceinline__ void load_epi(KGemmArgs &g, Epi<RCAP> &e, int c_act) {
+__device__ __forceinline__ void load_epi(KArgs<RCAP> &g, Epi<RCAP> &e, int c_act) {
   fill_moduli<RCAP>(e, g.mods, c_act);
   e.out_dtype = g.out_dtype;
   e.out_ld = g.out_ld;
@@ -544,7 +594,7 @@ __device__ __forceinline__ void store_value(const Epi<RCAP> &e, int64_t y, int64
 // idx = row * out_ld + col, the element's offset in the output; cs the
 // column's float-epilogue factors (col_scale).
 template <int RCAP, bool FAST, int OUT>
-__device__ __forceinline__ void finish_element(KGemmArgs &g, const Epi<RCAP> &e, int c_act,
+__device__ __forceinline__ void finish_element(KArgs<RCAP> &g, const Epi<RCAP> &e, int c_act,
                                                const int32_t (&v)[RCAP], int64_t idx, ColScale cs) {
   const int64_t y = garner_from_sums<RCAP>(e, v, FAST ? RCAP : c_act);
   store_value<RCAP, OUT>(e, y, idx, cs);
@@ -573,7 +623,7 @@ __device__ __forceinline__ void with_epilogue(const Epi<RCAP> &e, int c_act, F &
 // wholly inside the output (nearly every tile) runs a copy of the loop with
 // no per-element bounds test.
 template <int RCAP, int MI, int NJ>
-__device__ __forceinline__ void register_epilogue(KGemmArgs &g, const Epi<RCAP> &e, int c_act,
+__device__ __forceinline__ void register_epilogue(KArgs<RCAP> &g, const Epi<RCAP> &e, int c_act,
                                                   const i32x4 (&acc)[RCAP][MI][NJ], int r0, int c0,
                                                   int m_lim, int n_lim, const ColScale (&cs)[NJ]) {
   const int lane = threadIdx.x & 63;
@@ -650,7 +700,8 @@ struct KRange {
   int ks0, nk, a_k;
 };
 
-__device__ __forceinline__ KRange k_range(KGemmArgs &g, int split) {
+template <typename G>
+__device__ __forceinline__ KRange k_range(G &g, int split) {
   KRange r;
   r.ks0 = split * g.kchunk;
   r.nk = min(g.kchunk, (g.kp >> 6) - r.ks0);
@@ -726,7 +777,7 @@ constexpr bool mfma_splits(int rcap, int mb, int nb) { return rcap <= 4 && nb ==
 // Returns true in the wave that finishes the tile, whose acc then holds
 // sums congruent to the whole-K accumulators.
 template <int RCAP, int MI, int NJ>
-__device__ __forceinline__ bool split_exchange(KGemmArgs &g, const Epi<RCAP> &e, i32x4 (&acc)[RCAP][MI][NJ],
+__device__ __forceinline__ bool split_exchange(KArgs<RCAP> &g, const Epi<RCAP> &e, i32x4 (&acc)[RCAP][MI][NJ],
                                                int64_t slot, int split) {
   static_assert(RCAP <= 4, "one byte per channel in a 32-bit word");
   constexpr int CH = MI * NJ;  // 1 KB chunks per wave and split
@@ -817,8 +868,8 @@ constexpr int stream_u_of(int rcap, bool araw, int mb, int nb, int ucap = 4) {
 }
 
 template <int RCAP, int MB, int NB, bool ARAW, int UCAP>
-__global__ __launch_bounds__(256) void stream_kernel(const GemmArgs args) {
-  KGemmArgs &g = kernel_args<GemmArgs>();
+__global__ __launch_bounds__(256) void stream_kernel(const GemmArgsK<RCAP> args) {
+  KArgs<RCAP> &g = kernel_args<GemmArgsK<RCAP>>();
   prefetch_kernel_args<kGemmHotArgBytes>();
   constexpr int BM = 16 * MB, BN = 16 * NB, TILE = BM * BN;
   constexpr int AP = ARAW ? 1 : RCAP;
@@ -1035,9 +1086,9 @@ constexpr int mfma_ac_of(int rcap, int mb, bool araw) {
 
 // NWV: waves (column groups of 16*NB) per workgroup, 4 or 3.
 template <int RCAP, int MB, int NB, int P, bool ARAW, int NWV = 4>
-__global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgs args) {
-  KGemmArgs &g = kernel_args<GemmArgs>();
-  prefetch_kernel_args<static_cast<int>(sizeof(GemmArgs))>();
+__global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgsK<RCAP> args) {
+  KArgs<RCAP> &g = kernel_args<GemmArgsK<RCAP>>();
+  prefetch_kernel_args<kGemmArgBytes<RCAP>>();
   constexpr int BM = 16 * MB, BNW = 16 * NB;
   constexpr int AP = ARAW ? 1 : RCAP;
   constexpr int PLANE = BM * kLdsRow;
@@ -1225,12 +1276,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 template <int RCAP, int NW>
-__global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
+__global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgsK<RCAP> args) {
   static_assert(RCAP <= 4, "the 256 x 64 x R tile holds R <= 4 channels");
   static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   constexpr int S = kLdsStages;               // even: each step's stage is a constant in a trip
-  KGemmArgs &g = kernel_args<GemmArgs>();
-  prefetch_kernel_args<static_cast<int>(sizeof(GemmArgs))>();
+  KArgs<RCAP> &g = kernel_args<GemmArgsK<RCAP>>();
+  prefetch_kernel_args<kGemmArgBytes<RCAP>>();
   constexpr int AF = kLdsBM / 16;             // A fragments per stage
   constexpr int BF = RCAP * (kLdsBN / 16);    // B fragments per stage
   constexpr int STAGE = (AF + BF) * 1024;
@@ -1440,7 +1491,7 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgs args) {
 // Launchers for one channel capacity (instantiated per translation unit).
 // ---------------------------------------------------------------------------
 template <int RCAP, bool ARAW>
-bool launch_stream(GemmArgs g, int mb, int nb, int ks, int ucap, hipStream_t st) {
+bool launch_stream(GemmArgsK<RCAP> g, int mb, int nb, int ks, int ucap, hipStream_t st) {
 #define RNSMX_STREAM(MB_, NB_, UCAP_)                                                        \
   if (mb == MB_ && nb == NB_ && ucap == UCAP_) {                                            \
     g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                                          \
@@ -1469,7 +1520,7 @@ bool launch_stream(GemmArgs g, int mb, int nb, int ks, int ucap, hipStream_t st)
 // i.e. all of K = 768 in flight, 12.1 us against 11.0 us with 3).  NBSEL: the tile widths this
 // instantiation covers (0 all, 1 or 2 only NB = NBSEL).
 template <int RCAP, bool ARAW, int NBSEL>
-bool launch_mfma(GemmArgs g, int mb, int nb, int p_req, int nwv, hipStream_t st) {
+bool launch_mfma(GemmArgsK<RCAP> g, int mb, int nb, int p_req, int nwv, hipStream_t st) {
 #define RNSMX_MFMA_P(MB_, NB_, P_)                                                          \
   if (p == P_ && nwv == 4) {                                                                \
     hipLaunchKernelGGL((mfma_kernel<RCAP, MB_, NB_, P_, ARAW>), grid, dim3(256), 0, st, g); \
@@ -1547,11 +1598,12 @@ inline GemmGrid gemm_grid(const GemmChoice &c, int64_t m, int64_t n) {
 }
 
 template <int RCAP>
-bool launch_lds(GemmArgs g, bool araw, hipStream_t st) {
+bool launch_lds(const GemmArgs &host, bool araw, hipStream_t st) {
   if constexpr (RCAP != 4) {
     return false;
   } else {
-    if (!lds_kernel_fits(g, araw, RCAP)) return false;
+    if (!lds_kernel_fits(host, araw, RCAP)) return false;
+    GemmArgsK<RCAP> g = compact_args<RCAP>(host);
     g.tiles_m = (g.m + kLdsBM - 1) / kLdsBM;
     g.tiles_n = (g.n + kLdsBN - 1) / kLdsBN;
     const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n * g.splits));
@@ -1568,14 +1620,14 @@ bool launch_gemm_part(const GemmArgs &g, bool araw, const GemmChoice &c, hipStre
     return launch_lds<RCAP>(g, araw, st);
   } else if constexpr (PART == 0) {
     const int ucap = c.kind == kStreamWide ? 8 : 4;
-    return araw ? launch_stream<RCAP, true>(g, c.mb, c.nb, c.ks, ucap, st)
-                : launch_stream<RCAP, false>(g, c.mb, c.nb, c.ks, ucap, st);
+    return araw ? launch_stream<RCAP, true>(compact_args<RCAP>(g), c.mb, c.nb, c.ks, ucap, st)
+                : launch_stream<RCAP, false>(compact_args<RCAP>(g), c.mb, c.nb, c.ks, ucap, st);
   } else {
     const int nwv = c.kind == kMfma3 ? 3 : 4;
     if constexpr (PART == 1 || PART == 2)
-      return launch_mfma<RCAP, true, PART>(g, c.mb, c.nb, c.ks, nwv, st);
+      return launch_mfma<RCAP, true, PART>(compact_args<RCAP>(g), c.mb, c.nb, c.ks, nwv, st);
     else
-      return launch_mfma<RCAP, false, 0>(g, c.mb, c.nb, c.ks, nwv, st);
+      return launch_mfma<RCAP, false, 0>(compact_args<RCAP>(g), c.mb, c.nb, c.ks, nwv, st);
   }
 }
 

@@ -39,6 +39,8 @@ EXPORTED_SYMBOLS = (
     "rnsmx_matmul_residues_prepared",
     "rnsmx_gemm_plan",
     "rnsmx_quantize_symmetric",
+    "rnsmx_linear_workspace_bytes",
+    "rnsmx_linear_forward",
     "rnsmx_decode_garner",
 )
 
@@ -140,6 +142,10 @@ _SIGNATURES = {
                ctypes.POINTER(Epilogue), _P, _P]),
     "rnsmx_gemm_plan": (_I32, [_I64, _I64, _I64, _I32, _I32, ctypes.POINTER(Plan)]),
     "rnsmx_quantize_symmetric": (_I32, [_P, _I32, _I64, _I32, _P, _P, _P, _P]),
+    "rnsmx_linear_workspace_bytes": (_I64, [_I64, _I64, _I64, _I32, _I32]),
+    "rnsmx_linear_forward": (
+        _I32, [_P, _I32, _I32, _I32, _I32, _I32, _P, ctypes.POINTER(Moduli), _P, _P,
+               ctypes.POINTER(Adaptive), _P, _I64, _P, _P]),
     "rnsmx_decode_garner": (_I32, [_P, _I64, ctypes.POINTER(Moduli), _P, _P]),
 }
 

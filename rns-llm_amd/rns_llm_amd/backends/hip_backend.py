@@ -182,6 +182,8 @@ class AdaptiveMetadata(Mapping):
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_FLOAT_CODES = {torch.float32: _native.FLOAT32, torch.float16: _native.FLOAT16,
+                torch.bfloat16: _native.BFLOAT16}
 
 
 def _stream_handle(device: torch.device) -> int:
@@ -196,6 +198,69 @@ def _stream_handle(device: torch.device) -> int:
 
 def _aligned(t: torch.Tensor) -> torch.Tensor:
     return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+class LinearCall:
+    """``RNSLinear.forward``'s device work bound to one prepared weight: one
+    ``rnsmx_linear_forward`` call per forward (activation quantization, then
+    the GEMM with the dequant epilogue), with every per-weight argument
+    resolved once here instead of on each call.  Counts the backend stats
+    the reference's forward counts (one activation encode, one fused GEMM)."""
+
+    def __init__(self, backend: "HipRNSBackend", prepared: "PreparedRNSWeight", w_scale: torch.Tensor,
+                 bias: torch.Tensor | None, quant_bits: int, adaptive: "PreparedAdaptiveRNSWeight | None"):
+        device = prepared.packed.device
+        consts = backend._constants(device, prepared.moduli)
+        self._fn = backend._lib.rnsmx_linear_forward
+        self._bytes_fn = backend._lib.rnsmx_linear_workspace_bytes
+        self._keep = (prepared, w_scale, bias, consts, adaptive)  # the pointers below stay valid
+        self._packed = prepared.packed.data_ptr()
+        self._mods = consts.native_ref
+        self._w_scale = w_scale.data_ptr()
+        self._bias = None if bias is None else bias.data_ptr()
+        self.k, self.n, self.bits = prepared.k, prepared.n, int(quant_bits)
+        self.channels = len(prepared.moduli)
+        self._index = device.index if device.index is not None else torch.cuda.current_device()
+        self._adaptive = adaptive
+        self._full_moduli = prepared.moduli
+        self._stats = backend._stats
+        self._gemm_key = f"fused_gemm_channels_{self.channels}"
+        self._ws_bytes: dict[int, int] = {}
+
+    def workspace_bytes(self, rows: int) -> int:
+        nbytes = self._ws_bytes.get(rows)
+        if nbytes is None:
+            nbytes = int(self._bytes_fn(rows, self.k, self.n, self.channels, self.bits))
+            if nbytes < 0:
+                raise ValueError("bad linear shape")
+            self._ws_bytes[rows] = nbytes
+        return nbytes
+
+    def __call__(self, x: torch.Tensor, rows: int, out: torch.Tensor, scratch: torch.Tensor):
+        """x: contiguous float activations holding [rows, K]; out: contiguous,
+        of x's dtype, holding [rows, N]; scratch: zero-initialised uint8 of
+        workspace_bytes(rows).  Returns the adaptive metadata when the layer
+        is adaptive, else None."""
+        meta = adaptive = None
+        if self._adaptive is not None:
+            meta = torch.empty((4,), dtype=torch.int64, device=x.device)
+            adaptive = ctypes.byref(_native.Adaptive(self._adaptive.min_channels,
+                                                     self._adaptive.absmax.data_ptr(), meta.data_ptr()))
+        rc = self._fn(x.data_ptr(), _FLOAT_CODES[x.dtype], rows, self.k, self.n, self.bits, self._packed,
+                      self._mods, self._w_scale, self._bias, adaptive, scratch.data_ptr(), scratch.numel(),
+                      out.data_ptr(), _raw_stream(self._index) if _raw_stream is not None
+                      else torch.cuda.current_stream().cuda_stream)
+        if rc:
+            _native.check(rc)
+        stats = self._stats
+        stats["encode_centered_calls"] += 1
+        stats["encode_centered_values"] += rows * self.k
+        stats["fused_gemm_calls"] += 1
+        if meta is None:
+            stats[self._gemm_key] += 1
+            return None
+        stats["adaptive_selections"] += 1
+        return AdaptiveMetadata(meta, self._full_moduli, stats)
 
 
 class HipRNSBackend:
@@ -351,6 +416,26 @@ class HipRNSBackend:
     @staticmethod
     def supports_fused(prepared) -> bool:
         return getattr(prepared, "packed", None) is not None
+
+    def bind_linear(self, prepared: PreparedRNSWeight, w_scale: torch.Tensor, bias: torch.Tensor | None,
+                    quant_bits: int, adaptive: PreparedAdaptiveRNSWeight | None = None) -> LinearCall | None:
+        """A ``LinearCall`` for ``RNSLinear.forward`` on this prepared weight
+        (float32 ``w_scale`` [N] and ``bias`` [N] or None), or None when the
+        one-call path cannot serve it: an adaptive weight whose device-side
+        selection is not proven safe takes the synchronous selection."""
+        if adaptive is not None and not adaptive.device_selection_is_safe(
+                torch.int8 if quant_bits == 8 else torch.int16):
+            return None
+        for name, t in (("w_scale", w_scale), ("bias", bias)):
+            if t is not None and (t.dtype != torch.float32 or t.numel() != prepared.n
+                                  or not t.is_contiguous() or t.device != prepared.packed.device):
+                raise ValueError(f"{name} must be a contiguous float32 [N] tensor on the weight's device")
+        return LinearCall(self, prepared, w_scale, bias, quant_bits, adaptive)
+
+    def create_linear_scratch(self, call: LinearCall, rows: int, device: torch.device) -> torch.Tensor:
+        """Zero-filled scratch for ``call`` at ``rows`` rows (the library's
+        K-split counters at its start must be zero at first use)."""
+        return torch.zeros((call.workspace_bytes(rows),), dtype=torch.uint8, device=device)
 
     # ------------------------------------------------------------------
     # Workspaces (cuda_backend.py:366-396)

@@ -14,9 +14,11 @@ reference's ``src/rns_llm/layers/rns_linear.py:17-275``:
 With the HIP backend the dequantization runs inside the GEMM epilogue
 (``fused_epilogue=True``, the default): the same float32 operations in the
 same order, each rounded to nearest even, so the result is bit-identical to
-the torch chain while saving its five elementwise launches.  Any other
-backend object with the reference contract is driven exactly as the
-reference drives it.
+the torch chain while saving its five elementwise launches.  The whole
+device part of a forward (activation quantization, GEMM, epilogue) is then
+one call into the library (``bind_linear``), bound once per prepared
+weight.  Any other backend object with the reference contract is driven
+exactly as the reference drives it.
 """
 from __future__ import annotations
 
@@ -29,6 +31,7 @@ from torch.nn import functional as F
 from ..moduli import choose_moduli_for_dot, validate_moduli
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_FLOAT_OUT = (torch.float32, torch.float16, torch.bfloat16)
 
 
 def _current_stream_handle(device: torch.device) -> int:
@@ -82,6 +85,9 @@ class RNSLinear(nn.Module):
         self._adaptive_prepared_weight = None
         self._workspace_by_rows: dict[tuple[int, int, int], object] = {}
         self.last_adaptive_metadata = None
+        self._linear_call = None
+        self._linear_key = None
+        self._linear_scratch: dict[tuple[int, int], torch.Tensor] = {}
         self.reset_parameters()
 
     @property
@@ -109,6 +115,9 @@ class RNSLinear(nn.Module):
         self._adaptive_prepared_weight = None
         self._workspace_by_rows = {}
         self.last_adaptive_metadata = None
+        self._linear_call = None
+        self._linear_key = None
+        self._linear_scratch = {}
 
     @classmethod
     def from_linear(cls, layer: nn.Linear, *, backend=None, moduli=None,
@@ -188,6 +197,31 @@ class RNSLinear(nn.Module):
         self._adaptive_prepared_weight = adaptive_prepared
         self._prepared_weight_version = version
         self._workspace_by_rows = {}
+        self._linear_call = None
+        self._linear_key = None
+
+    def _live_key(self):
+        """What the bound one-call forward depends on: the weight version and
+        the identity of the bias values (their float32 copy is bound)."""
+        bias = self.bias
+        return (self.weight._version,
+                None if bias is None else (bias.data_ptr(), bias._version, bias.dtype))
+
+    def _bind_linear(self):
+        """The backend's one-call forward for the current weight and bias
+        (None when the backend has none, or cannot serve this layer).  The
+        weight must be prepared."""
+        key = self._live_key()
+        if key != self._linear_key:
+            self._linear_call = None
+            bind = getattr(self.backend, "bind_linear", None)
+            if bind is not None and self.fused and self.fused_epilogue:
+                self._linear_call = bind(self._prepared_weight, self._weight_scale, self._bias_float(),
+                                         self.quant_bits,
+                                         self._adaptive_prepared_weight if self.adaptive_channels else None)
+            self._linear_key = key
+            self._linear_scratch = {}
+        return self._linear_call
 
     def _workspace(self, rows: int, channels: int | None = None):
         channels = len(self.moduli) if channels is None else int(channels)
@@ -209,6 +243,23 @@ class RNSLinear(nn.Module):
         return self._prepared_weight.kernel == "cublas"
 
     def forward(self, inputs: torch.Tensor) -> torch.Tensor:
+        call = self._linear_call
+        if (call is not None and self.mode == "rns" and not self.training and inputs.is_cuda
+                and inputs.dtype in _FLOAT_OUT and self._linear_key == self._live_key()):
+            # prepared weight, unchanged since the call was bound: one library
+            # call (quantize, GEMM, dequant epilogue) into a fresh output
+            x = inputs if inputs.is_contiguous() else inputs.contiguous()
+            rows = x.numel() // self.in_features
+            key = (rows, _current_stream_handle(x.device))
+            scratch = self._linear_scratch.get(key)
+            if scratch is None:
+                scratch = self.backend.create_linear_scratch(call, rows, x.device)
+                self._linear_scratch[key] = scratch
+            out = torch.empty(inputs.shape[:-1] + (self.out_features,), dtype=inputs.dtype, device=x.device)
+            metadata = call(x, rows, out, scratch)
+            if metadata is not None:
+                self.last_adaptive_metadata = metadata
+            return out
         if self.mode == "torch":
             return F.linear(inputs, self.weight, self.bias)
         if self.mode != "rns":
@@ -221,6 +272,9 @@ class RNSLinear(nn.Module):
         self.prepare_weight()
         original_shape = inputs.shape[:-1]
         flat = inputs.reshape(-1, self.in_features)
+        if inputs.dtype in _FLOAT_OUT and inputs.is_cuda:
+            if self._bind_linear() is not None:
+                return self.forward(inputs)  # the bound path above
         if (hasattr(self.backend, "quantize_symmetric") and flat.is_cuda
                 and flat.dtype in (torch.float32, torch.float16, torch.bfloat16)):
             # the same scale and integers as the torch chain below, in two launches

@@ -463,7 +463,8 @@ def test_rnslinear_weight_version_invalidates_cache(backend):
 # activation quantization (RNSLinear._symmetric_scale / _quantize)
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("shape", [(1, 768), (3, 100), (256, 768), (4096, 768), (2, 5, 33)])
+@pytest.mark.parametrize("shape", [(1, 768), (3, 100), (256, 768), (4096, 768), (2, 5, 33),
+                                   (16, 1024), (1, 16385)])  # one-workgroup form up to 16384 values
 @pytest.mark.parametrize("bits", [8, 12])
 def test_quantize_symmetric_matches_reference_chain(backend, dtype, shape, bits):
     gen = torch.Generator().manual_seed(sum(shape) + bits)
