@@ -88,7 +88,9 @@ typedef struct rnsmx_moduli {
  * 48*nb; int8 activations read in place, up to 4 channels).
  * splits: workgroups splitting K per output tile (0 or 1 = none; up to 4
  * channels, and for the stream kernel ks = 1): each reduces its partial
- * sums to residues, and the last to finish a tile reconstructs it.  A plan
+ * sums to residues, and the last to finish a tile reconstructs it.  tail:
+ * split only the tiles past the last full round of 256 (the others run
+ * whole, first).  A plan
  * that names a kernel that is not built, or does not fit the call, makes the
  * call fail with RNSMX_EINVAL.  Results never depend on the plan.  No
  * counterpart in the reference (cuBLAS picks its own kernels there); for
@@ -98,6 +100,7 @@ typedef struct rnsmx_plan {
   int32_t kind;
   int32_t mb, nb, ks;
   int32_t splits;
+  int32_t tail;
 } rnsmx_plan_t;
 
 /* Thread-local text of the last error (empty string when none). */

@@ -73,10 +73,11 @@ struct GemmArgsOf {
   int32_t tiles_m, tiles_n;  // output tile grid (set at launch)
   int32_t threads;           // workgroup size (set at launch; read here rather than
                              // from the hidden arguments, a cache line of its own)
-  // K split over workgroups (split_exchange): every output tile is computed
-  // by `splits` workgroups, split s taking K steps [s * kchunk, (s + 1) *
-  // kchunk) (the last one the rest); splits = 1, kchunk = kp / 64 otherwise
-  int32_t splits, kchunk;
+  // K split over workgroups (split_exchange): tiles [0, split_from) run
+  // whole; every later tile is computed by `splits` workgroups, split s
+  // taking K steps [s * kchunk, (s + 1) * kchunk) (the last one the rest).
+  // splits = 1, split_from = tiles, kchunk = kp / 64 without a split.
+  int32_t splits, kchunk, split_from;
   uint32_t *tickets;  // one arrival counter per (tile, wave), zero between calls
   int8_t *xchg;       // partial residues, [tile * waves + wave][split][MI * NJ][4 words][64 lanes] x 4 bytes
   // adaptive prefix
@@ -123,9 +124,10 @@ inline GemmArgsK<RCAP> compact_args(const GemmArgs &g) {
 enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kLds = 3, kStreamWide = 4, kMfma3 = 5 };
 
 // ks: waves splitting K (stream kernel) or ring depth, 0 = automatic (MFMA
-// kernel); splits: workgroups splitting K (1 = none).
+// kernel); splits: workgroups splitting K (1 = none); tail: only the tiles
+// of the last, partial round of 256 are split (the others run whole).
 struct GemmChoice {
-  int kind, mb, nb, ks, splits;
+  int kind, mb, nb, ks, splits, tail;
 };
 
 // Geometry of one launch: output tiles, waves per workgroup, and the 16-byte
@@ -673,23 +675,47 @@ __device__ __forceinline__ i32x4 select16(bool keep, i32x4 v) {
   return keep ? v : zero;
 }
 
-// Workgroup -> (output tile, K split).  Workgroups are handed to the 8 XCDs
-// round-robin (workgroup b runs on XCD b % 8), and each XCD has its own L2.
-// Work units are numbered split-major, then M-block fastest, so giving
-// every XCD one contiguous run of unit numbers keeps the workgroups that
-// read the same weight columns (and K range) on the same L2.  The map is a
-// bijection on [0, tiles * splits) for any count.
-__device__ __forceinline__ void tile_of(int tiles_m, int tiles_n, int splits, int &mt, int &nt, int &split) {
-  const int tiles = tiles_m * tiles_n;
-  const int total = tiles * splits;
-  const int b = blockIdx.x;
+// Bijection of [0, total) that gives each XCD one contiguous run of unit
+// numbers.  Workgroups are handed to the 8 XCDs round-robin (workgroup b
+// runs on XCD b % 8), and each XCD has its own L2; units are numbered
+// M-block fastest, so contiguous runs keep the workgroups that read the
+// same weight columns (and K range) on the same L2.
+__device__ __forceinline__ int xcd_order(int b, int total) {
   const int xcd = b & 7, local = b >> 3;
   const int base = total >> 3, rem = total & 7;
-  const int t = xcd * base + min(xcd, rem) + local;
-  split = t / tiles;
-  const int u = t - split * tiles;
-  mt = u % tiles_m;
-  nt = u / tiles_m;
+  return xcd * base + min(xcd, rem) + local;
+}
+
+// What one workgroup computes: output tile (mt, nt) and its K split
+// (split < 0: the whole K range), and for a split tile its index among the
+// split tiles (the exchange slot).  Workgroups [0, split_from) take the
+// whole tiles [0, split_from): they are dispatched first and spread over
+// every XCD.  The rest take (tile, split) units of the tiles from
+// split_from on, split-major.
+struct WorkUnit {
+  int mt, nt, split, split_tile;
+};
+
+template <typename G>
+__device__ __forceinline__ WorkUnit work_of(G &g) {
+  const int tiles = g.tiles_m * g.tiles_n;
+  const int whole = g.split_from;
+  const int b = blockIdx.x;
+  WorkUnit w;
+  int t;
+  if (b < whole) {
+    t = xcd_order(b, whole);
+    w.split = -1;
+  } else {
+    const int parted = tiles - whole;
+    const int u = xcd_order(b - whole, parted * g.splits);
+    w.split = u / parted;
+    t = whole + (u - w.split * parted);
+  }
+  w.mt = t % g.tiles_m;
+  w.nt = t / g.tiles_m;
+  w.split_tile = t - whole;
+  return w;
 }
 
 // The K range of one split, in 64-byte steps from ks0: nk steps (at least
@@ -703,9 +729,15 @@ struct KRange {
 template <typename G>
 __device__ __forceinline__ KRange k_range(G &g, int split) {
   KRange r;
-  r.ks0 = split * g.kchunk;
-  r.nk = min(g.kchunk, (g.kp >> 6) - r.ks0);
-  r.a_k = g.a_k - r.ks0 * 64;
+  if (split < 0) {
+    r.ks0 = 0;
+    r.nk = g.kp >> 6;
+    r.a_k = g.a_k;
+  } else {
+    r.ks0 = split * g.kchunk;
+    r.nk = min(g.kchunk, (g.kp >> 6) - r.ks0);
+    r.a_k = g.a_k - r.ks0 * 64;
+  }
   return r;
 }
 
@@ -881,8 +913,8 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgsK<RCAP> args)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nthreads = g.threads, ks_n = nthreads >> 6;
   const int c_act = active_channels<RCAP>(g, red, &bcast, nthreads);
-  int mt, nt, split;
-  tile_of(g.tiles_m, g.tiles_n, g.splits, mt, nt, split);
+  const WorkUnit wu = work_of(g);
+  const int mt = wu.mt, nt = wu.nt, split = wu.split;
   const int m0 = mt * BM, n0 = nt * BN;
   const KRange kr = k_range(g, split);
   const int nk = kr.nk, a_k = kr.a_k;
@@ -983,7 +1015,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgsK<RCAP> args)
     // a K split over workgroups (one wave each): only the last to finish
     // this tile goes on
     if constexpr (stream_splits(RCAP, MB, NB)) {
-      if (g.splits > 1 && !split_exchange<RCAP, MB, NB>(g, e, acc, mt + static_cast<int64_t>(nt) * g.tiles_m, split))
+      if (split >= 0 && !split_exchange<RCAP, MB, NB>(g, e, acc, wu.split_tile, split))
         return;
     }
     const int64_t idx0 = static_cast<int64_t>(m0 + 4 * (lane >> 4)) * e.out_ld + n0 + (lane & 15);
@@ -1103,8 +1135,8 @@ __global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgsK<RCAP> ar
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c_act = active_channels<RCAP>(g, red, &bcast, NT);
-  int mt, nt, split;
-  tile_of(g.tiles_m, g.tiles_n, g.splits, mt, nt, split);
+  const WorkUnit wu = work_of(g);
+  const int mt = wu.mt, nt = wu.nt, split = wu.split;
   const int m0 = mt * BM, n0 = nt * (NWV * BNW) + wave * BNW;
   const KRange kr = k_range(g, split);
   const int nk = kr.nk, a_k = kr.a_k;
@@ -1225,8 +1257,8 @@ __global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgsK<RCAP> ar
   trip(steps - P, std::false_type{});
 
   if constexpr (mfma_splits(RCAP, MB, NB)) {
-    if (g.splits > 1 &&
-        !split_exchange<RCAP, MB, NB>(g, e, acc, (mt + static_cast<int64_t>(nt) * g.tiles_m) * NWV + wave, split))
+    if (split >= 0 &&
+        !split_exchange<RCAP, MB, NB>(g, e, acc, static_cast<int64_t>(wu.split_tile) * NWV + wave, split))
       return;
   }
   register_epilogue<RCAP, MB, NB>(g, e, c_act, acc, m0, n0, m_lim, n_lim, cs);
@@ -1296,8 +1328,8 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgsK<RCAP> args
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int c_act = active_channels<RCAP>(g, red, &bcast, 64 * NW);
-  int mt, nt, split;
-  tile_of(g.tiles_m, g.tiles_n, g.splits, mt, nt, split);
+  const WorkUnit wu = work_of(g);
+  const int mt = wu.mt, nt = wu.nt, split = wu.split;
   const int m0 = mt * kLdsBM, n0 = nt * kLdsBN;
   const KRange kr = k_range(g, split);
   const int nk = kr.nk;  // a multiple of the stage count (the launcher sizes kchunk so)
@@ -1481,8 +1513,8 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgsK<RCAP> args
   // the loads issued for steps past K land before the workgroup ends
   wait_vmcnt<0>();
 
-  if (g.splits > 1 &&
-      !split_exchange<RCAP, MI, NJ>(g, e, acc, (mt + static_cast<int64_t>(nt) * g.tiles_m) * NW + wave, split))
+  if (split >= 0 &&
+      !split_exchange<RCAP, MI, NJ>(g, e, acc, static_cast<int64_t>(wu.split_tile) * NW + wave, split))
     return;
   register_epilogue<RCAP, MI, NJ>(g, e, c_act, acc, rw0, cw0, m_lim, n_lim, cs);
 }
@@ -1496,7 +1528,7 @@ bool launch_stream(GemmArgsK<RCAP> g, int mb, int nb, int ks, int ucap, hipStrea
   if (mb == MB_ && nb == NB_ && ucap == UCAP_) {                                            \
     g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                                          \
     g.tiles_n = (g.n + 16 * NB_ - 1) / (16 * NB_);                                          \
-    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n * g.splits));               \
+    const dim3 grid(static_cast<unsigned>(g.split_from + (g.tiles_m * g.tiles_n - g.split_from) * g.splits));               \
     const size_t lds = ks > 1 ? static_cast<size_t>(RCAP) * 256 * MB_ * NB_ * 4 : 0;         \
     g.threads = 64 * ks;                                                                    \
     hipLaunchKernelGGL((stream_kernel<RCAP, MB_, NB_, ARAW, UCAP_>), grid, dim3(64 * ks), lds, st, g); \
@@ -1538,7 +1570,7 @@ bool launch_mfma(GemmArgsK<RCAP> g, int mb, int nb, int p_req, int nwv, hipStrea
     if (mb == MB_ && nb == NB_) {                                          \
       g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                       \
       g.tiles_n = (g.n + 16 * nwv * NB_ - 1) / (16 * nwv * NB_);           \
-      const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n * g.splits)); \
+      const dim3 grid(static_cast<unsigned>(g.split_from + (g.tiles_m * g.tiles_n - g.split_from) * g.splits)); \
       const int p = p_req > 0 ? p_req : PDEF;                              \
       __VA_ARGS__                                                          \
       return false;                                                        \
@@ -1606,7 +1638,7 @@ bool launch_lds(const GemmArgs &host, bool araw, hipStream_t st) {
     GemmArgsK<RCAP> g = compact_args<RCAP>(host);
     g.tiles_m = (g.m + kLdsBM - 1) / kLdsBM;
     g.tiles_n = (g.n + kLdsBN - 1) / kLdsBN;
-    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n * g.splits));
+    const dim3 grid(static_cast<unsigned>(g.split_from + (g.tiles_m * g.tiles_n - g.split_from) * g.splits));
     hipLaunchKernelGGL((lds_kernel<RCAP, 8>), grid, dim3(512), 0, st, g);
     return true;
   }

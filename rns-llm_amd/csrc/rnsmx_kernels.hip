@@ -481,6 +481,15 @@ static void split_steps(const GemmChoice &c, int nk, int &splits, int &kchunk) {
   splits = (nk + kchunk - 1) / kchunk;
 }
 
+// Tiles that run whole (workgroups [0, whole) of the launch): all of them
+// without a split, none with a uniform split, and with a tail split those of
+// the full rounds of 256 (one workgroup per CU: the LDS kernel).
+static int64_t whole_tiles(const GemmChoice &c, int64_t tiles) {
+  if (c.splits <= 1) return tiles;
+  if (!c.tail) return 0;
+  return (tiles - 1) / 256 * 256;
+}
+
 // Whether `c` may split K: a tile built with the exchange (stream_splits,
 // mfma_splits: up to 4 channels, one residue byte per channel in the
 // exchange word), one wave per stream workgroup (the waves of a larger one
@@ -496,7 +505,7 @@ static bool split_fits(const GemmChoice &c, const GemmArgs &g) {
     built = rcap <= 4;
   else
     built = mfma_splits(rcap, c.mb, c.nb);
-  return built && gr.tiles * gr.waves <= RNSMX_SPLIT_TICKETS;
+  return built && (gr.tiles - whole_tiles(c, gr.tiles)) * gr.waves <= RNSMX_SPLIT_TICKETS;
 }
 
 // Exchange-area bytes of a choice (0 without a split).
@@ -506,7 +515,8 @@ static int64_t xchg_bytes(const GemmChoice &c, const GemmArgs &g) {
   split_steps(c, g.kp / 64, splits, kchunk);
   if (splits <= 1) return 0;
   const GemmGrid gr = gemm_grid(c, g.m, g.n);
-  return round_up(gr.tiles * gr.waves * splits * gr.chunks * 1024, 256);
+  const int64_t parted = gr.tiles - whole_tiles(c, gr.tiles);
+  return round_up(parted * gr.waves * splits * gr.chunks * 1024, 256);
 }
 
 // The automatic split count for a choice of kernel and tile, from sweeps on
@@ -532,11 +542,24 @@ static int64_t xchg_bytes(const GemmChoice &c, const GemmArgs &g) {
 // least 16 K steps per split and at most 512 workgroups (for the stream
 // kernel only when that is 4 or more); 128-511 tiles of the MFMA or LDS
 // kernel, 2 splits once K >= 8192; otherwise none.
+// The LDS kernel runs one workgroup per CU, so its tiles go in rounds of
+// 256; when the last round holds at most half that (and K is long), only
+// that round's tiles are split (tail), over the CUs it would leave idle:
+// C5 M=512 (384 tiles, 1.5 rounds) runs 256 whole tiles, then 128 tiles in
+// two halves of K.
 static int choose_splits(const GemmChoice &c, const GemmArgs &g) {
   const int nk = g.kp / 64;
   const int64_t tiles = gemm_grid(c, g.m, g.n).tiles;
   const bool stream = c.kind == kStream || c.kind == kStreamWide;
   int s = 1;
+  if (c.kind == kLds && tiles >= 256) {
+    const int64_t last = tiles - (tiles - 1) / 256 * 256;  // tiles of the last round
+    if (last <= 128 && nk >= 32) {
+      const int64_t cap = std::min<int64_t>(4, 256 / last);
+      while (2 * s <= cap) s *= 2;
+    }
+    return s;
+  }
   if (tiles < 128) {
     const int64_t cap = std::min<int64_t>(std::min<int64_t>(8, 512 / tiles), nk / 16);
     while (2 * s <= cap) s *= 2;
@@ -555,6 +578,7 @@ static GemmChoice auto_plan(const GemmArgs &g, bool araw, bool allow_split) {
   GemmChoice t = c;
   if (t.kind == kStream || t.kind == kStreamWide) t.ks = 1;
   t.splits = choose_splits(c, g);
+  t.tail = t.kind == kLds && gemm_grid(t, g.m, g.n).tiles >= 256;
   if (t.splits > 1 && split_fits(t, g)) return t;
   return c;
 }
@@ -569,7 +593,7 @@ static int32_t plan_from(const rnsmx_plan_t *plan, const GemmArgs &g, bool araw,
   if (k != kStream && k != kMfma && k != kLds && k != kStreamWide && k != kMfma3)
     return fail(RNSMX_EINVAL, "plan kind must be 0 (auto), 1 (stream), 2 (mfma), 3 (lds), 4 (wide stream) or 5 (3-wave mfma)");
   if (k != kLds && (plan->mb < 1 || plan->nb < 1)) return fail(RNSMX_EINVAL, "tile blocks must be positive");
-  c = GemmChoice{k, plan->mb, plan->nb, plan->ks, std::max(1, plan->splits)};
+  c = GemmChoice{k, plan->mb, plan->nb, plan->ks, std::max(1, plan->splits), plan->tail != 0};
   if (c.splits > 1 && (!allow_split || !split_fits(c, g)))
     return fail(RNSMX_EINVAL, "this plan cannot split K over workgroups (channels, stream waves, or counters)");
   return RNSMX_OK;
@@ -592,6 +616,8 @@ static int32_t launch_gemm(GemmArgs g, bool araw, const GemmChoice &c, uint32_t 
   g.kchunk = g.kp / 64;
   g.tickets = tickets;
   g.xchg = xchg;
+  const int64_t tiles = gemm_grid(c, g.m, g.n).tiles;
+  g.split_from = static_cast<int32_t>(tiles);
   if (c.splits > 1) {
     if (c.kind == kLds && !lds_kernel_fits(g, araw, rcap)) {
       set_error("no GEMM kernel for kind %d, tile %d x %d, %d channels", c.kind, c.mb, c.nb, g.mods.channels);
@@ -600,6 +626,7 @@ static int32_t launch_gemm(GemmArgs g, bool araw, const GemmChoice &c, uint32_t 
     split_steps(c, g.kp / 64, g.splits, g.kchunk);
     if (g.splits > 1 && (tickets == nullptr || xchg == nullptr))
       return fail(RNSMX_EINVAL, "a K split needs the workspace's counters and exchange area");
+    if (g.splits > 1) g.split_from = static_cast<int32_t>(whole_tiles(c, tiles));
   }
   using PartFn = bool (*)(const GemmArgs &, bool, const GemmChoice &, hipStream_t);
 #define RNSMX_PARTS(R)                                                                      \
@@ -930,7 +957,7 @@ int32_t rnsmx_matmul_centered_fused_out(const int8_t *a_dev, const int8_t *b_dev
   {
     const int64_t total = R * n16 * nk * 64;
     const GemmGrid gr = gemm_grid(c, m, n);
-    const int64_t ntickets = c.splits > 1 ? gr.tiles * gr.waves : 0;
+    const int64_t ntickets = c.splits > 1 ? (gr.tiles - whole_tiles(c, gr.tiles)) * gr.waves : 0;
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 16384));
     hipLaunchKernelGGL(transpose_frag_kernel, dim3(blocks), dim3(256), 0, st, b_dev, static_cast<int64_t>(k),
                        static_cast<int64_t>(n), n16, nk, total, b_nk, tickets, ntickets);
@@ -1234,6 +1261,7 @@ int32_t rnsmx_gemm_plan(int64_t m, int64_t n, int64_t k, int32_t channels, int32
   out->nb = c.nb;
   out->ks = c.ks;
   out->splits = c.splits;
+  out->tail = c.splits > 1 ? c.tail : 0;
   return RNSMX_OK;
 }
 

@@ -85,21 +85,21 @@ class Plan(ctypes.Structure):
         ("nb", ctypes.c_int32),
         ("ks", ctypes.c_int32),
         ("splits", ctypes.c_int32),
+        ("tail", ctypes.c_int32),
     ]
 
-    def as_tuple(self) -> tuple[int, int, int, int, int]:
-        return (self.kind, self.mb, self.nb, self.ks, self.splits)
+    def as_tuple(self) -> tuple[int, ...]:
+        return (self.kind, self.mb, self.nb, self.ks, self.splits, self.tail)
 
 
 def make_plan(plan) -> "Plan | None":
-    """A ``Plan`` from a (kind, mb, nb, ks[, splits]) tuple; None stays None."""
+    """A ``Plan`` from a (kind, mb, nb, ks[, splits[, tail]]) tuple; None stays None."""
     if plan is None or isinstance(plan, Plan):
         return plan
     fields = tuple(int(v) for v in plan)
-    if len(fields) == 4:
-        fields += (1,)
-    if len(fields) != 5:
-        raise ValueError("a plan is (kind, mb, nb, ks) or (kind, mb, nb, ks, splits)")
+    fields += (1, 0)[len(fields) - 4:] if 4 <= len(fields) < 6 else ()
+    if len(fields) != 6:
+        raise ValueError("a plan is (kind, mb, nb, ks[, splits[, tail]])")
     return Plan(*fields)
 
 
@@ -149,7 +149,7 @@ _SIGNATURES = {
     "rnsmx_decode_garner": (_I32, [_P, _I64, ctypes.POINTER(Moduli), _P, _P]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class NativeError(RuntimeError):

@@ -224,6 +224,13 @@ def test_split_k_lds_kernel(backend, m, k, n, splits):
     run_case(backend, DENSE4, m, k, n, seed=m + splits, plan=(3, 0, 0, 0, splits), repeat=2)
 
 
+@pytest.mark.parametrize("m,n,splits", [(517, 64 * 90 - 3, 2), (256 * 2 + 9, 64 * 100 + 5, 4), (300, 64 * 160, 2)])
+def test_tail_split_lds_kernel(backend, m, n, splits):
+    # tiles past the last full round of 256 split (270, 300 and 320 tiles:
+    # 14, 44 and 64 split tiles), the others whole; ragged M and N
+    run_case(backend, DENSE4, m, 1024, n, seed=m + n, plan=(3, 0, 0, 0, splits, 1), repeat=2)
+
+
 @pytest.mark.parametrize("plan", [(1, 1, 1, 1, 4), (2, 3, 1, 4, 2), (5, 2, 1, 4, 2), (3, 0, 0, 0, 2)])
 def test_split_k_adaptive_prefix(backend, plan):
     k = 512

@@ -52,43 +52,46 @@ def gemm_plan(m, n, k, channels=4, raw_a=1):
 # 3 LDS-staged, 4 stream with 8-step chunks, 5 MFMA with 48-column tiles;
 # splits: workgroups sharing each output tile's K range
 PLANS = [
-    ((1, 2304, 768, 4), (1, 1, 1, 3, 1)),       # decode: stream, 3 waves split 12 K steps
-    ((64, 2304, 768, 4), (1, 1, 1, 3, 1)),      # stream up to 64 rows at short K
-    ((96, 2304, 768, 4), (1, 2, 1, 3, 1)),      # stream: 432 tiles of 32 x 16
-    ((128, 768, 768, 4), (1, 2, 1, 3, 1)),      # stream: 192 tiles
-    ((128, 2304, 768, 4), (5, 2, 1, 4, 1)),     # 576 stream tiles: MFMA, 32 x 48 (192 tiles)
-    ((256, 1536, 768, 4), (5, 2, 1, 4, 1)),     # 32 x 48 fills 256 CUs (32 x 64: 192)
-    ((256, 3072, 768, 4), (5, 4, 1, 4, 1)),     # 64 x 48, 256 tiles, ties 64 x 64 on rows
-    ((256, 3072, 1024, 4), (5, 4, 1, 4, 1)),
-    ((128, 2304, 768, 6), (2, 2, 1, 4, 1)),     # 48-column tiles only up to 4 channels
-    ((224, 2304, 768, 4), (2, 2, 1, 4, 1)),     # 252 tiles of 32 rows: one round
-    ((256, 2304, 768, 4), (2, 3, 1, 4, 1)),     # headline: 216 tiles of 48 rows
-    ((320, 2304, 768, 4), (2, 3, 1, 4, 1)),     # 252 tiles of 48 rows
-    ((384, 2304, 768, 4), (2, 4, 1, 0, 1)),     # 64 rows (216 tiles) tie 32 rows (2 rounds)
-    ((256, 4608, 768, 4), (2, 3, 1, 4, 1)),     # no height fits one round: 48 rows (2 rounds)
-    ((256, 2304, 768, 6), (2, 4, 1, 0, 1)),     # no 48-row tile past 4 channels
-    ((4096, 2304, 768, 4), (2, 4, 1, 0, 1)),    # C4 QKV: over 512 tiles at every height
-    ((1, 12288, 4096, 4), (4, 1, 1, 4, 1)),     # C5 decode: stream with 8-step chunks
-    ((16, 12288, 4096, 4), (4, 1, 1, 4, 1)),    # long K, 16 rows: stream, 8-step chunks
-    ((16, 2048, 2048, 4), (1, 1, 1, 4, 1)),     # K = 2048: 4-step chunks
-    ((1, 12288, 4096, 6), (1, 1, 1, 4, 1)),     # 8-step chunks only up to 4 channels
-    ((32, 12288, 4096, 4), (2, 2, 1, 4, 1)),    # long K, wide N: MFMA, 32 rows
-    ((48, 12288, 4096, 4), (2, 3, 1, 4, 1)),
-    ((64, 12288, 4096, 4), (2, 4, 1, 0, 1)),
-    ((128, 12288, 4096, 4), (2, 4, 1, 0, 1)),   # 32 rows would need 768 tiles
-    ((512, 12288, 4096, 4), (3, 0, 0, 0, 1)),   # LDS-staged, 256 x 64 tiles
-    ((2048, 12288, 4096, 4), (3, 0, 0, 0, 1)),
-    ((2048, 12288, 4096, 6), (2, 4, 1, 0, 1)),  # the LDS kernel holds at most 4 channels
+    ((1, 2304, 768, 4), (1, 1, 1, 3, 1, 0)),       # decode: stream, 3 waves split 12 K steps
+    ((64, 2304, 768, 4), (1, 1, 1, 3, 1, 0)),      # stream up to 64 rows at short K
+    ((96, 2304, 768, 4), (1, 2, 1, 3, 1, 0)),      # stream: 432 tiles of 32 x 16
+    ((128, 768, 768, 4), (1, 2, 1, 3, 1, 0)),      # stream: 192 tiles
+    ((128, 2304, 768, 4), (5, 2, 1, 4, 1, 0)),     # 576 stream tiles: MFMA, 32 x 48 (192 tiles)
+    ((256, 1536, 768, 4), (5, 2, 1, 4, 1, 0)),     # 32 x 48 fills 256 CUs (32 x 64: 192)
+    ((256, 3072, 768, 4), (5, 4, 1, 4, 1, 0)),     # 64 x 48, 256 tiles, ties 64 x 64 on rows
+    ((256, 3072, 1024, 4), (5, 4, 1, 4, 1, 0)),
+    ((128, 2304, 768, 6), (2, 2, 1, 4, 1, 0)),     # 48-column tiles only up to 4 channels
+    ((224, 2304, 768, 4), (2, 2, 1, 4, 1, 0)),     # 252 tiles of 32 rows: one round
+    ((256, 2304, 768, 4), (2, 3, 1, 4, 1, 0)),     # headline: 216 tiles of 48 rows
+    ((320, 2304, 768, 4), (2, 3, 1, 4, 1, 0)),     # 252 tiles of 48 rows
+    ((384, 2304, 768, 4), (2, 4, 1, 0, 1, 0)),     # 64 rows (216 tiles) tie 32 rows (2 rounds)
+    ((256, 4608, 768, 4), (2, 3, 1, 4, 1, 0)),     # no height fits one round: 48 rows (2 rounds)
+    ((256, 2304, 768, 6), (2, 4, 1, 0, 1, 0)),     # no 48-row tile past 4 channels
+    ((4096, 2304, 768, 4), (2, 4, 1, 0, 1, 0)),    # C4 QKV: over 512 tiles at every height
+    ((1, 12288, 4096, 4), (4, 1, 1, 4, 1, 0)),     # C5 decode: stream with 8-step chunks
+    ((16, 12288, 4096, 4), (4, 1, 1, 4, 1, 0)),    # long K, 16 rows: stream, 8-step chunks
+    ((16, 2048, 2048, 4), (1, 1, 1, 4, 1, 0)),     # K = 2048: 4-step chunks
+    ((1, 12288, 4096, 6), (1, 1, 1, 4, 1, 0)),     # 8-step chunks only up to 4 channels
+    ((32, 12288, 4096, 4), (2, 2, 1, 4, 1, 0)),    # long K, wide N: MFMA, 32 rows
+    ((48, 12288, 4096, 4), (2, 3, 1, 4, 1, 0)),
+    ((64, 12288, 4096, 4), (2, 4, 1, 0, 1, 0)),
+    ((128, 12288, 4096, 4), (2, 4, 1, 0, 1, 0)),   # 32 rows would need 768 tiles
+    ((512, 12288, 4096, 4), (3, 0, 0, 0, 2, 1)),   # LDS-staged, 256 x 64 tiles: 384 = 256 whole + 128 split in 2
+    ((2048, 12288, 4096, 4), (3, 0, 0, 0, 1, 0)),
+    ((2048, 12288, 4096, 6), (2, 4, 1, 0, 1, 0)),  # the LDS kernel holds at most 4 channels
     # K split over workgroups: few tiles and long K
-    ((1, 768, 16384, 4), (4, 1, 1, 1, 8)),    # decode: 8 one-wave workgroups per 16 x 16 tile
-    ((1, 768, 4096, 4), (4, 1, 1, 1, 4)),     # 16 K steps per split: 4 splits
-    ((1, 768, 2048, 4), (1, 1, 1, 4, 1)),     # 2 one-wave splits lose to 4 waves in one workgroup
-    ((1, 2304, 16384, 4), (4, 1, 1, 4, 1)),   # 144 stream tiles: no split
-    ((256, 256, 8192, 4), (2, 2, 1, 4, 8)),   # 32 tiles: 8 splits (256 workgroups)
-    ((256, 768, 4096, 4), (2, 2, 1, 4, 4)),   # 96 tiles: at most 512 workgroups -> 4
-    ((512, 512, 8192, 4), (2, 2, 1, 4, 2)),   # 128 tiles, K >= 8192: 2
-    ((2048, 768, 16384, 4), (2, 4, 1, 0, 2)),
-    ((256, 256, 8192, 6), (2, 2, 1, 4, 1)),   # the exchange holds at most 4 channels
+    ((1, 768, 16384, 4), (4, 1, 1, 1, 8, 0)),    # decode: 8 one-wave workgroups per 16 x 16 tile
+    ((1, 768, 4096, 4), (4, 1, 1, 1, 4, 0)),     # 16 K steps per split: 4 splits
+    ((1, 768, 2048, 4), (1, 1, 1, 4, 1, 0)),     # 2 one-wave splits lose to 4 waves in one workgroup
+    ((1, 2304, 16384, 4), (4, 1, 1, 4, 1, 0)),   # 144 stream tiles: no split
+    ((256, 256, 8192, 4), (2, 2, 1, 4, 8, 0)),   # 32 tiles: 8 splits (256 workgroups)
+    ((256, 768, 4096, 4), (2, 2, 1, 4, 4, 0)),   # 96 tiles: at most 512 workgroups -> 4
+    ((512, 512, 8192, 4), (2, 2, 1, 4, 2, 0)),   # 128 tiles, K >= 8192: 2
+    ((2048, 768, 16384, 4), (2, 4, 1, 0, 2, 0)),
+    ((256, 256, 8192, 6), (2, 2, 1, 4, 1, 0)),   # the exchange holds at most 4 channels
+    ((640, 12288, 4096, 4), (3, 0, 0, 0, 4, 1)),    # 576 LDS tiles: the last 64 split in 4
+    ((1280, 12288, 4096, 4), (3, 0, 0, 0, 1, 0)),   # 960 tiles: 192 in the last round, not split
+    ((512, 12288, 1024, 4), (2, 4, 1, 0, 1, 0)),    # short K: LDS only for full rounds, MFMA unsplit
 ]
 
 
