@@ -59,6 +59,7 @@ sys.path.insert(0, os.path.join(ROOT, "rns-llm_amd"))
 sys.path.insert(0, ROOT)
 
 DENSE4 = (255, 253, 251, 247)
+DENSE6 = (255, 253, 251, 247, 241, 239)
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
 CALIB_BYTES = 64 << 20   # device copy used to scale the PMC byte counters
@@ -250,6 +251,58 @@ def measure_shape(backend, name, m, k, n_each, parts, steps, warmup, rotate_byte
         "ops_eff": ops, "bytes_alg": bytes_alg,
     }
     del prepared, ws
+    torch.cuda.empty_cache()
+    return row
+
+
+def measure_wide(backend, m, k, n, packed, steps, warmup, rotate_bytes, seed, device):
+    """Wide path: int16 weights and int16 activations (RNSLinear's
+    quant_bits=16) on the 6-channel dense set, the weights stored as
+    residue planes (6 bytes per value) or packed (2 bytes per value, the
+    residues formed inside the GEMM).  Same timing as measure_shape."""
+    import torch
+
+    r = len(DENSE6)
+    kp = (k + 63) // 64 * 64
+    per_weight = (2 if packed else r) * ((n + 15) // 16 * 16) * kp
+    count = max(2, math.ceil(rotate_bytes / per_weight))
+    prep = backend.prepare_weight_packed_nk if packed else backend.prepare_weight_nk
+    gen = torch.Generator(device=device).manual_seed(seed)
+    weights, w0 = [], None
+    for i in range(count):
+        w = torch.randint(-32767, 32768, (n, k), generator=gen, device=device, dtype=torch.int32).to(torch.int16)
+        weights.append(prep(w, DENSE6))
+        if i == 0:
+            w0 = w
+    a = torch.randint(-32767, 32768, (m, k), generator=gen, device=device, dtype=torch.int32).to(torch.int16)
+    ws = backend.create_workspace(device=device, channels=r, m=m, n=n)
+
+    def call(i):
+        return backend.matmul_prepared_fused(a, weights[i % count], workspace=ws)
+
+    out0 = call(0).clone()
+    exact_check(out0, a, w0, max_rows=16)
+
+    def step(i):
+        call(i)
+
+    ms, host_ms = graph_steps(step, steps, warmup)
+    if not torch.equal(call(0), out0):
+        raise SystemExit("parity failure: repeated call differs")
+    ops = 2 * r * m * k * n
+    bytes_alg = 2 * m * k + per_weight + 8 * m * n
+    t_ops, t_bytes = ops / (INT8_PEAK_TOPS * 1e12), bytes_alg / (HBM_PEAK_GBS * 1e9)
+    bound = "hbm" if t_bytes >= t_ops else "mfma"
+    row = {
+        "config": "C5 shape, int16 weights and activations, 6 channels, " + ("packed" if packed else "residue planes"),
+        "m": m, "k": k, "n": n, "channels": r, "weight_form": "packed" if packed else "planes",
+        "weight_bytes": per_weight, "weight_copies": count,
+        "us_per_call_graph": ms * 1000.0, "host_ms_per_step": host_ms,
+        "eff_tops": ops / (ms * 1e-3) / 1e12, "gbs_alg": bytes_alg / (ms * 1e-3) / 1e9,
+        "bound": bound, "roofline_frac": (t_bytes if bound == "hbm" else t_ops) / (ms * 1e-3),
+        "ops_eff": ops, "bytes_alg": bytes_alg,
+    }
+    del weights, ws
     torch.cuda.empty_cache()
     return row
 
@@ -623,6 +676,13 @@ def main():
                 f"{rows[-1]['channels']} channels, "
                 f"{rows[-1]['eff_tops']:.1f} eff TOPS, {rows[-1]['gbs_alg']:.0f} GB/s alg, "
                 f"{rows[-1]['bound']} roofline {rows[-1]['roofline_frac']:.3f}")
+        for m in (1, 16, 512):
+            for packed in (False, True):
+                rows.append(measure_wide(backend, m, 4096, 12288, packed, args.steps, args.warmup, rot, 91, device))
+                log(f"bench: wide int16 x int16, 6 channels, {rows[-1]['weight_form']} weights "
+                    f"({rows[-1]['weight_bytes'] / 1e6:.1f} MB) M={m}: {rows[-1]['us_per_call_graph']:.2f} us/step, "
+                    f"{rows[-1]['eff_tops']:.1f} eff TOPS, {rows[-1]['gbs_alg']:.0f} GB/s alg, "
+                    f"{rows[-1]['bound']} roofline {rows[-1]['roofline_frac']:.3f}")
         layer = measure_qkv_layer(backend, device)
         rows.append(layer)
         for r in layer["rows"]:

@@ -273,6 +273,50 @@ int32_t rnsmx_matmul_residues_prepared(
     const rnsmx_epilogue_t *epilogue, void *out_dev, void *stream);
 
 /*
+ * Packed weights: 2 bytes per weight value whatever the channel count, for
+ * int16 (quant_bits 12 or 16) or int8 weights.  The reference stores one
+ * byte per residue channel and names packed residues, or residues made
+ * inside the GEMM, as the way to a real memory saving (README.md:26-36,
+ * docs/RELEASE_V05.md:81-91); it has no such entry point.
+ *
+ * rnsmx_prepare_weight_packed: b_nk_dev [N][K] int8 or int16 -> packed_dev,
+ * two byte planes [2][ceil(N/16)][kp/64][1024] in the fragment-major order
+ * of rnsmx_prepare_weight: plane 0 holds hi = v >> 8 (arithmetic shift),
+ * plane 1 lo = (v & 255) - 128, so v = 256 hi + lo + 128 (zero past N and
+ * K).  No moduli: one packed weight serves any moduli set.  absmax_dev as
+ * in rnsmx_prepare_weight.
+ *
+ * rnsmx_matmul_packed_fused: rnsmx_matmul_prepared_fused against a packed
+ * weight, with the same arguments, results and errors, for 2 to 6
+ * channels.  Channel c's weight residue is never stored: with
+ * d_c = 256 mod m_c, v = d_c hi + lo + 128 (mod m_c), so the kernels run
+ * two MFMAs per channel (activation residues of d_c a against hi, of a
+ * against lo) and add 128 sum_k a_k per row.  Accumulators: 2 K 128
+ * max(floor(m/2)) + 255 < 2^31 (else RNSMX_ERANGE).  Plans: kind 1 (stream,
+ * mb 1 or 2, nb 1, ks 1-4) or 2 (MFMA, mb 2 or 4, nb 1), never split; NULL
+ * for the automatic one (rnsmx_packed_plan).  The workspace holds the
+ * encoded activations (rnsmx_packed_workspace_bytes).
+ */
+int32_t rnsmx_prepare_weight_packed(const void *b_nk_dev, int32_t dtype,
+                                    int32_t n, int32_t k, int8_t *packed_dev,
+                                    int32_t *absmax_dev, void *stream);
+
+int64_t rnsmx_packed_workspace_bytes(int64_t m, int64_t k, int64_t n,
+                                     int32_t channels);
+
+int32_t rnsmx_matmul_packed_fused(
+    const void *a_dev, int32_t a_dtype, int32_t m, int32_t k, int32_t n,
+    const int8_t *packed_dev, const rnsmx_moduli_t *mods,
+    const int16_t *lut_dev, int32_t lut_channels,
+    const rnsmx_adaptive_t *adaptive, const rnsmx_epilogue_t *epilogue,
+    const rnsmx_plan_t *plan, void *workspace_dev, int64_t workspace_bytes,
+    void *out_dev, void *stream);
+
+/* The plan rnsmx_matmul_packed_fused chooses by itself (host only). */
+int32_t rnsmx_packed_plan(int64_t m, int64_t n, int64_t k, int32_t channels,
+                          rnsmx_plan_t *out);
+
+/*
  * The plan rnsmx_matmul_prepared_fused chooses by itself for an M x N x K
  * product with `channels` moduli (kind 1-5, tile, ks, splits as in
  * rnsmx_plan_t).  raw_a != 0: int8 activations read in place, as the fused

@@ -372,3 +372,37 @@ def adaptive_matmul(a, b, moduli, *, min_channels=3, lut_channels=2):
     prefix = tuple(moduli)[:c]
     out = rns_matmul_centered(a, b, prefix, lut_channels=min(lut_channels, c))
     return out, {"channels": c, "bound": bound, "capacity": cap}
+
+
+# ---------------------------------------------------------------------------
+# Packed weights (no counterpart in the reference: its prepared weights keep
+# one byte per channel, ``README.md:26-36``).  Pinned in tests/test_oracle.py
+# by the round trip over every int16 value, the congruence for every
+# candidate modulus, and packed_channel_residues against the residues of the
+# exact product.
+# ---------------------------------------------------------------------------
+def pack16_split(values) -> tuple[np.ndarray, np.ndarray]:
+    """(hi, lo) with hi = v >> 8 and lo = (v & 255) - 128, both in int8
+    range for int16 v, so v = 256 hi + lo + 128."""
+    v = np.asarray(values, dtype=np.int64)
+    if v.size and (v.min() < -(1 << 15) or v.max() >= (1 << 15)):
+        raise ValueError("packed weights hold int16 values")
+    return v >> 8, (v & 255) - 128
+
+
+def packed_channel_residues(a, b, moduli) -> np.ndarray:
+    """Canonical residues [R, M, N] of A @ B computed the way the packed
+    kernels do, channel by channel: with d = 256 mod m, a_c the centered
+    residues of A and a'_c those of d * a_c, the sum
+    a'_c @ hi + a_c @ lo + 128 * rowsum(a_c), reduced mod m."""
+    mods = validate_moduli(moduli)
+    hi, lo = pack16_split(b)
+    a_c = encode_centered(a, mods).astype(np.int64)
+    out = []
+    for c, m in enumerate(mods):
+        d = 256 % m
+        r = np.mod(d * a_c[c], m)
+        a2 = r - m * (r > m // 2)
+        s = a2 @ hi + a_c[c] @ lo + 128 * a_c[c].sum(axis=1, keepdims=True)
+        out.append(np.mod(s, m))
+    return np.stack(out)

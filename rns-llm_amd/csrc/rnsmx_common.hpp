@@ -43,4 +43,11 @@ inline bool raw_accumulator_fits(const rnsmx_moduli_t &mods, int64_t k) {
   return k * 128 * static_cast<int64_t>(max_half(mods)) <= 0x7FFFFFFFLL;
 }
 
+// Packed weights: two products of centered residues (|.| <= max_half) by
+// weight bytes (|.| <= 128) per K index, plus a per-row term below 256:
+// 2 * K * 128 * max_half + 255 <= 2^31 - 1.
+inline bool packed_accumulator_fits(const rnsmx_moduli_t &mods, int64_t k) {
+  return k * 256 * static_cast<int64_t>(max_half(mods)) + 255 <= 0x7FFFFFFFLL;
+}
+
 }  // namespace rnsmx

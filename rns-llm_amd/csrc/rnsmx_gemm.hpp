@@ -23,6 +23,16 @@
 // layout, so every B load is one contiguous 1 KB (b_ld = bytes per column
 // block, b_cs = bytes per channel; columns past N and K past K are zero).
 //
+// Packed weights (the *_packed_kernel instances): B is two byte planes in
+// the same fragment order whatever the channel count, hi = v >> 8 and
+// lo = (v & 255) - 128 of each int16 weight v, so v = 256 hi + lo + 128 and,
+// with d_c = 256 mod m_c, v = d_c hi + lo + 128 (mod m_c).  Channel c's sum
+// is then sum_k a'_k hi_k + sum_k a_k lo_k + 128 sum_k a_k (mod m_c), where
+// a_k is the centered residue of the activation and a'_k that of d_c a_k:
+// two MFMAs per channel and K step, and a per-row term.  A holds 2R planes
+// [a (R planes) | a' (R planes)] followed by int32 [R][packed_corr_ld(M)]
+// with (128 sum_k a_k) mod m_c per row (rnsmx_kernels.hip encodes them).
+//
 // MFMA v_mfma_i32_16x16x64_i8: lane l feeds A row (l & 15) and B column
 // (l & 15), both with K bytes [16 * (l >> 4), +16) of a 64-byte step, and
 // receives D rows 4 * (l >> 4) + t (t = 0..3) of column (l & 15).
@@ -143,10 +153,12 @@ struct GemmGrid {
 // library compiles in parallel:
 //   P0 stream kernels, P1 MFMA kernels with raw int8 A and 64-column tiles,
 //   P2 MFMA kernels with raw int8 A and 128-column tiles, P3 MFMA kernels
-//   with residue-plane A, P4 the LDS-staged kernel.
+//   with residue-plane A, P4 the LDS-staged kernel, P5 the stream and MFMA
+//   kernels for packed weights (channel capacities 4 and 6).
 // launch_gemm_rR_pP returns false when the part has no kernel for the choice.
-constexpr int kGemmParts = 5;
-inline int gemm_part_of(const GemmChoice &c, bool araw) {
+constexpr int kGemmParts = 6;
+inline int gemm_part_of(const GemmChoice &c, bool araw, bool packed = false) {
+  if (packed) return 5;
   if (c.kind == kStream || c.kind == kStreamWide) return 0;
   if (c.kind == kLds) return 4;
   if (!araw) return 3;
@@ -157,7 +169,7 @@ inline int gemm_part_of(const GemmChoice &c, bool araw) {
   bool RNSMX_GEMM_PART_NAME(R, P)(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st);
 #define RNSMX_GEMM_PARTS_DECL(R)                                                             \
   RNSMX_GEMM_PART_DECL(R, 0) RNSMX_GEMM_PART_DECL(R, 1) RNSMX_GEMM_PART_DECL(R, 2) \
-  RNSMX_GEMM_PART_DECL(R, 3) RNSMX_GEMM_PART_DECL(R, 4)
+  RNSMX_GEMM_PART_DECL(R, 3) RNSMX_GEMM_PART_DECL(R, 4) RNSMX_GEMM_PART_DECL(R, 5)
 RNSMX_GEMM_PARTS_DECL(3)
 RNSMX_GEMM_PARTS_DECL(4)
 RNSMX_GEMM_PARTS_DECL(6)
@@ -675,6 +687,40 @@ __device__ __forceinline__ i32x4 select16(bool keep, i32x4 v) {
   return keep ? v : zero;
 }
 
+// Packed weights: the row stride of the per-row terms after the 2R
+// activation planes, past every row a tile of up to 64 rows can address.
+__host__ __device__ constexpr int64_t packed_corr_ld(int64_t m) { return (m + 63) / 64 * 64 + 64; }
+
+// Byte offset of activation plane p of a packed-weight product: planes
+// [0, RCAP) are the residues a of channel p, [RCAP, 2 RCAP) the residues a'
+// of channel p - RCAP, which start after all `channels` a planes.  Channels
+// at or past the active count read channel 0 (as plane_off).
+template <int RCAP>
+__device__ __forceinline__ int64_t packed_plane_off(int p, int c_act, int channels, int64_t stride) {
+  const int c = p < RCAP ? p : p - RCAP;
+  return (p < RCAP ? 0 : channels * stride) + plane_off(c, c_act, stride);
+}
+
+// Adds each row's term (128 sum_k a_k) mod m_c to the channel sums of a
+// (16 MI) x (16 NJ) block whose top row is r0 (packed weights; added once
+// per tile, before any exchange).  The lane's rows 4 (lane >> 4) .. +3 of
+// each 16-row block are one aligned 16-byte load.
+template <int RCAP, int MI, int NJ>
+__device__ __forceinline__ void add_packed_rows(KArgs<RCAP> &g, i32x4 (&acc)[RCAP][MI][NJ], int r0, int c_act) {
+  const int lane = threadIdx.x & 63;
+  const int64_t ld = packed_corr_ld(g.m);
+  const int32_t *terms = reinterpret_cast<const int32_t *>(g.a + 2 * g.mods.channels * g.a_cs);
+  static_for<RCAP>([&](auto C) {
+    constexpr int c = decltype(C)::value;
+    if (c >= c_act) return;
+    static_for<MI>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      const i32x4 t = *reinterpret_cast<const i32x4 *>(terms + c * ld + r0 + 16 * i + 4 * (lane >> 4));
+      static_for<NJ>([&](auto J) { acc[c][i][decltype(J)::value] += t; });
+    });
+  });
+}
+
 // Bijection of [0, total) that gives each XCD one contiguous run of unit
 // numbers.  Workgroups are handed to the 8 XCDs round-robin (workgroup b
 // runs on XCD b % 8), and each XCD has its own L2; units are numbered
@@ -893,19 +939,23 @@ __device__ __forceinline__ bool split_exchange(KArgs<RCAP> &g, const Epi<RCAP> &
 // registers (two waves per SIMD), at most ucap (4; 8 for the wide form,
 // which long-K decode takes: C5 M=1 39.5 us against 42.5 with 4, while at
 // K = 768 the larger chunks cost 7-15 %).
-constexpr int stream_u_of(int rcap, bool araw, int mb, int nb, int ucap = 4) {
-  const int frags = (araw ? 1 : rcap) * mb + rcap * nb;  // 16-byte loads per K step
+constexpr int stream_u_of(int rcap, bool araw, int mb, int nb, int ucap = 4, bool pk = false) {
+  // 16-byte loads per K step (packed weights: 2R activation planes, 2 weight planes)
+  const int frags = (pk ? 2 * rcap : araw ? 1 : rcap) * mb + (pk ? 2 : rcap) * nb;
   const int u = (240 - 4 * rcap * mb * nb) / (4 * frags);
   return u < 1 ? 1 : (u > ucap ? ucap : u);
 }
 
-template <int RCAP, int MB, int NB, bool ARAW, int UCAP>
-__global__ __launch_bounds__(256) void stream_kernel(const GemmArgsK<RCAP> args) {
+// PK: packed weights (two byte planes; activations as 2R residue planes).
+template <int RCAP, int MB, int NB, bool ARAW, int UCAP, bool PK>
+__device__ __forceinline__ void stream_body() {
   KArgs<RCAP> &g = kernel_args<GemmArgsK<RCAP>>();
   prefetch_kernel_args<kGemmHotArgBytes>();
+  static_assert(!(PK && ARAW), "packed weights take residue-plane activations");
   constexpr int BM = 16 * MB, BN = 16 * NB, TILE = BM * BN;
-  constexpr int AP = ARAW ? 1 : RCAP;
-  constexpr int U = stream_u_of(RCAP, ARAW, MB, NB, UCAP);
+  constexpr int AP = PK ? 2 * RCAP : ARAW ? 1 : RCAP;  // activation planes per K step
+  constexpr int BP = PK ? 2 : RCAP;                    // weight planes per K step
+  constexpr int U = stream_u_of(RCAP, ARAW, MB, NB, UCAP, PK);
   extern __shared__ __attribute__((aligned(16))) int32_t sacc[];  // [RCAP][TILE] when KS > 1
   __shared__ int64_t red[4];
   __shared__ int bcast;
@@ -933,9 +983,15 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgsK<RCAP> args)
     const int jb = min(nt * NB + j, nblk - 1);
     bp[j] = g.b + static_cast<int64_t>(jb) * g.b_ld + kr.ks0 * 1024 + lane * 16;
   });
-  int64_t boff[RCAP], aoff[AP];
-  static_for<RCAP>([&](auto C) { boff[decltype(C)::value] = plane_off(decltype(C)::value, c_act, g.b_cs); });
-  static_for<AP>([&](auto PP) { aoff[decltype(PP)::value] = plane_off(decltype(PP)::value, c_act, g.a_cs); });
+  int64_t boff[BP], aoff[AP];
+  static_for<BP>([&](auto C) {
+    constexpr int c = decltype(C)::value;
+    boff[c] = PK ? c * g.b_cs : plane_off(c, c_act, g.b_cs);
+  });
+  static_for<AP>([&](auto PP) {
+    constexpr int p = decltype(PP)::value;
+    aoff[p] = PK ? packed_plane_off<RCAP>(p, c_act, g.mods.channels, g.a_cs) : plane_off(p, c_act, g.a_cs);
+  });
 
   const i32x4 zero = {0, 0, 0, 0};
   i32x4 acc[RCAP][MB][NB];
@@ -943,7 +999,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgsK<RCAP> args)
     static_for<MB>([&](auto I) { static_for<NB>([&](auto J) { acc[C][I][J] = acc_zero(); }); });
   });
 
-  i32x4 fa[U][AP][MB], fb[U][RCAP][NB];
+  i32x4 fa[U][AP][MB], fb[U][BP][NB];
   auto load_chunk = [&](int q) {
     static_for<U>([&](auto UU) {
       constexpr int u = decltype(UU)::value;
@@ -958,7 +1014,7 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgsK<RCAP> args)
           fa[u][p][i] = select16(av, load16(ap[i] + aoff[p] + kac));
         });
       });
-      static_for<RCAP>([&](auto C) {
+      static_for<BP>([&](auto C) {
         constexpr int c = decltype(C)::value;
         static_for<NB>([&](auto J) {
           constexpr int j = decltype(J)::value;
@@ -978,8 +1034,16 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgsK<RCAP> args)
           constexpr int i = decltype(I)::value;
           static_for<NB>([&](auto J) {
             constexpr int j = decltype(J)::value;
-            acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][ARAW ? 0 : c][i], fb[u][c][j],
-                                                                 acc[c][i][j], 0, 0, 0);
+            if constexpr (PK) {
+              // a' x hi + a x lo: the channel's residue of the weight, formed by the MFMAs
+              acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][RCAP + c][i], fb[u][0][j],
+                                                                   acc[c][i][j], 0, 0, 0);
+              acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][c][i], fb[u][1][j],
+                                                                   acc[c][i][j], 0, 0, 0);
+            } else {
+              acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][ARAW ? 0 : c][i], fb[u][c][j],
+                                                                   acc[c][i][j], 0, 0, 0);
+            }
           });
         });
       });
@@ -1009,6 +1073,11 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgsK<RCAP> args)
   for (int q = wave * U + ks_n * U; q < nk; q += ks_n * U) {
     load_chunk(q);
     mfma_chunk();
+  }
+  // packed weights: the per-row term, once per tile (wave 0 of the whole K
+  // or of its first split)
+  if constexpr (PK) {
+    if (wave == 0 && split <= 0) add_packed_rows<RCAP, MB, NB>(g, acc, m0, c_act);
   }
 
   if (ks_n == 1) {
@@ -1088,6 +1157,16 @@ __global__ __launch_bounds__(256) void stream_kernel(const GemmArgsK<RCAP> args)
   });
 }
 
+template <int RCAP, int MB, int NB, bool ARAW, int UCAP>
+__global__ __launch_bounds__(256) void stream_kernel(const GemmArgsK<RCAP> args) {
+  stream_body<RCAP, MB, NB, ARAW, UCAP, false>();
+}
+
+template <int RCAP, int MB, int NB, int UCAP>
+__global__ __launch_bounds__(256) void stream_packed_kernel(const GemmArgsK<RCAP> args) {
+  stream_body<RCAP, MB, NB, false, UCAP, true>();
+}
+
 // ---------------------------------------------------------------------------
 // MFMA GEMM (M > 128 where the LDS kernel does not apply: C2 M=256, C4;
 // also smaller batches of wide or long-K shapes, e.g. C5 M=32-128).  A
@@ -1111,18 +1190,16 @@ __device__ __forceinline__ int a_chunk_off(int row, int part) {
   return row * kLdsRow + ((part ^ ((row >> 1) & 3)) << 4);
 }
 
-constexpr int mfma_ac_of(int rcap, int mb, bool araw) {
-  const int chunks = (araw ? 1 : rcap) * 16 * mb * 4;
-  return (chunks + 255) / 256;
-}
-
-// NWV: waves (column groups of 16*NB) per workgroup, 4 or 3.
-template <int RCAP, int MB, int NB, int P, bool ARAW, int NWV = 4>
-__global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgsK<RCAP> args) {
+// NWV: waves (column groups of 16*NB) per workgroup, 4 or 3.  PK: packed
+// weights (two byte planes; activations as 2R residue planes).
+template <int RCAP, int MB, int NB, int P, bool ARAW, int NWV, bool PK>
+__device__ __forceinline__ void mfma_body() {
   KArgs<RCAP> &g = kernel_args<GemmArgsK<RCAP>>();
   prefetch_kernel_args<kGemmArgBytes<RCAP>>();
+  static_assert(!(PK && ARAW), "packed weights take residue-plane activations");
   constexpr int BM = 16 * MB, BNW = 16 * NB;
-  constexpr int AP = ARAW ? 1 : RCAP;
+  constexpr int AP = PK ? 2 * RCAP : ARAW ? 1 : RCAP;  // activation planes staged per K step
+  constexpr int BP = PK ? 2 : RCAP;                    // weight planes per K step
   constexpr int PLANE = BM * kLdsRow;
   constexpr int ACH = AP * BM * 4;  // 16-byte A chunks per K step
   constexpr int NT = 64 * NWV;
@@ -1152,10 +1229,11 @@ __global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgsK<RCAP> ar
     const int qq = inside ? q : 0;
     const int p = qq / (BM * 4), w = qq % (BM * 4), row = w >> 2, part = w & 3;
     const int grow = min(m0 + row, g.m - 1);
-    asrc[i] = g.a + plane_off(p, c_act, g.a_cs) + static_cast<int64_t>(grow) * g.a_ld + kr.ks0 * 64;
+    const int64_t poff = PK ? packed_plane_off<RCAP>(p, c_act, g.mods.channels, g.a_cs) : plane_off(p, c_act, g.a_cs);
+    asrc[i] = g.a + poff + static_cast<int64_t>(grow) * g.a_ld + kr.ks0 * 64;
     alds[i] = inside ? p * PLANE + a_chunk_off(row, part) : AP * PLANE;
     apart[i] = part * 16;
-    aon[i] = inside && (ARAW || p < c_act);
+    aon[i] = inside && (ARAW || (PK ? p % RCAP : p) < c_act);
   });
   const int8_t *bp[NB];
   const int nblk = (g.n + 15) >> 4;
@@ -1164,12 +1242,15 @@ __global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgsK<RCAP> ar
     const int jb = min((n0 >> 4) + j, nblk - 1);
     bp[j] = g.b + static_cast<int64_t>(jb) * g.b_ld + kr.ks0 * 1024 + lane * 16;
   });
-  int64_t boff[RCAP];
-  static_for<RCAP>([&](auto C) { boff[decltype(C)::value] = plane_off(decltype(C)::value, c_act, g.b_cs); });
+  int64_t boff[BP];
+  static_for<BP>([&](auto C) {
+    constexpr int c = decltype(C)::value;
+    boff[c] = PK ? c * g.b_cs : plane_off(c, c_act, g.b_cs);
+  });
 
   const i32x4 zero = {0, 0, 0, 0};
   i32x4 ra[P][AC];
-  i32x4 fb[P][RCAP][NB];
+  i32x4 fb[P][BP][NB];
   // loads of K step ks (clamped to the last one; A of steps past K is zero)
   auto gload = [&](auto SLOT, int ks) {
     constexpr int s = decltype(SLOT)::value;
@@ -1180,7 +1261,7 @@ __global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgsK<RCAP> ar
       const bool keep = aon[i] && ks < nk && ka < a_k;
       ra[s][i] = select16(keep, load16(asrc[i] + min(ka, a_k - 16)));
     });
-    static_for<RCAP>([&](auto C) {
+    static_for<BP>([&](auto C) {
       constexpr int c = decltype(C)::value;
       static_for<NB>([&](auto J) {
         constexpr int j = decltype(J)::value;
@@ -1226,7 +1307,7 @@ __global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgsK<RCAP> ar
       constexpr int s = decltype(SS)::value;
       const int ks = ks0 + s;
       const int buf = ks & 1;
-      i32x4 fa[MB];
+      i32x4 fa[MB], fa2[MB];
       // skip inactive channels and the steps past K (a straight-line form
       // measured 13 % slower here: C2 M=256 12.2 -> 13.8 us)
       static_for<RCAP>([&](auto C) {
@@ -1236,13 +1317,21 @@ __global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgsK<RCAP> ar
           static_for<MB>([&](auto I) {
             constexpr int i = decltype(I)::value;
             fa[i] = *reinterpret_cast<const i32x4 *>(&As[buf][(ARAW ? 0 : c) * PLANE + a_frag + i * 16 * kLdsRow]);
+            if constexpr (PK)
+              fa2[i] = *reinterpret_cast<const i32x4 *>(&As[buf][(RCAP + c) * PLANE + a_frag + i * 16 * kLdsRow]);
           });
         }
         static_for<MB>([&](auto I) {
           constexpr int i = decltype(I)::value;
           static_for<NB>([&](auto J) {
             constexpr int j = decltype(J)::value;
-            acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[s][c][j], acc[c][i][j], 0, 0, 0);
+            if constexpr (PK) {
+              // a' x hi + a x lo: the channel's residue of the weight, formed by the MFMAs
+              acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa2[i], fb[s][0][j], acc[c][i][j], 0, 0, 0);
+              acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[s][1][j], acc[c][i][j], 0, 0, 0);
+            } else {
+              acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[s][c][j], acc[c][i][j], 0, 0, 0);
+            }
           });
         });
       });
@@ -1256,12 +1345,26 @@ __global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgsK<RCAP> ar
   for (int ks0 = 0; ks0 < steps - P; ks0 += P) trip(ks0, std::true_type{});
   trip(steps - P, std::false_type{});
 
+  // packed weights: the per-row term, once per tile (the whole K or its first split)
+  if constexpr (PK) {
+    if (split <= 0) add_packed_rows<RCAP, MB, NB>(g, acc, m0, c_act);
+  }
   if constexpr (mfma_splits(RCAP, MB, NB)) {
     if (split >= 0 &&
         !split_exchange<RCAP, MB, NB>(g, e, acc, static_cast<int64_t>(wu.split_tile) * NWV + wave, split))
       return;
   }
   register_epilogue<RCAP, MB, NB>(g, e, c_act, acc, m0, n0, m_lim, n_lim, cs);
+}
+
+template <int RCAP, int MB, int NB, int P, bool ARAW, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV) void mfma_kernel(const GemmArgsK<RCAP> args) {
+  mfma_body<RCAP, MB, NB, P, ARAW, NWV, false>();
+}
+
+template <int RCAP, int MB, int NB, int P>
+__global__ __launch_bounds__(256) void mfma_packed_kernel(const GemmArgsK<RCAP> args) {
+  mfma_body<RCAP, MB, NB, P, false, 4, true>();
 }
 
 // ---------------------------------------------------------------------------
@@ -1644,22 +1747,67 @@ bool launch_lds(const GemmArgs &host, bool araw, hipStream_t st) {
   }
 }
 
-// Body of one part launcher (rnsmx_gemm_part.hip).
+// Packed-weight kernels: stream tiles of 16 or 32 rows, MFMA tiles of 32 or
+// 64 rows x 64 columns (ring depth 3 or 2: the 2R activation planes double
+// the register ring of A chunks), up to 6 channels.  Not split over
+// workgroups.
+template <int RCAP>
+bool launch_packed(GemmArgsK<RCAP> g, const GemmChoice &c, hipStream_t st) {
+  if constexpr (RCAP != 4 && RCAP != 6) {
+    return false;
+  } else {
+    if (c.splits > 1) return false;
+    if (c.kind == kStream) {
+#define RNSMX_STREAM_PK(MB_)                                                                           \
+  if (c.mb == MB_ && c.nb == 1) {                                                                     \
+    g.tiles_m = (g.m + 16 * MB_ - 1) / (16 * MB_);                                                    \
+    g.tiles_n = (g.n + 15) / 16;                                                                      \
+    const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));                                   \
+    const size_t lds = c.ks > 1 ? static_cast<size_t>(RCAP) * 256 * MB_ * 4 : 0;                      \
+    g.threads = 64 * c.ks;                                                                            \
+    hipLaunchKernelGGL((stream_packed_kernel<RCAP, MB_, 1, 4>), grid, dim3(64 * c.ks), lds, st, g);   \
+    return true;                                                                                      \
+  }
+      RNSMX_STREAM_PK(1)
+      RNSMX_STREAM_PK(2)
+#undef RNSMX_STREAM_PK
+      return false;
+    }
+    if (c.kind == kMfma && c.nb == 1 && (c.mb == 2 || c.mb == 4)) {
+      g.tiles_m = (g.m + 16 * c.mb - 1) / (16 * c.mb);
+      g.tiles_n = (g.n + 63) / 64;
+      const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));
+      if (c.mb == 2)
+        hipLaunchKernelGGL((mfma_packed_kernel<RCAP, 2, 1, 3>), grid, dim3(256), 0, st, g);
+      else
+        hipLaunchKernelGGL((mfma_packed_kernel<RCAP, 4, 1, 2>), grid, dim3(256), 0, st, g);
+      return true;
+    }
+    return false;
+  }
+}
+
+// Body of one part launcher (rnsmx_gemm_part.hip).  PART 5 is chosen only
+// for packed weights (gemm_part_of), whatever the activation form.
 template <int RCAP, int PART>
 bool launch_gemm_part(const GemmArgs &g, bool araw, const GemmChoice &c, hipStream_t st) {
-  if (gemm_part_of(c, araw) != PART) return false;
-  if constexpr (PART == 4) {
-    return launch_lds<RCAP>(g, araw, st);
-  } else if constexpr (PART == 0) {
-    const int ucap = c.kind == kStreamWide ? 8 : 4;
-    return araw ? launch_stream<RCAP, true>(compact_args<RCAP>(g), c.mb, c.nb, c.ks, ucap, st)
-                : launch_stream<RCAP, false>(compact_args<RCAP>(g), c.mb, c.nb, c.ks, ucap, st);
+  if constexpr (PART == 5) {
+    return launch_packed<RCAP>(compact_args<RCAP>(g), c, st);
+  } else if constexpr (PART == 4) {
+    return gemm_part_of(c, araw) == PART && launch_lds<RCAP>(g, araw, st);
   } else {
-    const int nwv = c.kind == kMfma3 ? 3 : 4;
-    if constexpr (PART == 1 || PART == 2)
-      return launch_mfma<RCAP, true, PART>(compact_args<RCAP>(g), c.mb, c.nb, c.ks, nwv, st);
-    else
-      return launch_mfma<RCAP, false, 0>(compact_args<RCAP>(g), c.mb, c.nb, c.ks, nwv, st);
+    if (gemm_part_of(c, araw) != PART) return false;
+    if constexpr (PART == 0) {
+      const int ucap = c.kind == kStreamWide ? 8 : 4;
+      return araw ? launch_stream<RCAP, true>(compact_args<RCAP>(g), c.mb, c.nb, c.ks, ucap, st)
+                  : launch_stream<RCAP, false>(compact_args<RCAP>(g), c.mb, c.nb, c.ks, ucap, st);
+    } else {
+      const int nwv = c.kind == kMfma3 ? 3 : 4;
+      if constexpr (PART == 1 || PART == 2)
+        return launch_mfma<RCAP, true, PART>(compact_args<RCAP>(g), c.mb, c.nb, c.ks, nwv, st);
+      else
+        return launch_mfma<RCAP, false, 0>(compact_args<RCAP>(g), c.mb, c.nb, c.ks, nwv, st);
+    }
   }
 }
 

@@ -4,7 +4,7 @@
 #include "rnsmx_gemm.hpp"
 
 #if !defined(RNSMX_RCAP) || !defined(RNSMX_PART)
-#error "build with -DRNSMX_RCAP=<3|4|6|10> -DRNSMX_PART=<0..3>"
+#error "build with -DRNSMX_RCAP=<3|4|6|10> -DRNSMX_PART=<0..5>"
 #endif
 
 #define RNSMX_PASTE_PART(R, P) RNSMX_GEMM_PART_NAME(R, P)

@@ -40,7 +40,7 @@ extern "C" {
 
 const char *rnsmx_last_error(void) { return rnsmx::g_error; }
 
-int32_t rnsmx_abi_version(void) { return 4; }
+int32_t rnsmx_abi_version(void) { return 5; }
 
 int32_t rnsmx_moduli_init(const int32_t *moduli, int32_t channels,
                           rnsmx_moduli_t *out) {

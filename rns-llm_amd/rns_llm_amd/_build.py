@@ -18,7 +18,7 @@ INCLUDE = os.path.join(REPO, "include")
 OBJDIR = os.path.join(ROOT, "_build")
 OUT = os.path.join(PKG, "librnsmx.so")
 GEMM_CAPACITIES = (3, 4, 6, 10)
-GEMM_PARTS = 5
+GEMM_PARTS = 6
 # (source, object name, extra flags)
 UNITS = [("rnsmx_kernels.hip", "rnsmx_kernels", []), ("rnsmx_host.cpp", "rnsmx_host", [])] + [
     ("rnsmx_gemm_part.hip", f"rnsmx_gemm_r{r}_p{p}", [f"-DRNSMX_RCAP={r}", f"-DRNSMX_PART={p}"])

@@ -38,6 +38,10 @@ EXPORTED_SYMBOLS = (
     "rnsmx_matmul_prepared_fused_noalloc",
     "rnsmx_matmul_residues_prepared",
     "rnsmx_gemm_plan",
+    "rnsmx_prepare_weight_packed",
+    "rnsmx_packed_workspace_bytes",
+    "rnsmx_matmul_packed_fused",
+    "rnsmx_packed_plan",
     "rnsmx_quantize_symmetric",
     "rnsmx_linear_workspace_bytes",
     "rnsmx_linear_forward",
@@ -141,6 +145,13 @@ _SIGNATURES = {
         _I32, [_P, _I64, _I32, _I32, _I32, _P, ctypes.POINTER(Moduli), _P, _I32,
                ctypes.POINTER(Epilogue), _P, _P]),
     "rnsmx_gemm_plan": (_I32, [_I64, _I64, _I64, _I32, _I32, ctypes.POINTER(Plan)]),
+    "rnsmx_prepare_weight_packed": (_I32, [_P, _I32, _I32, _I32, _P, _P, _P]),
+    "rnsmx_packed_workspace_bytes": (_I64, [_I64, _I64, _I64, _I32]),
+    "rnsmx_matmul_packed_fused": (
+        _I32, [_P, _I32, _I32, _I32, _I32, _P, ctypes.POINTER(Moduli), _P, _I32,
+               ctypes.POINTER(Adaptive), ctypes.POINTER(Epilogue), ctypes.POINTER(Plan),
+               _P, _I64, _P, _P]),
+    "rnsmx_packed_plan": (_I32, [_I64, _I64, _I64, _I32, ctypes.POINTER(Plan)]),
     "rnsmx_quantize_symmetric": (_I32, [_P, _I32, _I64, _I32, _P, _P, _P, _P]),
     "rnsmx_linear_workspace_bytes": (_I64, [_I64, _I64, _I64, _I32, _I32]),
     "rnsmx_linear_forward": (
@@ -149,7 +160,7 @@ _SIGNATURES = {
     "rnsmx_decode_garner": (_I32, [_P, _I64, ctypes.POINTER(Moduli), _P, _P]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class NativeError(RuntimeError):

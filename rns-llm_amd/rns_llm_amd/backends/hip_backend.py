@@ -58,14 +58,18 @@ class _DeviceConstants:
 
 @dataclass(frozen=True)
 class PreparedRNSWeight:
-    """Weight encoded once into centered residue planes.
+    """Weight prepared once for the fused GEMM.
 
     ``packed`` is the storage the kernels read, fragment-major
-    ``[R, ceil(N/16), kp/64, 1024]``: the 1 KB fragment of column block ``jb``
+    ``[P, ceil(N/16), kp/64, 1024]``: the 1 KB fragment of column block ``jb``
     and K step ``ks`` holds, at byte ``16*l``, column ``16*jb + l % 16`` and K
-    bytes ``64*ks + 16*(l // 16)`` .. ``+16`` (zero past N and K).
-    ``residues`` is the reference-shaped ``[R, K, N]`` tensor, unpacked from
-    it on first access.
+    bytes ``64*ks + 16*(l // 16)`` .. ``+16`` (zero past N and K).  With
+    ``form == "planes"`` the P = R planes are the centered residues of every
+    channel; with ``form == "packed"`` (int8/int16 weights, 2 bytes per value
+    whatever R) the two planes are ``hi = v >> 8`` and ``lo = (v & 255) -
+    128`` and the kernels form each channel's residue from them.
+    ``residues`` is the reference-shaped ``[R, K, N]`` tensor, unpacked on
+    first access.
     """
 
     moduli: tuple[int, ...]
@@ -74,16 +78,37 @@ class PreparedRNSWeight:
     kernel: str
     packed: torch.Tensor
     absmax: torch.Tensor | None = None  # int32 [1], max |B| on the device
+    form: str = "planes"
+
+    def _unpack(self, planes: torch.Tensor) -> torch.Tensor:
+        p, n16, nk, _ = planes.shape
+        grid = planes.view(p, n16, nk, 4, 16, 16).permute(0, 2, 3, 5, 1, 4)
+        return grid.reshape(p, nk * 64, n16 * 16)[:, :self.k, :self.n]
+
+    @functools.cached_property
+    def values(self) -> torch.Tensor:
+        """The weight as int32 [K, N] (packed form only)."""
+        if self.form != "packed":
+            raise ValueError("values are kept only by packed weights")
+        hi, lo = self._unpack(self.packed).to(torch.int32)
+        return hi * 256 + lo + 128
 
     @functools.cached_property
     def residues(self) -> torch.Tensor:
-        r, n16, nk, _ = self.packed.shape
-        planes = self.packed.view(r, n16, nk, 4, 16, 16).permute(0, 2, 3, 5, 1, 4)
-        return planes.reshape(r, nk * 64, n16 * 16)[:, :self.k, :self.n]
+        if self.form == "packed":
+            mods = torch.tensor(self.moduli, dtype=torch.int32, device=self.packed.device).view(-1, 1, 1)
+            r = torch.remainder(self.values.unsqueeze(0), mods)
+            return torch.where(r > mods // 2, r - mods, r).to(torch.int8)
+        return self._unpack(self.packed)
 
     @property
     def kp(self) -> int:
         return int(self.packed.shape[2]) * _native.K_ALIGN
+
+    @property
+    def nbytes(self) -> int:
+        """Bytes of weight storage the kernels read."""
+        return int(self.packed.numel())
 
 
 @dataclass
@@ -422,7 +447,10 @@ class HipRNSBackend:
         """A ``LinearCall`` for ``RNSLinear.forward`` on this prepared weight
         (float32 ``w_scale`` [N] and ``bias`` [N] or None), or None when the
         one-call path cannot serve it: an adaptive weight whose device-side
-        selection is not proven safe takes the synchronous selection."""
+        selection is not proven safe takes the synchronous selection, and a
+        packed weight takes the quantize + packed GEMM calls."""
+        if prepared.form != "planes":
+            return None
         if adaptive is not None and not adaptive.device_selection_is_safe(
                 torch.int8 if quant_bits == 8 else torch.int16):
             return None
@@ -474,6 +502,16 @@ class HipRNSBackend:
         if nbytes is None:
             nbytes = int(self._lib.rnsmx_prepared_workspace_bytes(
                 m, k, n, channels, None if plan is None else ctypes.byref(plan)))
+            if nbytes < 0:
+                raise ValueError("bad workspace shape")
+            self._ws_bytes[key] = nbytes
+        return nbytes
+
+    def _packed_workspace_bytes(self, m: int, k: int, n: int, channels: int) -> int:
+        key = ("packed", m, k, n, channels)
+        nbytes = self._ws_bytes.get(key)
+        if nbytes is None:
+            nbytes = int(self._lib.rnsmx_packed_workspace_bytes(m, k, n, channels))
             if nbytes < 0:
                 raise ValueError("bad workspace shape")
             self._ws_bytes[key] = nbytes
@@ -620,6 +658,39 @@ class HipRNSBackend:
         return PreparedRNSWeight(moduli=mods, k=k, n=n, kernel=kernel, packed=packed,
                                  absmax=absmax)
 
+    def _prepare_packed_nk(self, b_nk: torch.Tensor, mods: tuple[int, ...], k: int,
+                           n: int) -> PreparedRNSWeight:
+        if b_nk.dtype not in (torch.int8, torch.int16):
+            raise ValueError("packed weights take int8/int16 values")
+        if not 2 <= len(mods) <= 6:
+            raise ValueError("packed weights take 2..6 channels")
+        kp = (k + _native.K_ALIGN - 1) // _native.K_ALIGN * _native.K_ALIGN
+        packed = torch.empty((2, (n + 15) // 16, kp // _native.K_ALIGN, 1024), dtype=torch.int8,
+                             device=b_nk.device)
+        absmax = torch.zeros((1,), dtype=torch.int32, device=b_nk.device)
+        self._stats["pack_weight_calls"] += 1
+        _native.check(self._lib.rnsmx_prepare_weight_packed(
+            _aligned(b_nk).data_ptr(), _native.dtype_code(b_nk.dtype), n, k, packed.data_ptr(),
+            absmax.data_ptr(), _stream_handle(b_nk.device)))
+        return PreparedRNSWeight(moduli=mods, k=k, n=n, kernel=KERNEL_NAME, packed=packed,
+                                 absmax=absmax, form="packed")
+
+    def prepare_weight_packed(self, b: torch.Tensor, moduli: Iterable[int]) -> PreparedRNSWeight:
+        """B [K, N] int8/int16 -> packed weight, 2 bytes per value for any
+        channel count (2..6 channels).  No counterpart in the reference,
+        whose prepared storage is one byte per channel (``README.md:26-36``
+        names packed residues as the route to a memory saving)."""
+        self._validate_matrix(b, "b", 2)
+        mods = validate_moduli(moduli)
+        return self._prepare_packed_nk(b.t().contiguous(), mods, int(b.shape[0]), int(b.shape[1]))
+
+    def prepare_weight_packed_nk(self, w: torch.Tensor, moduli: Iterable[int]) -> PreparedRNSWeight:
+        """``prepare_weight_packed(w.T)`` for a quantized nn.Linear weight
+        W [N, K], without the transpose."""
+        self._validate_matrix(w, "w", 2)
+        mods = validate_moduli(moduli)
+        return self._prepare_packed_nk(w, mods, int(w.shape[1]), int(w.shape[0]))
+
     def prepare_weight(self, b: torch.Tensor, moduli: Iterable[int]) -> PreparedRNSWeight:
         """B [K, N] int8/int16/int32 -> prepared centered residues."""
         self._validate_matrix(b, "b", 2)
@@ -684,7 +755,11 @@ class HipRNSBackend:
             workspace = self.create_workspace(device=device, channels=channels, m=m, n=n, k=k)
         self._check_workspace(workspace, channels=channels, m=m, n=n, device=device)
         plan = _native.make_plan(plan)
-        scratch = self._scratch(workspace, self._prepared_workspace_bytes(m, k, n, channels, plan))
+        packed_form = prepared.form == "packed"
+        if packed_form:
+            scratch = self._scratch(workspace, self._packed_workspace_bytes(m, k, n, channels))
+        else:
+            scratch = self._scratch(workspace, self._prepared_workspace_bytes(m, k, n, channels, plan))
         epi = None
         target = workspace.output
         if out is not None:
@@ -708,7 +783,8 @@ class HipRNSBackend:
         self._stats["fused_gemm_calls"] += 1
         if count_channels:
             self._stats[f"fused_gemm_channels_{channels}"] += 1
-        _native.check(self._lib.rnsmx_matmul_prepared_fused(
+        entry = self._lib.rnsmx_matmul_packed_fused if packed_form else self._lib.rnsmx_matmul_prepared_fused
+        _native.check(entry(
             _aligned(a).data_ptr(), _native.dtype_code(a.dtype), m, k, n,
             prepared.packed.data_ptr(), consts.native_ref, consts.compact_lut.data_ptr(),
             lut_channels, adaptive, epi, None if plan is None else ctypes.byref(plan),
@@ -780,14 +856,15 @@ class HipRNSBackend:
         return exact if decode else self._encode_int64_centered(exact, prepared_weight.moduli)
 
     def prepare_weight_adaptive(self, b: torch.Tensor, moduli: Iterable[int], *,
-                                min_channels: int = 3) -> PreparedAdaptiveRNSWeight:
-        """Encode once; every prefix variant shares the storage."""
-        full = self.prepare_weight(b, moduli)
+                                min_channels: int = 3, packed: bool = False) -> PreparedAdaptiveRNSWeight:
+        """Encode once; every prefix variant shares the storage (residue
+        planes, or with ``packed`` the 2-byte packed form)."""
+        full = self.prepare_weight_packed(b, moduli) if packed else self.prepare_weight(b, moduli)
         return self._adaptive_from(full, min_channels)
 
     def prepare_weight_adaptive_nk(self, w: torch.Tensor, moduli: Iterable[int], *,
-                                   min_channels: int = 3) -> PreparedAdaptiveRNSWeight:
-        full = self.prepare_weight_nk(w, moduli)
+                                   min_channels: int = 3, packed: bool = False) -> PreparedAdaptiveRNSWeight:
+        full = self.prepare_weight_packed_nk(w, moduli) if packed else self.prepare_weight_nk(w, moduli)
         return self._adaptive_from(full, min_channels)
 
     def _adaptive_from(self, full: PreparedRNSWeight, min_channels: int) -> PreparedAdaptiveRNSWeight:
@@ -798,8 +875,10 @@ class HipRNSBackend:
             prefix = full.moduli[:c]
             kernel = self.select_centered_kernel(k=full.k, n=full.n, moduli=prefix,
                                                  requested="auto", device=full.packed.device)
+            # residue planes: the prefix's planes; packed bytes serve every prefix whole
+            storage = full.packed if full.form == "packed" else full.packed[:c]
             variants[c] = PreparedRNSWeight(moduli=prefix, k=full.k, n=full.n, kernel=kernel,
-                                            packed=full.packed[:c], absmax=full.absmax)
+                                            packed=storage, absmax=full.absmax, form=full.form)
         return PreparedAdaptiveRNSWeight(variants, full.moduli, full.absmax, min_channels)
 
     def select_adaptive_variant(self, a: torch.Tensor, prepared: PreparedAdaptiveRNSWeight):

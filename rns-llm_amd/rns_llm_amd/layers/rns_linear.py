@@ -48,7 +48,8 @@ class RNSLinear(nn.Module):
                  moduli: Iterable[int] | None = None, moduli_strategy: str = "dense_coprime",
                  mode: str = "torch", kernel: str = "auto", quant_bits: int = 8,
                  fused: bool = True, lut_channels: int = 2, adaptive_channels: bool = False,
-                 adaptive_min_channels: int = 3, fused_epilogue: bool = True) -> None:
+                 adaptive_min_channels: int = 3, fused_epilogue: bool = True,
+                 packed_weights: bool = False) -> None:
         super().__init__()
         if quant_bits not in (8, 12, 16):
             raise ValueError("quant_bits must be 8, 12 or 16")
@@ -71,6 +72,11 @@ class RNSLinear(nn.Module):
         chosen = tuple(moduli) if moduli is not None else choose_moduli_for_dot(
             self.in_features, qmax, qmax, strategy=moduli_strategy)
         self.moduli = validate_moduli(chosen)
+        # packed_weights (no counterpart in the reference): keep the quantized
+        # weight as 2 bytes per value instead of one byte per channel
+        self.packed_weights = bool(packed_weights)
+        if self.packed_weights and len(self.moduli) > 6:
+            raise ValueError("packed weights take at most 6 channels")
 
         self.weight = nn.Parameter(torch.empty(out_features, in_features))
         if bias:
@@ -124,14 +130,16 @@ class RNSLinear(nn.Module):
                     moduli_strategy: str = "dense_coprime", mode: str = "torch",
                     kernel: str = "auto", quant_bits: int = 8, fused: bool = True,
                     lut_channels: int = 2, adaptive_channels: bool = False,
-                    adaptive_min_channels: int = 3, fused_epilogue: bool = True) -> "RNSLinear":
+                    adaptive_min_channels: int = 3, fused_epilogue: bool = True,
+                    packed_weights: bool = False) -> "RNSLinear":
         result = cls(layer.in_features, layer.out_features, bias=layer.bias is not None,
                      backend=backend, moduli=moduli, moduli_strategy=moduli_strategy, mode=mode,
                      kernel=kernel, quant_bits=quant_bits, fused=fused,
                      lut_channels=lut_channels, adaptive_channels=adaptive_channels,
                      adaptive_min_channels=adaptive_min_channels,
-                     fused_epilogue=fused_epilogue).to(device=layer.weight.device,
-                                                      dtype=layer.weight.dtype)
+                     fused_epilogue=fused_epilogue,
+                     packed_weights=packed_weights).to(device=layer.weight.device,
+                                                       dtype=layer.weight.dtype)
         result.weight.data.copy_(layer.weight.data)
         if layer.bias is not None and result.bias is not None:
             result.bias.data.copy_(layer.bias.data)
@@ -176,8 +184,16 @@ class RNSLinear(nn.Module):
         scale = self._symmetric_scale(w, dim=1)
         quantized = self._quantize(w, scale)  # [N, K]
         native_nk = hasattr(self.backend, "prepare_weight_nk")
+        if self.packed_weights and not hasattr(self.backend, "prepare_weight_packed_nk"):
+            raise ValueError("this backend has no packed weights")
         adaptive_prepared = None
-        if self.adaptive_channels:
+        if self.adaptive_channels and self.packed_weights:
+            adaptive_prepared = self.backend.prepare_weight_adaptive_nk(
+                quantized.contiguous(), self.moduli, min_channels=self.adaptive_min_channels, packed=True)
+            prepared = adaptive_prepared.variants[len(self.moduli)]
+        elif self.packed_weights:
+            prepared = self.backend.prepare_weight_packed_nk(quantized.contiguous(), self.moduli)
+        elif self.adaptive_channels:
             if native_nk:
                 adaptive_prepared = self.backend.prepare_weight_adaptive_nk(
                     quantized.contiguous(), self.moduli, min_channels=self.adaptive_min_channels)

@@ -1,0 +1,156 @@
+"""Packed weights: 2 bytes per weight value for any channel count
+(rnsmx_prepare_weight_packed / rnsmx_matmul_packed_fused).
+
+  * the device pack equals the oracle's byte split (hi = v >> 8, lo =
+    (v & 255) - 128) in the fragment-major layout, padding included;
+  * every packed product equals the exact int64 product: stream and MFMA
+    kernels (automatic and every forced plan), ragged M, N and K, int8,
+    int16 and int32 activations, 4 to 6 channels, int16 extremes;
+  * the device-side adaptive prefix on packed weights picks what the
+    oracle's selection picks (5 and 6 channels);
+  * RNSLinear with packed_weights equals the residue-plane layer and the
+    CPU float chain bit for bit (quant_bits 12 and 16, float32/16/bf16)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import linear_oracle
+from oracle import rns_oracle as ro
+from rns_llm_amd import RNSLinear
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+DENSE6 = (255, 253, 251, 247, 241, 239)
+DENSE5 = DENSE6[:5]
+DENSE4 = DENSE6[:4]
+
+
+def ints(shape, lo, hi, seed, dtype=torch.int16):
+    gen = torch.Generator().manual_seed(seed)
+    return torch.randint(lo, hi + 1, shape, generator=gen, dtype=torch.int32).to(dtype)
+
+
+def exact(a, w_nk):
+    return torch.from_numpy(ro.exact_matmul(a.numpy(), w_nk.t().numpy()))
+
+
+@pytest.mark.parametrize("n,k", [(1, 1), (37, 100), (64, 1024), (300, 777)])
+@pytest.mark.parametrize("dtype", [torch.int8, torch.int16])
+def test_pack_layout_matches_oracle_split(backend, n, k, dtype):
+    lim = 127 if dtype == torch.int8 else 32767
+    w = ints((n, k), -lim - 1, lim, n * 31 + k, dtype)
+    w[0, 0] = -lim - 1
+    w[-1, -1] = lim
+    prepared = backend.prepare_weight_packed_nk(w.to(DEV), DENSE6)
+    kp = (k + 63) // 64 * 64
+    n16 = (n + 15) // 16
+    assert prepared.form == "packed" and prepared.nbytes == 2 * n16 * 16 * kp
+    # the fragment grid back to [2][kp][16 n16]: byte 16 l + b of fragment
+    # (jb, ks) is column 16 jb + l % 16, K index 64 ks + 16 (l // 16) + b
+    grid = prepared.packed.cpu().view(2, n16, kp // 64, 4, 16, 16).permute(0, 2, 3, 5, 1, 4)
+    grid = grid.reshape(2, kp, n16 * 16).to(torch.int64)
+    hi, lo = ro.pack16_split(w.t().numpy())
+    np.testing.assert_array_equal(grid[0, :k, :n].numpy(), hi)
+    np.testing.assert_array_equal(grid[1, :k, :n].numpy(), lo)
+    # padding holds v = 0: hi 0, lo -128
+    assert (grid[0, k:] == 0).all() and (grid[0, :, n:] == 0).all()
+    assert (grid[1, k:] == -128).all() and (grid[1, :, n:] == -128).all()
+    assert int(prepared.absmax.item()) == int(w.to(torch.int32).abs().max())
+    assert torch.equal(prepared.values.cpu(), w.t().to(torch.int32))
+
+
+# (M, K, N): stream tiles (M <= 64, or 32-row tiles), MFMA tiles of 32 and
+# 64 rows, ragged everything, K below one step and spanning many
+SHAPES = [(1, 768, 768), (3, 100, 37), (16, 4096, 512), (40, 1000, 300), (96, 768, 2304),
+          (129, 768, 2304), (256, 2048, 1000), (500, 64, 70), (1024, 1024, 4096)]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+@pytest.mark.parametrize("moduli,a_lim", [(DENSE6, 32767), (DENSE5, 2047)], ids=["r6_int16", "r5_int12"])
+def test_packed_product_is_exact(backend, m, k, n, moduli, a_lim):
+    a = ints((m, k), -a_lim, a_lim, m + k + n)
+    w = ints((n, k), -32768, 32767, m * 3 + k)
+    a[0, : min(k, 8)] = -a_lim
+    w[0, : min(k, 8)] = -32768
+    want = exact(a, w)
+    prepared = backend.prepare_weight_packed_nk(w.to(DEV), moduli)
+    ws = backend.create_workspace(device=torch.device(DEV), channels=len(moduli), m=m, n=n)
+    for _ in range(2):
+        out = backend.matmul_prepared_fused(a.to(DEV), prepared, workspace=ws)
+        assert torch.equal(out.cpu(), want)
+
+
+# (kind, mb, nb, ks): stream 16 or 32 rows over 1-4 waves, MFMA 32 or 64 rows
+PLANS = [(1, 1, 1, 1), (1, 1, 1, 2), (1, 1, 1, 4), (1, 2, 1, 1), (1, 2, 1, 3), (2, 2, 1, 0), (2, 4, 1, 0)]
+
+
+@pytest.mark.parametrize("plan", PLANS, ids=lambda p: "k%d_%dx%d_ks%d" % p)
+@pytest.mark.parametrize("moduli", [DENSE4, DENSE6], ids=["r4", "r6"])
+@pytest.mark.parametrize("a_dtype", [torch.int8, torch.int16, torch.int32])
+def test_packed_every_plan_and_activation_type(backend, plan, moduli, a_dtype):
+    m, k, n = 70, 300, 130
+    # 4 channels hold K * 127 * 32767 (int8-range activations); 6 hold int16 ones
+    a_lim = 127 if len(moduli) == 4 else 32767
+    a = ints((m, k), -a_lim, a_lim, plan[1] * 10 + plan[3], a_dtype)
+    w = ints((n, k), -32768, 32767, 5 + len(moduli))
+    prepared = backend.prepare_weight_packed_nk(w.to(DEV), moduli)
+    out = backend.matmul_prepared_fused(a.to(DEV), prepared, plan=plan)
+    assert torch.equal(out.cpu(), exact(a.to(torch.int32), w))
+
+
+@pytest.mark.parametrize("expect,b_max", [(5, 127), (6, 32767)])
+def test_packed_adaptive_prefix(backend, expect, b_max):
+    """As the residue-plane test of the device prefix: int16 activations
+    against the 6-channel set, min_channels 3; a row L1 near K * 2^15 times
+    max|B| = 127 needs 5 channels, times 32767 needs 6."""
+    m, k, n = 7, 1024, 40
+    a = ints((m, k), -32767, 32767, expect)
+    a[m // 2] = 32767
+    w = ints((n, k), -b_max, b_max, expect + 1)
+    w[0, 0] = b_max
+    adaptive = backend.prepare_weight_adaptive_nk(w.to(DEV), DENSE6, min_channels=3, packed=True)
+    assert adaptive.variants[6].form == "packed" and adaptive.device_selection_is_safe(torch.int16)
+    out, meta = backend.matmul_prepared_adaptive_fused(a.to(DEV), adaptive, return_metadata=True)
+    c, bound, cap = ro.adaptive_select(a.numpy(), b_max, DENSE6, min_channels=3)
+    assert c == expect
+    assert dict(meta) == {"channels": c, "bound": bound, "capacity": cap}
+    assert torch.equal(out.cpu(), exact(a, w))
+
+
+@pytest.mark.parametrize("quant_bits", [12, 16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_rnslinear_packed_equals_planes_and_oracle(backend, quant_bits, dtype):
+    k, n, rows = 768, 200, 33
+    gen = torch.Generator().manual_seed(quant_bits)
+    x = torch.randn((rows, k), generator=gen).to(dtype)
+    layers = []
+    for packed in (False, True):
+        layer = RNSLinear(k, n, mode="rns", backend=backend, quant_bits=quant_bits,
+                          packed_weights=packed).to(device=DEV, dtype=dtype).eval()
+        layers.append(layer)
+    with torch.no_grad():
+        layers[1].weight.copy_(layers[0].weight)
+        layers[1].bias.copy_(layers[0].bias)
+        y_planes = layers[0](x.to(DEV))
+        backend.reset_stats()
+        y_packed = layers[1](x.to(DEV))
+    assert backend.stats_snapshot().get("pack_weight_calls") == 1
+    assert layers[1]._prepared_weight.form == "packed"
+    assert layers[1]._prepared_weight.nbytes * len(layers[1].moduli) == 2 * layers[0]._prepared_weight.nbytes
+    assert torch.equal(y_packed.cpu(), y_planes.cpu())
+    want, _ = linear_oracle.linear_forward(x, layers[1].weight.detach().cpu(), layers[1].bias.detach().cpu(),
+                                           bits=quant_bits)
+    assert torch.equal(y_packed.cpu(), want)
+
+
+def test_rnslinear_packed_adaptive(backend):
+    k, n = 1024, 96
+    gen = torch.Generator().manual_seed(3)
+    layer = RNSLinear(k, n, mode="rns", backend=backend, quant_bits=16, adaptive_channels=True,
+                      packed_weights=True).to(DEV).eval()
+    x = torch.randn((5, k), generator=gen)
+    with torch.no_grad():
+        y = layer(x.to(DEV))
+    want, _ = linear_oracle.linear_forward(x, layer.weight.detach().cpu(), layer.bias.detach().cpu(), bits=16)
+    assert torch.equal(y.cpu(), want)

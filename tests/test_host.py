@@ -200,6 +200,61 @@ def test_c_abi_rejects_bad_arguments_without_gpu():
     assert rc == _native.EINVAL and b"cannot split" in lib.rnsmx_last_error()
 
 
+def packed_plan(m, n, k, channels=6):
+    out = _native.Plan()
+    _native.check(_native.lib().rnsmx_packed_plan(m, n, k, channels, ctypes.byref(out)))
+    return out.as_tuple()
+
+
+# packed weights: the stream kernel where the residue-plane choice takes it
+# (16- or 32-row tiles, K over as many waves as chunks allow, at most 4),
+# else the MFMA kernel with 32- or 64-row tiles (fewest rows per CU, 64 on a
+# tie); never split
+PACKED_PLANS = [
+    ((1, 12288, 4096, 6), (1, 1, 1, 4, 1, 0)),   # decode: chunks of 3 steps, 4 waves
+    ((1, 768, 768, 6), (1, 1, 1, 4, 1, 0)),
+    ((1, 768, 768, 4), (1, 1, 1, 3, 1, 0)),      # 4 channels: chunks of 4 steps, 3 waves
+    ((96, 2304, 768, 6), (1, 2, 1, 4, 1, 0)),    # 432 stream tiles of 32 x 16
+    ((100, 2304, 768, 6), (2, 2, 1, 0, 1, 0)),   # MFMA: 144 tiles of 32 rows beat 72 of 64
+    ((1024, 4096, 1024, 6), (2, 4, 1, 0, 1, 0)),  # 256 rows per CU either way: 64
+]
+
+
+@pytest.mark.parametrize("shape,plan", PACKED_PLANS)
+def test_packed_plan_rules(shape, plan):
+    assert packed_plan(*shape) == plan
+
+
+def test_packed_queries_and_rejects_without_gpu():
+    lib = _native.lib()
+    tickets = 4 * _native.SPLIT_TICKETS
+    # counters + 2R activation planes + int32 row terms [R][round_up(M, 64) + 64] + row norms
+    assert lib.rnsmx_packed_workspace_bytes(1, 768, 768, 6) == tickets + (2 * 6 * 768 + 4 * 6 * 128) + 256
+    assert lib.rnsmx_packed_workspace_bytes(100, 100, 37, 5) == (
+        tickets + (2 * 5 * 100 * 128 + 4 * 5 * 192 + 255) // 256 * 256 + (8 * 100 + 255) // 256 * 256)
+    assert lib.rnsmx_packed_workspace_bytes(1, 768, 768, 7) == -1
+    out = _native.Plan()
+    assert lib.rnsmx_packed_plan(1, 768, 768, 7, ctypes.byref(out)) == _native.EINVAL
+    x = ctypes.c_int64(0)
+    assert lib.rnsmx_prepare_weight_packed(ctypes.addressof(x), _native.INT32, 4, 64, ctypes.addressof(x),
+                                           None, None) == _native.EINVAL
+    assert b"int8 or int16" in lib.rnsmx_last_error()
+    c7 = _native.make_moduli((255, 253, 251, 247, 241, 239, 233))
+    rc = lib.rnsmx_matmul_packed_fused(None, _native.INT16, 4, 64, 4, None, ctypes.byref(c7),
+                                       None, 0, None, None, None, None, 0, None, None)
+    assert rc == _native.EINVAL and b"at most 6" in lib.rnsmx_last_error()
+    c6 = _native.make_moduli((255, 253, 251, 247, 241, 239))
+    # 2 * K * 128 * 127 + 255 past 2^31 - 1 from K = 66,053
+    rc = lib.rnsmx_matmul_packed_fused(None, _native.INT16, 4, 66_053, 4, None, ctypes.byref(c6),
+                                       None, 0, None, None, None, None, 0, None, None)
+    assert rc == _native.ERANGE
+    for bad in (_native.Plan(2, 3, 1, 0, 1), _native.Plan(1, 1, 1, 1, 2), _native.Plan(3, 0, 0, 0, 1)):
+        rc = lib.rnsmx_matmul_packed_fused(ctypes.addressof(x), _native.INT16, 4, 64, 8, ctypes.addressof(x),
+                                           ctypes.byref(c6), None, 0, None, None, ctypes.byref(bad),
+                                           ctypes.addressof(x), 1 << 20, ctypes.addressof(x), None)
+        assert rc == _native.EINVAL and b"packed weights run" in lib.rnsmx_last_error()
+
+
 # --------------------------------------------------------------------------
 # host logic: moduli.py against the oracle
 # --------------------------------------------------------------------------

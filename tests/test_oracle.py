@@ -380,3 +380,47 @@ def test_torch_cpu_restatement_is_exact():
     big_p, coeffs = tco.crt_coefficients(mods)
     assert big_p == 3_999_736_455
     assert all(c % m == 1 and all(c % o == 0 for o in mods if o != m) for c, m in zip(coeffs, mods))
+
+
+def test_pack16_split_round_trip_every_int16():
+    v = np.arange(-(1 << 15), 1 << 15, dtype=np.int64)
+    hi, lo = ro.pack16_split(v)
+    assert hi.min() == -128 and hi.max() == 127 and lo.min() == -128 and lo.max() == 127
+    np.testing.assert_array_equal(256 * hi + lo + 128, v)
+    # the bytes the device stores: two's-complement high byte, low byte with its top bit flipped
+    np.testing.assert_array_equal(hi & 0xFF, (v >> 8) & 0xFF)
+    np.testing.assert_array_equal(lo & 0xFF, (v & 0xFF) ^ 0x80)
+    with pytest.raises(ValueError):
+        ro.pack16_split([1 << 15])
+
+
+@pytest.mark.parametrize("strategy", ["dense_coprime", "large_primes", "small_primes"])
+def test_packed_congruence_every_modulus(strategy):
+    """v = (256 mod m) hi + lo + 128 (mod m) for every int16 v and every
+    candidate modulus: the identity the packed kernels rely on."""
+    v = np.arange(-(1 << 15), 1 << 15, dtype=np.int64)
+    hi, lo = ro.pack16_split(v)
+    for m in ro.candidates_for_strategy(strategy):
+        np.testing.assert_array_equal(np.mod((256 % m) * hi + lo + 128, m), np.mod(v, m))
+
+
+@pytest.mark.parametrize("moduli,a_lim,b_lim", [((255, 253, 251, 247, 241, 239), 32767, 32767),
+                                                ((255, 253, 251, 247, 241), 2047, 32767),
+                                                ((255, 253, 251, 247), 127, 127)])
+def test_packed_channel_residues_equal_exact_product(moduli, a_lim, b_lim):
+    """The packed kernels' per-channel sum (a' hi + a lo + 128 rowsum a)
+    reduces to the residues of the exact product, including the int16
+    extremes; dropping the row term or using d = m - 256 fails."""
+    rng = np.random.default_rng(7)
+    a = rng.integers(-a_lim, a_lim + 1, size=(9, 70))
+    b = rng.integers(-b_lim - 1, b_lim + 1, size=(70, 11))
+    b[0, 0], b[1, 1], a[0, 0] = -b_lim - 1, b_lim, -a_lim
+    want = ro.encode_canonical(ro.exact_matmul(a, b), moduli).astype(np.int64)
+    np.testing.assert_array_equal(ro.packed_channel_residues(a, b, moduli), want)
+    # a planted mistake in the restatement (no row term) is caught
+    hi, lo = ro.pack16_split(b)
+    ac = ro.encode_centered(a, moduli).astype(np.int64)
+    m = moduli[0]
+    r = np.mod((256 % m) * ac[0], m)
+    wrong = np.mod((r - m * (r > m // 2)) @ hi + ac[0] @ lo, m)
+    assert not np.array_equal(wrong, want[0])
