@@ -676,7 +676,7 @@ def main():
                 f"{rows[-1]['channels']} channels, "
                 f"{rows[-1]['eff_tops']:.1f} eff TOPS, {rows[-1]['gbs_alg']:.0f} GB/s alg, "
                 f"{rows[-1]['bound']} roofline {rows[-1]['roofline_frac']:.3f}")
-        for m in (1, 16, 512):
+        for m in (1, 4, 16, 512):
             for packed in (False, True):
                 rows.append(measure_wide(backend, m, 4096, 12288, packed, args.steps, args.warmup, rot, 91, device))
                 log(f"bench: wide int16 x int16, 6 channels, {rows[-1]['weight_form']} weights "

@@ -131,7 +131,8 @@ inline GemmArgsK<RCAP> compact_args(const GemmArgs &g) {
 
 // kStreamWide: the stream kernel with chunks of up to 8 K steps (long K).
 // kMfma3: the MFMA kernel with three column waves (48*nb-column tiles).
-enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kLds = 3, kStreamWide = 4, kMfma3 = 5 };
+// kRows: packed weights at decode (rows_packed_kernel: MFMA rows are channels).
+enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kLds = 3, kStreamWide = 4, kMfma3 = 5, kRows = 6 };
 
 // ks: waves splitting K (stream kernel) or ring depth, 0 = automatic (MFMA
 // kernel); splits: workgroups splitting K (1 = none); tail: only the tiles
@@ -1168,6 +1169,113 @@ __global__ __launch_bounds__(256) void stream_packed_kernel(const GemmArgsK<RCAP
 }
 
 // ---------------------------------------------------------------------------
+// Packed weights at decode (a few tokens): the MFMA rows carry channels.
+// The packed weight bytes hi and lo are the same for every channel, so one
+// 16-row A fragment can hold RCAP channels of TPB = 16 / RCAP tokens (row
+// t * RCAP + c: token t, channel c) and a single MFMA against hi (or lo)
+// makes every channel's product at once: per K step two B loads, two A
+// loads per block of TPB tokens and three MFMAs (a' x hi + a x lo into the
+// sums, a x ones into the row sums that carry the 128 sum_k a_k term),
+// where the per-channel form issues 2R A loads and 2R MFMAs per 16 rows.
+// A is encoded for this kernel as [block][a' | a][kp/64][1 KB] fragments
+// (a_cs = bytes per block); rows past the tokens or channels are zero.
+// A workgroup owns 16 columns and every token (NBLK = 1, 2, 4 or 8 blocks;
+// the B fragments of a step serve them all); its KS waves split K as in
+// stream_kernel, chunks of U steps in flight per wave (fewer with more
+// blocks: their A fragments share the registers).  The
+// sums meet in LDS, where each thread gathers the RCAP channel sums of one
+// output element (a column of the fragment) for the Garner epilogue.  The
+// row-sum term keeps |sum| <= 2 K 128 max_half + 128 K max_half (host
+// bound: K <= 44,035 for max_half = 127).
+// ---------------------------------------------------------------------------
+template <int RCAP, int NBLK>
+__global__ __launch_bounds__(256) void rows_packed_kernel(const GemmArgsK<RCAP> args) {
+  KArgs<RCAP> &g = kernel_args<GemmArgsK<RCAP>>();
+  prefetch_kernel_args<kGemmHotArgBytes>();
+  static_assert(RCAP == 4 || RCAP == 6, "4 or 6 channel rows per token");
+  constexpr int TPB = 16 / RCAP;                                   // tokens per 16-row block
+  constexpr int U = NBLK == 1 ? 8 : NBLK == 2 ? 6 : NBLK == 4 ? 4 : 2;  // K steps per chunk
+  __shared__ __attribute__((aligned(16))) int32_t sums[NBLK][16][16];
+  __shared__ int64_t red[4];
+  __shared__ int bcast;
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nthreads = g.threads, ks_n = nthreads >> 6;
+  const int c_act = active_channels<RCAP>(g, red, &bcast, nthreads);
+  const int n0 = blockIdx.x * 16;
+  const int nk = g.kp >> 6;
+  const int64_t mstride = static_cast<int64_t>(nk) * 1024;  // a' fragments, then a fragments
+  const int8_t *ap = g.a + lane * 16;
+  const int8_t *bp = g.b + static_cast<int64_t>(blockIdx.x) * g.b_ld + lane * 16;
+  const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+
+  i32x4 acc[NBLK], rsum[NBLK];
+  static_for<NBLK>([&](auto B) {
+    acc[decltype(B)::value] = acc_zero();
+    rsum[decltype(B)::value] = acc_zero();
+  });
+  i32x4 fh[U], fl[U], fa2[U][NBLK], fa[U][NBLK];
+  auto load_chunk = [&](int q) {
+    static_for<U>([&](auto UU) {
+      constexpr int u = decltype(UU)::value;
+      const int ks = min(q + u, nk - 1);
+      const bool live = q + u < nk;  // steps past K: zero activations
+      fh[u] = load16(bp + ks * 1024);
+      fl[u] = load16(bp + g.b_cs + ks * 1024);
+      static_for<NBLK>([&](auto B) {
+        constexpr int b = decltype(B)::value;
+        fa2[u][b] = select16(live, load16(ap + b * g.a_cs + ks * 1024));
+        fa[u][b] = select16(live, load16(ap + b * g.a_cs + mstride + ks * 1024));
+      });
+    });
+  };
+  auto mfma_chunk = [&]() {
+    static_for<U>([&](auto UU) {
+      constexpr int u = decltype(UU)::value;
+      static_for<NBLK>([&](auto B) {
+        constexpr int b = decltype(B)::value;
+        acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa2[u][b], fh[u], acc[b], 0, 0, 0);
+        acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][b], fl[u], acc[b], 0, 0, 0);
+        rsum[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][b], ones, rsum[b], 0, 0, 0);
+      });
+    });
+  };
+  load_chunk(wave * U);
+  Epi<RCAP> e;
+  load_epi<RCAP>(g, e, c_act);
+  pin_epi<RCAP>(e);
+  for (int i = threadIdx.x; i < NBLK * 256; i += nthreads) (&sums[0][0][0])[i] = 0;
+  if (wave * U < nk) mfma_chunk();
+  for (int q = wave * U + ks_n * U; q < nk; q += ks_n * U) {
+    load_chunk(q);
+    mfma_chunk();
+  }
+  __syncthreads();
+  // channel sums of every element: a' hi + a lo + 128 sum_k a
+  static_for<NBLK>([&](auto B) {
+    constexpr int b = decltype(B)::value;
+    static_for<4>([&](auto T) {
+      constexpr int t = decltype(T)::value;
+      atomicAdd(&sums[b][4 * (lane >> 4) + t][lane & 15], acc[b][t] + 128 * rsum[b][t]);
+    });
+  });
+  __syncthreads();
+
+  const int m_lim = g.m, n_lim = g.n;
+  with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) {
+    for (int x = threadIdx.x; x < m_lim * 16; x += nthreads) {
+      const int token = x >> 4, j = x & 15, col = n0 + j;
+      if (col >= n_lim) continue;
+      const int b = token / TPB, row0 = (token % TPB) * RCAP;
+      int32_t v[RCAP];
+      static_for<RCAP>([&](auto C) { v[decltype(C)::value] = sums[b][row0 + decltype(C)::value][j]; });
+      finish_element<RCAP, decltype(FAST)::value, decltype(OUT)::value>(
+          g, e, c_act, v, static_cast<int64_t>(token) * e.out_ld + col, col_scale<RCAP>(e, col, n_lim));
+    }
+  });
+}
+
+// ---------------------------------------------------------------------------
 // MFMA GEMM (M > 128 where the LDS kernel does not apply: C2 M=256, C4;
 // also smaller batches of wide or long-K shapes, e.g. C5 M=32-128).  A
 // workgroup of 4 waves owns a (16*MB) x (4*16*NB) tile: the A rows (shared by
@@ -1719,6 +1827,10 @@ inline GemmGrid gemm_grid(const GemmChoice &c, int64_t m, int64_t n) {
     r.tiles = cdiv(m, 16 * c.mb) * cdiv(n, 16 * c.nb);
     r.waves = c.ks < 1 ? 1 : c.ks;
     r.chunks = c.mb * c.nb;
+  } else if (c.kind == kRows) {
+    r.tiles = cdiv(n, 16);
+    r.waves = c.ks < 1 ? 1 : c.ks;
+    r.chunks = c.mb;
   } else if (c.kind == kLds) {
     r.tiles = cdiv(m, kLdsBM) * cdiv(n, kLdsBN);
     r.waves = 8;
@@ -1757,6 +1869,19 @@ bool launch_packed(GemmArgsK<RCAP> g, const GemmChoice &c, hipStream_t st) {
     return false;
   } else {
     if (c.splits > 1) return false;
+    if (c.kind == kRows && c.ks >= 1 && c.ks <= 4) {
+      g.tiles_m = 1;
+      g.tiles_n = (g.n + 15) / 16;
+      g.threads = 64 * c.ks;
+      const dim3 grid(static_cast<unsigned>(g.tiles_n)), block(64 * c.ks);
+      switch (c.mb) {
+        case 1: hipLaunchKernelGGL((rows_packed_kernel<RCAP, 1>), grid, block, 0, st, g); return true;
+        case 2: hipLaunchKernelGGL((rows_packed_kernel<RCAP, 2>), grid, block, 0, st, g); return true;
+        case 4: hipLaunchKernelGGL((rows_packed_kernel<RCAP, 4>), grid, block, 0, st, g); return true;
+        case 8: hipLaunchKernelGGL((rows_packed_kernel<RCAP, 8>), grid, block, 0, st, g); return true;
+        default: return false;
+      }
+    }
     if (c.kind == kStream) {
 #define RNSMX_STREAM_PK(MB_)                                                                           \
   if (c.mb == MB_ && c.nb == 1) {                                                                     \

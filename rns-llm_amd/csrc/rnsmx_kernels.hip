@@ -219,6 +219,58 @@ __global__ __launch_bounds__(256) void encode_frag_kernel(const EncodeArgs e) {
   }
 }
 
+// Activations for rows_packed_kernel (packed weights at decode):
+// [block][a' | a][kp/64][1 KB] MFMA A fragments in which row t * rpt + c of
+// block b holds token b * (16 / rpt) + t, channel c (a' = centered residue
+// of d_c a, d_c = 256 mod m_c); rows past the tokens or the channels and K
+// past cols are zero.  One wave per fragment: lane l writes row l & 15, K
+// bytes 64 ks + 16 (l >> 4) .. +16.
+struct TokenRowsArgs {
+  const void *values;
+  int64_t m, cols, nk, blocks;  // blocks: the GEMM's (blocks past the tokens are zero)
+  int32_t rpt;                  // rows per token: the kernel's channel capacity
+  int8_t *out;
+  rnsmx_moduli_t mods;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void encode_token_rows_kernel(const TokenRowsArgs e) {
+  const int lane = threadIdx.x & 63;
+  const int tpb = 16 / e.rpt;
+  const int64_t f = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (f >= e.blocks * 2 * e.nk) return;
+  const int64_t ks = f % e.nk, b = f / (2 * e.nk);
+  const bool scaled = (f / e.nk) % 2 == 0;  // a' fragments first
+  const int r = lane & 15, t = r / e.rpt, c = r % e.rpt;
+  const int64_t token = b * tpb + t, k0 = ks * 64 + (lane >> 4) * 16;
+  i32x4 w = {0, 0, 0, 0};
+  if (t < tpb && token < e.m && c < e.mods.channels) {
+    const T *src = static_cast<const T *>(e.values) + token * e.cols;
+    int32_t v[16];
+    if (e.cols % 16 == 0 && k0 + 16 <= e.cols) {
+      load16<T>(src + k0, v);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) v[q] = (k0 + q < e.cols) ? static_cast<int32_t>(src[k0 + q]) : 0;
+    }
+    const uint32_t m = static_cast<uint32_t>(e.mods.moduli[c]);
+    const uint32_t magic = e.mods.magic[c], c31 = e.mods.c31[c];
+    const int32_t d = static_cast<int32_t>(256u % m);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int32_t x = centered_i32(v[4 * g + q], m, magic, c31);
+        if (scaled) x = centered_i32(d * x, m, magic, c31);
+        packed |= (static_cast<uint32_t>(x) & 0xFFu) << (8 * q);
+      }
+      w[g] = static_cast<int32_t>(packed);
+    }
+  }
+  *reinterpret_cast<i32x4 *>(e.out + f * 1024 + lane * 16) = w;
+}
+
 // Packed weight preparation: int8/int16 [N][K] -> two byte planes in the
 // fragment-major order of encode_frag_kernel ([2][N16][nk][1024]): hi =
 // v >> 8 and lo = (v & 255) - 128, so v = 256 hi + lo + 128 with both bytes
@@ -771,8 +823,24 @@ static int32_t launch_encode_rows(int32_t dtype, const EncodeArgs &e, hipStream_
 // waves), else the MFMA kernel with 32- or 64-row tiles, whichever leaves
 // fewer rows on a CU (rounds of 256 workgroups times the tile height;
 // 64 rows on a tie); never split over workgroups.
+// Packed weights at decode: rows_packed_kernel for up to 8 blocks of
+// 16 / R tokens (R = 4 or 6 channel rows each; the fewest blocks, a power
+// of two, that hold M) while its sums fit int32 (K * 384 * 127 for moduli
+// up to 255).
+static constexpr int kRowsMaxKp = 44032;
+static constexpr int kRowsMaxBlocks = 8;
+
+static int rows_steps_of(int nblk) { return nblk == 1 ? 8 : nblk == 2 ? 6 : nblk == 4 ? 4 : 2; }
+
 static GemmChoice packed_auto(const GemmArgs &g) {
   const int rcap = g.mods.channels <= 4 ? 4 : 6;
+  const int tpb = 16 / rcap;
+  if (g.m <= kRowsMaxBlocks * tpb && g.kp <= kRowsMaxKp) {
+    int nblk = 1;
+    while (nblk * tpb < g.m) nblk *= 2;
+    const int u = rows_steps_of(nblk);
+    return GemmChoice{kRows, nblk, 1, std::min(4, std::max(1, (g.kp / 64 + u - 1) / u)), 1, 0};
+  }
   GemmChoice c = choose_gemm(g, false);
   c.splits = 1;
   c.tail = 0;
@@ -801,10 +869,19 @@ static int32_t packed_plan_from(const rnsmx_plan_t *plan, const GemmArgs &g, Gem
   }
   const bool stream = plan->kind == kStream && (plan->mb == 1 || plan->mb == 2) && plan->nb == 1;
   const bool mfma = plan->kind == kMfma && (plan->mb == 2 || plan->mb == 4) && plan->nb == 1;
-  if (!(stream || mfma) || plan->splits > 1 || plan->tail != 0)
-    return fail(RNSMX_EINVAL, "packed weights run the stream kernel (16- or 32-row tiles) or the MFMA kernel "
-                              "(32- or 64-row tiles), one column block, K not split over workgroups");
-  c = GemmChoice{plan->kind, plan->mb, 1, stream ? plan->ks : 0, 1, 0};
+  const bool rows = plan->kind == kRows && (plan->mb == 1 || plan->mb == 2 || plan->mb == 4 || plan->mb == 8) &&
+                    plan->nb == 1 && plan->ks >= 1 && plan->ks <= 4;
+  if (!(stream || mfma || rows) || plan->splits > 1 || plan->tail != 0)
+    return fail(RNSMX_EINVAL, "packed weights run the stream kernel (16- or 32-row tiles), the MFMA kernel "
+                              "(32- or 64-row tiles) or the channel-row kernel (1, 2, 4 or 8 token blocks), one "
+                              "column block, K not split over workgroups");
+  if (rows) {
+    const int tpb = 16 / (g.mods.channels <= 4 ? 4 : 6);
+    if (g.m > plan->mb * tpb) return fail(RNSMX_EINVAL, "channel-row plan: more tokens than its blocks hold");
+    if (g.kp * int64_t{384} * max_half(g.mods) > INT32_MAX)
+      return fail(RNSMX_ERANGE, "channel-row plan: K * 384 * max(floor(m/2)) exceeds the int32 sums");
+  }
+  c = GemmChoice{plan->kind, plan->mb, 1, stream || rows ? plan->ks : 0, 1, 0};
   return RNSMX_OK;
 }
 
@@ -1205,12 +1282,15 @@ static PreparedLayout prepared_layout(bool araw, int64_t m, int64_t kp, int32_t 
 }
 
 // Packed-weight workspace: [split counters (unused: never split)][2R
-// activation planes, then the int32 row terms [R][packed_corr_ld(M)]][row
-// L1 norms].
+// activation planes, then the int32 row terms [R][packed_corr_ld(M)]; or
+// (up to 32 tokens) 8 blocks of channel-row fragments][row L1 norms].
 static PreparedLayout packed_layout(int64_t m, int64_t kp, int32_t channels) {
   PreparedLayout l{};
   l.a_res = kTicketBytes;
-  l.row_l1 = l.a_res + round_up(2 * channels * m * kp + 4 * channels * packed_corr_ld(m), 256);
+  // per-channel planes, or (up to 8 tokens) two blocks of channel-row fragments
+  const int64_t planes = 2 * channels * m * kp + 4 * channels * packed_corr_ld(m);
+  const int64_t rows = m <= kRowsMaxBlocks * 4 ? int64_t{kRowsMaxBlocks} * 2 * kp * 16 : 0;
+  l.row_l1 = l.a_res + round_up(std::max(planes, rows), 256);
   l.xchg = l.row_l1 + round_up(8 * m, 256);
   l.total = l.xchg;
   return l;
@@ -1305,7 +1385,31 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
   e.row_l1 = min_ch != 0 ? row_l1 : nullptr;
   e.absmax = nullptr;
   e.mods = *mods;
-  if (packed) {
+  const bool rows = packed && c.kind == kRows;
+  if (rows) {
+    TokenRowsArgs t{};
+    t.values = a_dev;
+    t.m = m;
+    t.cols = k;
+    t.nk = kp / 64;
+    t.rpt = R <= 4 ? 4 : 6;
+    t.blocks = c.mb;
+    t.out = a_res;
+    t.mods = *mods;
+    const int64_t frags = t.blocks * 2 * t.nk;
+    const dim3 grid(static_cast<unsigned>((frags + 3) / 4)), block(256);
+    switch (a_dtype) {
+      case RNSMX_INT8: hipLaunchKernelGGL(encode_token_rows_kernel<int8_t>, grid, block, 0, st, t); break;
+      case RNSMX_INT16: hipLaunchKernelGGL(encode_token_rows_kernel<int16_t>, grid, block, 0, st, t); break;
+      default: hipLaunchKernelGGL(encode_token_rows_kernel<int32_t>, grid, block, 0, st, t); break;
+    }
+    if (int32_t rc = check_launch("encode_token_rows")) return rc;
+    if (min_ch != 0) {  // the row norms of the adaptive bound
+      EncodeArgs l1 = e;
+      l1.out = nullptr;
+      if (int32_t rc = launch_encode_rows(a_dtype, l1, st)) return rc;
+    }
+  } else if (packed) {
     if (int32_t rc = launch_encode_rows(a_dtype, e, st, true)) return rc;
   } else if (!araw || (min_ch != 0 && !l1_in_gemm)) {
     if (int32_t rc = launch_encode_rows(a_dtype, e, st)) return rc;
@@ -1316,7 +1420,7 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
     g.a_cs = 0;
   } else {
     g.a = a_res;
-    g.a_cs = kp * m;
+    g.a_cs = rows ? 2 * kp * 16 : kp * m;  // channel-row fragments: bytes per token block
   }
   g.b = packed_dev;
   g.b_ld = kp * 16;

@@ -6,6 +6,8 @@
   * every packed product equals the exact int64 product: stream and MFMA
     kernels (automatic and every forced plan), ragged M, N and K, int8,
     int16 and int32 activations, 4 to 6 channels, int16 extremes;
+  * decode shapes on the channel-row kernel (MFMA rows carry channels: 1
+    to 8 blocks of 16 / R tokens), every wave count, float epilogues;
   * the device-side adaptive prefix on packed weights picks what the
     oracle's selection picks (5 and 6 channels);
   * RNSLinear with packed_weights equals the residue-plane layer and the
@@ -99,13 +101,63 @@ def test_packed_every_plan_and_activation_type(backend, plan, moduli, a_dtype):
     assert torch.equal(out.cpu(), exact(a.to(torch.int32), w))
 
 
+# decode: the channel-row kernel (kind 6) with 1, 2, 4 or 8 blocks of 16 / R
+# tokens, every wave count, ragged N and K, three activation types
+ROW_CASES = [(DENSE6, 1), (DENSE6, 2), (DENSE6, 3), (DENSE6, 4), (DENSE6, 7), (DENSE6, 16), (DENSE4, 1),
+             (DENSE4, 5), (DENSE4, 8), (DENSE4, 12), (DENSE4, 32), (DENSE5, 3)]
+
+
+@pytest.mark.parametrize("moduli,m", ROW_CASES, ids=lambda v: str(len(v)) if isinstance(v, tuple) else str(v))
+@pytest.mark.parametrize("ks", [0, 1, 3, 4])
+@pytest.mark.parametrize("a_dtype", [torch.int8, torch.int16, torch.int32])
+def test_packed_channel_rows_exact(backend, moduli, m, ks, a_dtype):
+    k, n = 1000, 77
+    a_lim = 127 if len(moduli) == 4 or a_dtype == torch.int8 else 2047 if len(moduli) == 5 else 32767
+    a = ints((m, k), -a_lim, a_lim, m * 7 + ks, a_dtype)
+    a[0, :4] = -a_lim
+    w = ints((n, k), -32768, 32767, 11 * len(moduli) + m)
+    w[0, :4] = -32768
+    prepared = backend.prepare_weight_packed_nk(w.to(DEV), moduli)
+    tpb = 16 // (4 if len(moduli) <= 4 else 6)
+    blocks = 1
+    while blocks * tpb < m:
+        blocks *= 2
+    plan = None if ks == 0 else (6, blocks, 1, ks)
+    ws = backend.create_workspace(device=torch.device(DEV), channels=len(moduli), m=m, n=n)
+    for _ in range(2):
+        out = backend.matmul_prepared_fused(a.to(DEV), prepared, workspace=ws, plan=plan)
+        assert torch.equal(out.cpu(), exact(a.to(torch.int32), w))
+
+
+@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_packed_channel_rows_float_epilogue(backend, m, out_dtype):
+    k, n = 4096, 130
+    a = ints((m, k), -32767, 32767, m)
+    w = ints((n, k), -32767, 32767, m + 1)
+    want = exact(a, w)
+    gen = torch.Generator().manual_seed(9)
+    a_scale = torch.tensor([3e-5], dtype=torch.float32)
+    w_scale = torch.rand((n,), generator=gen) * 1e-4
+    bias = torch.randn((n,), generator=gen)
+    prepared = backend.prepare_weight_packed_nk(w.to(DEV), DENSE6)
+    out = torch.empty((m, n), dtype=out_dtype, device=DEV)
+    backend.matmul_prepared_fused(a.to(DEV), prepared, out=out, a_scale=a_scale.to(DEV),
+                                  w_scale=w_scale.to(DEV), bias=bias.to(DEV))
+    ref = ((want.float() * a_scale.view(1, 1)) * w_scale.unsqueeze(0) + bias).to(out_dtype)
+    bits = torch.int32 if out_dtype == torch.float32 else torch.int16
+    assert torch.equal(out.cpu().view(bits), ref.view(bits))
+
+
+@pytest.mark.parametrize("m", [1, 3, 7])
 @pytest.mark.parametrize("expect,b_max", [(5, 127), (6, 32767)])
-def test_packed_adaptive_prefix(backend, expect, b_max):
+def test_packed_adaptive_prefix(backend, m, expect, b_max):
     """As the residue-plane test of the device prefix: int16 activations
     against the 6-channel set, min_channels 3; a row L1 near K * 2^15 times
-    max|B| = 127 needs 5 channels, times 32767 needs 6."""
-    m, k, n = 7, 1024, 40
-    a = ints((m, k), -32767, 32767, expect)
+    max|B| = 127 needs 5 channels, times 32767 needs 6 (on the channel-row
+    kernel: 1, 2 or 4 blocks)."""
+    k, n = 1024, 40
+    a = ints((m, k), -32767, 32767, expect + m)
     a[m // 2] = 32767
     w = ints((n, k), -b_max, b_max, expect + 1)
     w[0, 0] = b_max
@@ -118,10 +170,11 @@ def test_packed_adaptive_prefix(backend, expect, b_max):
     assert torch.equal(out.cpu(), exact(a, w))
 
 
+@pytest.mark.parametrize("rows", [1, 3, 33])
 @pytest.mark.parametrize("quant_bits", [12, 16])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-def test_rnslinear_packed_equals_planes_and_oracle(backend, quant_bits, dtype):
-    k, n, rows = 768, 200, 33
+def test_rnslinear_packed_equals_planes_and_oracle(backend, quant_bits, dtype, rows):
+    k, n = 768, 200
     gen = torch.Generator().manual_seed(quant_bits)
     x = torch.randn((rows, k), generator=gen).to(dtype)
     layers = []

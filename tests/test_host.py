@@ -206,14 +206,23 @@ def packed_plan(m, n, k, channels=6):
     return out.as_tuple()
 
 
-# packed weights: the stream kernel where the residue-plane choice takes it
-# (16- or 32-row tiles, K over as many waves as chunks allow, at most 4),
-# else the MFMA kernel with 32- or 64-row tiles (fewest rows per CU, 64 on a
-# tie); never split
+# packed weights: the channel-row kernel for up to eight blocks of 16 / R
+# tokens (kind 6, mb = blocks, a power of two), then the stream kernel where the
+# residue-plane choice takes it (16- or 32-row tiles, K over as many waves
+# as chunks allow, at most 4), else the MFMA kernel with 32- or 64-row
+# tiles (fewest rows per CU, 64 on a tie); never split
 PACKED_PLANS = [
-    ((1, 12288, 4096, 6), (1, 1, 1, 4, 1, 0)),   # decode: chunks of 3 steps, 4 waves
-    ((1, 768, 768, 6), (1, 1, 1, 4, 1, 0)),
-    ((1, 768, 768, 4), (1, 1, 1, 3, 1, 0)),      # 4 channels: chunks of 4 steps, 3 waves
+    ((1, 12288, 4096, 6), (6, 1, 1, 4, 1, 0)),   # decode: channel rows, chunks of 8 steps, 4 waves
+    ((1, 768, 768, 6), (6, 1, 1, 2, 1, 0)),
+    ((2, 768, 768, 6), (6, 1, 1, 2, 1, 0)),      # 2 tokens x 6 channel rows in one block
+    ((3, 768, 768, 6), (6, 2, 1, 2, 1, 0)),      # two blocks, chunks of 6 steps
+    ((8, 768, 768, 4), (6, 2, 1, 2, 1, 0)),      # 4 tokens x 4 channel rows per block
+    ((5, 768, 768, 6), (6, 4, 1, 3, 1, 0)),      # four blocks, chunks of 4 steps
+    ((9, 768, 768, 4), (6, 4, 1, 3, 1, 0)),
+    ((16, 12288, 4096, 6), (6, 8, 1, 4, 1, 0)),  # eight blocks, chunks of 2 steps
+    ((17, 768, 768, 6), (1, 1, 1, 4, 1, 0)),     # past eight blocks: stream, chunks of 3 steps
+    ((33, 768, 768, 4), (1, 1, 1, 3, 1, 0)),     # 4 channels: chunks of 4 steps, 3 waves
+    ((1, 768, 50_000, 6), (1, 1, 1, 4, 1, 0)),   # K past the channel-row sums' int32 range
     ((96, 2304, 768, 6), (1, 2, 1, 4, 1, 0)),    # 432 stream tiles of 32 x 16
     ((100, 2304, 768, 6), (2, 2, 1, 0, 1, 0)),   # MFMA: 144 tiles of 32 rows beat 72 of 64
     ((1024, 4096, 1024, 6), (2, 4, 1, 0, 1, 0)),  # 256 rows per CU either way: 64
@@ -228,8 +237,10 @@ def test_packed_plan_rules(shape, plan):
 def test_packed_queries_and_rejects_without_gpu():
     lib = _native.lib()
     tickets = 4 * _native.SPLIT_TICKETS
-    # counters + 2R activation planes + int32 row terms [R][round_up(M, 64) + 64] + row norms
-    assert lib.rnsmx_packed_workspace_bytes(1, 768, 768, 6) == tickets + (2 * 6 * 768 + 4 * 6 * 128) + 256
+    # counters + the larger of (2R activation planes + int32 row terms [R][round_up(M, 64) + 64])
+    # and (up to 32 tokens) eight blocks of channel-row fragments [2][kp/64][1 KB] + row norms
+    assert lib.rnsmx_packed_workspace_bytes(1, 768, 768, 6) == tickets + max(
+        2 * 6 * 768 + 4 * 6 * 128, 8 * 2 * 768 * 16) + 256
     assert lib.rnsmx_packed_workspace_bytes(100, 100, 37, 5) == (
         tickets + (2 * 5 * 100 * 128 + 4 * 5 * 192 + 255) // 256 * 256 + (8 * 100 + 255) // 256 * 256)
     assert lib.rnsmx_packed_workspace_bytes(1, 768, 768, 7) == -1
@@ -248,7 +259,13 @@ def test_packed_queries_and_rejects_without_gpu():
     rc = lib.rnsmx_matmul_packed_fused(None, _native.INT16, 4, 66_053, 4, None, ctypes.byref(c6),
                                        None, 0, None, None, None, None, 0, None, None)
     assert rc == _native.ERANGE
-    for bad in (_native.Plan(2, 3, 1, 0, 1), _native.Plan(1, 1, 1, 1, 2), _native.Plan(3, 0, 0, 0, 1)):
+    rows_plan = _native.Plan(6, 1, 1, 2, 1)  # one block holds 2 tokens of 6 channels, not 4
+    rc = lib.rnsmx_matmul_packed_fused(ctypes.addressof(x), _native.INT16, 4, 64, 8, ctypes.addressof(x),
+                                       ctypes.byref(c6), None, 0, None, None, ctypes.byref(rows_plan),
+                                       ctypes.addressof(x), 1 << 20, ctypes.addressof(x), None)
+    assert rc == _native.EINVAL and b"more tokens" in lib.rnsmx_last_error()
+    for bad in (_native.Plan(2, 3, 1, 0, 1), _native.Plan(1, 1, 1, 1, 2), _native.Plan(3, 0, 0, 0, 1),
+                _native.Plan(6, 3, 1, 1, 1), _native.Plan(6, 16, 1, 1, 1), _native.Plan(6, 1, 1, 5, 1)):
         rc = lib.rnsmx_matmul_packed_fused(ctypes.addressof(x), _native.INT16, 4, 64, 8, ctypes.addressof(x),
                                            ctypes.byref(c6), None, 0, None, None, ctypes.byref(bad),
                                            ctypes.addressof(x), 1 << 20, ctypes.addressof(x), None)
