@@ -1358,16 +1358,21 @@ __device__ __forceinline__ void mfma_body() {
 
   const i32x4 zero = {0, 0, 0, 0};
   i32x4 ra[P][AC];
+  bool akeep[P][AC];
   i32x4 fb[P][BP][NB];
-  // loads of K step ks (clamped to the last one; A of steps past K is zero)
+  // loads of K step ks (clamped to the last one; A of steps past K is
+  // zero).  The zeroing is applied when the A chunk is stored to LDS, P - 1
+  // steps later: a select right after the load would make the wave wait for
+  // that load (and, loads completing in order, for every load before it),
+  // emptying the ring once per trip.
   auto gload = [&](auto SLOT, int ks) {
     constexpr int s = decltype(SLOT)::value;
     const int kc = min(ks, nk - 1);
     static_for<AC>([&](auto II) {
       constexpr int i = decltype(II)::value;
       const int ka = kc * 64 + apart[i];
-      const bool keep = aon[i] && ks < nk && ka < a_k;
-      ra[s][i] = select16(keep, load16(asrc[i] + min(ka, a_k - 16)));
+      akeep[s][i] = aon[i] && ks < nk && ka < a_k;
+      ra[s][i] = load16(asrc[i] + min(ka, a_k - 16));
     });
     static_for<BP>([&](auto C) {
       constexpr int c = decltype(C)::value;
@@ -1381,7 +1386,7 @@ __device__ __forceinline__ void mfma_body() {
     constexpr int s = decltype(SLOT)::value;
     static_for<AC>([&](auto II) {
       constexpr int i = decltype(II)::value;
-      *reinterpret_cast<i32x4 *>(&As[buf][alds[i]]) = ra[s][i];
+      *reinterpret_cast<i32x4 *>(&As[buf][alds[i]]) = select16(akeep[s][i], ra[s][i]);
     });
   };
 
@@ -1649,9 +1654,13 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgsK<RCAP> args
     constexpr int nxt = (h + 1) % S, buf = h & 1, nl = (h & 1) ? NLO : NLE;
     // odd steps overwrite this step's A region: this wave's reads of it (the
     // A fragments read during the previous step, each followed by at least
-    // LAFTER B reads in issue order) must have completed before the barrier;
-    // LDS reads complete in order and the loop issues no scalar loads, so
-    // lgkmcnt(LAFTER) suffices and the trailing B reads stay in flight
+    // LAFTER B reads in issue order) must have completed before the barrier.
+    // LDS reads complete in order, so lgkmcnt(LAFTER) suffices and the
+    // trailing B reads stay in flight.  Other LGKM-counted operations (scalar
+    // loads, which may complete out of order) can only make this wait
+    // stricter: while any is outstanding it counts toward LAFTER, so fewer
+    // LDS reads are left in flight, never more (and the compiled loop issues
+    // none).
     constexpr int LAFTER = RCAP * NJ - MI;
     static_assert(LAFTER >= 0 && LAFTER < 16, "lgkmcnt is 4 bits");
     if constexpr (h & 1) __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (LAFTER << 8) | (0x3 << 14));
