@@ -584,11 +584,15 @@ __device__ __forceinline__ ColScale col_scale(const Epi<RCAP> &e, int col, int n
 // __fmul_rn / __fadd_rn are plain operators compiled with contraction on
 // in their own header, and after inlining the multiply and the add would
 // fuse into an FMA (one rounding instead of two).
+// Int64 outputs are written with non-temporal stores: the kernel never
+// reads them back, and streaming them past the L2 keeps the A and weight
+// lines the other tiles still read (C2 M=256 8.98 -> 8.72 us, C5 M=2048
+// about 1 % faster, measured A/B on one box).
 template <int RCAP, int OUT>
 __device__ __forceinline__ void store_value(const Epi<RCAP> &e, int64_t y, int64_t idx, ColScale cs) {
 #pragma clang fp contract(off)
   if (OUT == kOutInt64 || (OUT == kOutAny && e.out_dtype == RNSMX_INT64)) {
-    as_global<int64_t>(e.out)[idx] = y;
+    __builtin_nontemporal_store(y, &as_global<int64_t>(e.out)[idx]);
     return;
   }
   // with up to 4 channels |y| <= P/2 < 2^31: the 32-bit conversion rounds
