@@ -313,7 +313,7 @@ def measure_wide(backend, m, k, n, packed, steps, warmup, rotate_bytes, seed, de
 PMC_SHAPES = {
     "headline": [("C2", None, 768, 768, 3, 12)],
     "all": [("C2", 256, 768, 768, 3, 6), ("C3", 1, 768, 768, 1, 6), ("C5", 1, 4096, 4096, 3, 4),
-            ("C5", 2048, 4096, 4096, 3, 3)],
+            ("C5", 512, 4096, 4096, 3, 3), ("C5", 2048, 4096, 4096, 3, 3)],
 }
 
 
