@@ -236,9 +236,13 @@ int32_t rnsmx_matmul_prepared_fused(
  * rnsmx_matmul_prepared_fused without a workspace argument: the call uses a
  * library-owned static device array of RNSMX_NOALLOC_SCRATCH_BYTES per GPU
  * instead, and allocates nothing (no hipMalloc, no hipFree, no allocating
- * library call).  Same arguments, results and errors otherwise.  A call whose
- * scratch need (rnsmx_prepared_workspace_bytes for its shape and activation
- * type) exceeds the maximum fails with RNSMX_ESPACE before touching the GPU.
+ * library call).  Same arguments, results and errors otherwise.  With the
+ * automatic plan (plan NULL or kind 0) a K split whose exchange area does
+ * not fit the static scratch is dropped: the call then runs the automatic
+ * kernel unsplit (same results).  A call whose scratch need for the plan it
+ * runs still exceeds the maximum fails with RNSMX_ESPACE; that check, and
+ * those of the shape, moduli, activation type and plan, come before the
+ * GPU is touched.
  * The first call on each device resolves the array's address there and
  * clears its counters with one small kernel on `stream`; make that call
  * outside graph capture.  Every call on a GPU shares that GPU's array:
@@ -340,8 +344,12 @@ int32_t rnsmx_gemm_plan(int64_t m, int64_t n, int64_t k, int32_t channels,
  * RNSMX_QUANT_SCRATCH 32-bit words of per-block maxima passed from the
  * first launch to the second; its contents before a call do not matter,
  * and calls that share one scratch must not overlap (keep one per stream).
- * NaN inputs are not propagated (the reference's amax would propagate
- * them).
+ * Non-finite inputs follow the reference chain's float operations: a NaN
+ * anywhere makes the scale NaN (torch's amax propagates it) and an infinity
+ * (without NaN) makes it +inf; an element whose quotient x / scale is NaN
+ * quantizes to 0 (what the reference leaves to the float-to-integer cast),
+ * so the dequantized outputs of such a call are all NaN, as the reference's
+ * are.
  * Replaces RNSLinear._symmetric_scale + _quantize on activations
  * (src/rns_llm/layers/rns_linear.py:154-166, called at 249-250).
  */

@@ -952,16 +952,15 @@ struct QuantIn<Bf16Bits> {
 template <typename T>
 using QuantRaw = typename std::conditional<std::is_same<T, float>::value, float, uint16_t>::type;
 
-// Block-wide max of non-negative floats (256 threads).
-__device__ __forceinline__ float block_max256(float m, float *wmax) {
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
-  __syncthreads();
-  return fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+
+
+// max(a, b) that propagates NaN, as torch's amax does (fmaxf drops it).
+__device__ __forceinline__ float max_nan(float a, float b) {
+  return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
 }
 
-
-// max |x| over the elements this thread visits (tid, tid + stride, ...).
+// max |x| over the elements this thread visits (tid, tid + stride, ...);
+// NaN when any of them is NaN.
 template <typename T>
 __device__ __forceinline__ float quant_thread_amax(const QuantArgs &a, int64_t tid, int64_t stride) {
   using R = QuantRaw<T>;
@@ -969,13 +968,18 @@ __device__ __forceinline__ float quant_thread_amax(const QuantArgs &a, int64_t t
   const R *x = static_cast<const R *>(a.x);
   const int64_t nvec = a.vec ? a.count / V : 0;
   float m = 0.0f;
+  bool nan = false;
+  auto visit = [&](float v) {
+    m = fmaxf(m, fabsf(v));
+    nan |= v != v;
+  };
   for (int64_t i = tid; i < nvec; i += stride) {
     R v[V];
     *reinterpret_cast<uint4 *>(v) = reinterpret_cast<const uint4 *>(x)[i];
-    static_for<V>([&](auto E) { m = fmaxf(m, fabsf(QuantIn<T>::get(v[decltype(E)::value]))); });
+    static_for<V>([&](auto E) { visit(QuantIn<T>::get(v[decltype(E)::value])); });
   }
-  for (int64_t i = nvec * V + tid; i < a.count; i += stride) m = fmaxf(m, fabsf(QuantIn<T>::get(x[i])));
-  return m;
+  for (int64_t i = nvec * V + tid; i < a.count; i += stride) visit(QuantIn<T>::get(x[i]));
+  return nan ? __builtin_nanf("") : m;
 }
 
 // q = clamp(rint(x / s), -qmax, qmax) over the elements of (tid, stride).
@@ -985,8 +989,11 @@ __device__ __forceinline__ void quant_thread_apply(const QuantArgs &a, float s, 
   constexpr int V = 16 / sizeof(R);
   const R *x = static_cast<const R *>(a.x);
   Q *q = static_cast<Q *>(a.q);
+  // a NaN quotient (x NaN, s NaN, or x and s infinite) quantizes to 0, the
+  // value the hardware's float-to-integer conversion gives NaN
   auto quant = [&](R raw) {
-    return static_cast<Q>(fminf(fmaxf(rintf(QuantIn<T>::get(raw) / s), -a.qmax), a.qmax));
+    const float r = rintf(QuantIn<T>::get(raw) / s);
+    return static_cast<Q>(r != r ? 0.0f : fminf(fmaxf(r, -a.qmax), a.qmax));
   };
   const int64_t nvec = a.vec ? a.count / V : 0;
   for (int64_t i = tid; i < nvec; i += stride) {
@@ -1005,6 +1012,14 @@ __device__ __forceinline__ void quant_thread_apply(const QuantArgs &a, float s, 
   for (int64_t i = nvec * V + tid; i < a.count; i += stride) q[i] = quant(x[i]);
 }
 
+// Block-wide max of non-negative floats or NaN (256 threads; NaN wins).
+__device__ __forceinline__ float block_max256(float m, float *wmax) {
+  for (int off = 32; off > 0; off >>= 1) m = max_nan(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  return max_nan(max_nan(wmax[0], wmax[1]), max_nan(wmax[2], wmax[3]));
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void quant_amax_kernel(const QuantArgs a) {
   __shared__ float wmax[4];
@@ -1018,9 +1033,10 @@ template <typename T, typename Q>
 __global__ __launch_bounds__(256) void quant_apply_kernel(const QuantArgs a) {
   __shared__ float wmax[4];
   float t = 0.0f;
-  for (int b = threadIdx.x; b < a.nparts; b += blockDim.x) t = fmaxf(t, a.partial[b]);
+  for (int b = threadIdx.x; b < a.nparts; b += blockDim.x) t = max_nan(t, a.partial[b]);
   const float amax = block_max256(t, wmax);
-  const float s = fmaxf(amax * a.rcp, 1.1920928955078125e-07f);  // FLT_EPSILON
+  // clamp at FLT_EPSILON; NaN stays NaN (torch.clamp keeps it, fmaxf would not)
+  const float s = amax != amax ? amax : fmaxf(amax * a.rcp, 1.1920928955078125e-07f);
   if (blockIdx.x == 0 && threadIdx.x == 0) *a.scale = s;
   quant_thread_apply<T, Q>(a, s, static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x,
                            static_cast<int64_t>(gridDim.x) * blockDim.x);
@@ -1033,12 +1049,13 @@ template <typename T, typename Q>
 __global__ __launch_bounds__(1024) void quant_one_block_kernel(const QuantArgs a) {
   __shared__ float wmax[16];
   float m = quant_thread_amax<T>(a, threadIdx.x, blockDim.x);
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  for (int off = 32; off > 0; off >>= 1) m = max_nan(m, __shfl_xor(m, off, 64));
   if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
   __syncthreads();
   float amax = 0.0f;
-  for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) amax = fmaxf(amax, wmax[w]);
-  const float s = fmaxf(amax * a.rcp, 1.1920928955078125e-07f);  // FLT_EPSILON
+  for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) amax = max_nan(amax, wmax[w]);
+  // clamp at FLT_EPSILON; NaN stays NaN (torch.clamp keeps it, fmaxf would not)
+  const float s = amax != amax ? amax : fmaxf(amax * a.rcp, 1.1920928955078125e-07f);
   if (threadIdx.x == 0) *a.scale = s;
   quant_thread_apply<T, Q>(a, s, threadIdx.x, blockDim.x);
 }
@@ -1500,26 +1517,40 @@ int32_t rnsmx_matmul_prepared_fused_noalloc(const void *a_dev, int32_t a_dtype, 
                                             const rnsmx_plan_t *plan, void *out_dev, void *stream) {
   clear_error();
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (m > 0 && n > 0) {
-    // reject what cannot fit before touching the device
-    const int64_t need = rnsmx_prepared_workspace_bytes(m, k, n, mods ? mods->channels : 0, plan);
-    const bool raw = a_dtype == RNSMX_INT8 && k % 16 == 0;
-    const int64_t need_call =
-        mods && mods->channels >= 1 && mods->channels <= RNSMX_MAX_CHANNELS && k >= 1
-            ? prepared_need(raw && raw_accumulator_fits(*mods, k), m, k, n, mods->channels, plan)
-            : need;
-    if (need_call > RNSMX_NOALLOC_SCRATCH_BYTES) {
-      set_error("this call needs %lld bytes of scratch; the static scratch holds %lld (use "
-                "rnsmx_matmul_prepared_fused with a workspace)",
-                static_cast<long long>(need_call), static_cast<long long>(RNSMX_NOALLOC_SCRATCH_BYTES));
-      return RNSMX_ESPACE;
-    }
+  if (m == 0 || n == 0 || m < 0 || n < 0 || k < 1 || !mods || mods->channels < 1 ||
+      mods->channels > RNSMX_MAX_CHANNELS || dtype_size(a_dtype) == 0)
+    // nothing to launch, or an argument error: the workspace entry point
+    // returns it (an empty call, or the same status) without touching the GPU
+    return rnsmx_matmul_prepared_fused(a_dev, a_dtype, m, k, n, packed_dev, mods, lut_dev, lut_channels,
+                                       adaptive, epilogue, plan, nullptr, 0, out_dev, stream);
+  // The plan this call runs, checked on the host.  The automatic plan may
+  // split K over workgroups, whose exchange area can outgrow the static
+  // scratch where the same product unsplit fits (an LDS-kernel tail split
+  // at K = 4096, N = 12288 needs 16 MiB of exchange); it then runs unsplit.
+  const bool araw = a_dtype == RNSMX_INT8 && k % 16 == 0 && raw_accumulator_fits(*mods, k);
+  const GemmArgs g = plan_args(m, n, k, mods->channels, araw);
+  const int64_t kp = round_up(k, RNSMX_K_ALIGN);
+  GemmChoice c{};
+  if (int32_t rc = plan_from(plan, g, araw, true, c)) return rc;
+  rnsmx_plan_t own{};
+  const rnsmx_plan_t *run_plan = plan;
+  int64_t need = prepared_layout(araw, m, kp, mods->channels, xchg_bytes(c, g)).total;
+  if (need > RNSMX_NOALLOC_SCRATCH_BYTES && (plan == nullptr || plan->kind == kAuto)) {
+    c = auto_plan(g, araw, false);
+    own = rnsmx_plan_t{c.kind, c.mb, c.nb, c.ks, 1, 0};
+    run_plan = &own;
+    need = prepared_layout(araw, m, kp, mods->channels, 0).total;
+  }
+  if (need > RNSMX_NOALLOC_SCRATCH_BYTES) {
+    set_error("this call needs %lld bytes of scratch; the static scratch holds %lld (use "
+              "rnsmx_matmul_prepared_fused with a workspace)",
+              static_cast<long long>(need), static_cast<long long>(RNSMX_NOALLOC_SCRATCH_BYTES));
+    return RNSMX_ESPACE;
   }
   int8_t *ws = nullptr;
-  if (m > 0 && n > 0)
-    if (int32_t rc = static_scratch(st, &ws)) return rc;
+  if (int32_t rc = static_scratch(st, &ws)) return rc;
   return rnsmx_matmul_prepared_fused(a_dev, a_dtype, m, k, n, packed_dev, mods, lut_dev, lut_channels, adaptive,
-                                     epilogue, plan, ws, RNSMX_NOALLOC_SCRATCH_BYTES, out_dev, stream);
+                                     epilogue, run_plan, ws, RNSMX_NOALLOC_SCRATCH_BYTES, out_dev, stream);
 }
 
 int32_t rnsmx_matmul_residues_prepared(const int8_t *a_res_dev, int64_t a_ld, int32_t m, int32_t k,

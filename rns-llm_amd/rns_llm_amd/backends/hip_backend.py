@@ -530,31 +530,37 @@ class HipRNSBackend:
     # ------------------------------------------------------------------
     # Fused ops
     # ------------------------------------------------------------------
+    def _residue_operands(self, a_residues: torch.Tensor, b_residues: torch.Tensor,
+                          moduli: Iterable[int]) -> tuple[tuple[int, ...], int, int, int, int]:
+        """Checks a pair of centered residue planes a [R, M, K], b [R, K, N]
+        against each other and the moduli; returns (moduli, R, M, K, N)."""
+        for name, planes in (("a_residues", a_residues), ("b_residues", b_residues)):
+            self._validate_matrix(planes, name, 3)
+            if planes.dtype != torch.int8:
+                raise ValueError(f"{name} must hold centered int8 residues, not {planes.dtype}")
+        if a_residues.device != b_residues.device:
+            raise ValueError(f"a_residues is on {a_residues.device}, b_residues on {b_residues.device}")
+        (ra, m, k), (rb, kb, n) = a_residues.shape, b_residues.shape
+        if ra != rb or k != kb:
+            raise ValueError(f"residue planes [{ra}, {m}, {k}] x [{rb}, {kb}, {n}] do not chain "
+                             "(channels and K must agree)")
+        mods = validate_moduli(moduli)
+        if len(mods) != ra:
+            raise ValueError(f"{len(mods)} moduli for {ra} residue channels")
+        return mods, int(ra), int(m), int(k), int(n)
+
     def matmul_centered_fused(self, a_residues: torch.Tensor, b_residues: torch.Tensor,
                               moduli: Iterable[int], *, lut_channels: int = 0,
                               workspace: RNSWorkspace | None = None) -> torch.Tensor:
         """Residue planes a [R, M, K] and b [R, K, N] -> exact int64 [M, N]
         (``cuda_backend.py:398-459``).  Returns ``workspace.output``."""
-        self._validate_matrix(a_residues, "a_residues", 3)
-        self._validate_matrix(b_residues, "b_residues", 3)
-        if a_residues.dtype != torch.int8 or b_residues.dtype != torch.int8:
-            raise ValueError("fused path expects centered int8 residue planes")
-        if a_residues.device != b_residues.device:
-            raise ValueError("inputs must share device")
-        if (a_residues.shape[0] != b_residues.shape[0]
-                or a_residues.shape[2] != b_residues.shape[1]):
-            raise ValueError("R/K dimensions do not match")
+        mods, channels, m, k, n = self._residue_operands(a_residues, b_residues, moduli)
         if lut_channels not in (0, 1, 2):
-            raise ValueError("lut_channels must be 0, 1 or 2")
-        mods = validate_moduli(moduli)
-        channels, m, k = map(int, a_residues.shape)
-        n = int(b_residues.shape[2])
-        if channels != len(mods):
-            raise ValueError("moduli count does not match channels")
-        if not self.mfma_compatible(k=k, n=n, moduli=mods, device=a_residues.device):
-            raise ValueError("fused path requires an MFMA-compatible shape (2..10 channels, "
-                             "int32-safe K)")
+            raise ValueError(f"lut_channels is {lut_channels}; the table serves 0, 1 or 2 channels")
         device = a_residues.device
+        if not self.mfma_compatible(k=k, n=n, moduli=mods, device=device):
+            raise ValueError(f"no fused kernel for K={k} with moduli {mods}: 2..10 channels and "
+                             "K * max(m // 2)^2 within int32 are required")
         if workspace is None:
             workspace = self.create_workspace(device=device, channels=channels, m=m, n=n)
         self._check_workspace(workspace, channels=channels, m=m, n=n, device=device)
@@ -576,21 +582,8 @@ class HipRNSBackend:
         the same residue in every channel as the per-channel modular GEMM
         (CRT reconstruction preserves residues), so this is the fused product
         re-encoded."""
-        self._validate_matrix(a_residues, "a_residues", 3)
-        self._validate_matrix(b_residues, "b_residues", 3)
-        if a_residues.dtype != torch.int8 or b_residues.dtype != torch.int8:
-            raise ValueError("centered residue matrices must use torch.int8")
-        if a_residues.device != b_residues.device:
-            raise ValueError("a_residues and b_residues must share a device")
-        if a_residues.shape[0] != b_residues.shape[0]:
-            raise ValueError("channel counts do not match")
-        if a_residues.shape[2] != b_residues.shape[1]:
-            raise ValueError("K dimensions do not match")
-        mods = validate_moduli(moduli)
-        if len(mods) != a_residues.shape[0]:
-            raise ValueError("moduli count does not match residue channels")
-        self.select_centered_kernel(k=int(a_residues.shape[2]), n=int(b_residues.shape[2]),
-                                    moduli=mods, requested=kernel, device=a_residues.device)
+        mods, _, _, k, n = self._residue_operands(a_residues, b_residues, moduli)
+        self.select_centered_kernel(k=k, n=n, moduli=mods, requested=kernel, device=a_residues.device)
         exact = self.matmul_centered_fused(a_residues, b_residues, mods).clone()
         return self._encode_int64_centered(exact, mods)
 
@@ -881,19 +874,22 @@ class HipRNSBackend:
                                             packed=storage, absmax=full.absmax, form=full.form)
         return PreparedAdaptiveRNSWeight(variants, full.moduli, full.absmax, min_channels)
 
-    def select_adaptive_variant(self, a: torch.Tensor, prepared: PreparedAdaptiveRNSWeight):
-        """Host-side selection with the reference's synchronising bound
-        (``cuda_backend.py:577-600``); the fused adaptive call does not use
-        it."""
+    def _host_row_bound(self, a: torch.Tensor, max_abs_weight: int) -> int:
+        """max_i sum_k |a_ik| * max|B|, read on the host (one synchronisation)."""
         self._validate_matrix(a, "a", 2)
         if a.dtype not in (torch.int8, torch.int16, torch.int32):
-            raise ValueError("a must be int8/int16/int32")
-        max_row_l1 = int(a.to(torch.int64).abs().sum(dim=1).max().item()) if a.numel() else 0
-        bound = safe_l1_dot_bound(max_row_l1, prepared.max_abs_weight)
-        channels = minimal_prefix_channels(prepared.full_moduli, bound,
-                                           min_channels=prepared.min_channels)
-        self._stats["adaptive_selections"] += 1
-        self._stats[f"adaptive_channels_{channels}"] += 1
+            raise ValueError(f"a must be an int8, int16 or int32 matrix, not {a.dtype}")
+        row_l1 = a.to(torch.int64).abs().sum(dim=1)
+        return safe_l1_dot_bound(int(row_l1.max()) if row_l1.numel() else 0, max_abs_weight)
+
+    def select_adaptive_variant(self, a: torch.Tensor, prepared: PreparedAdaptiveRNSWeight):
+        """Host-side selection with the reference's synchronising bound
+        (``cuda_backend.py:577-600``): (variant, bound).  The device path of
+        the fused adaptive call does not use it."""
+        bound = self._host_row_bound(a, prepared.max_abs_weight)
+        channels = minimal_prefix_channels(prepared.full_moduli, bound, min_channels=prepared.min_channels)
+        for key in ("adaptive_selections", f"adaptive_channels_{channels}"):
+            self._stats[key] += 1
         return prepared.variants[channels], bound
 
     def matmul_prepared_adaptive_fused(self, a: torch.Tensor, prepared: PreparedAdaptiveRNSWeight,
@@ -992,44 +988,44 @@ class HipRNSBackend:
         return tuple(v.clone() for v in views) if clone_outputs else views
 
     # ------------------------------------------------------------------
-    # Convenience wrappers (cuda_backend.py:733-799)
+    # Convenience wrappers (cuda_backend.py:733-799): both integer operands
+    # encoded here, then a residue-domain entry point
     # ------------------------------------------------------------------
-    def matmul_wide(self, a: torch.Tensor, b: torch.Tensor, moduli: Iterable[int], *,
-                    decode: bool = True, kernel: str = "auto") -> torch.Tensor:
+    def _encode_operands(self, a: torch.Tensor, b: torch.Tensor, moduli: Iterable[int]):
+        """Centered residue planes of an integer pair a [M, K], b [K, N] of
+        one dtype: (a_res, b_res, moduli)."""
         self._validate_matrix(a, "a", 2)
         self._validate_matrix(b, "b", 2)
         if a.dtype not in (torch.int8, torch.int16, torch.int32):
-            raise ValueError("a must be int8/int16/int32")
+            raise ValueError(f"a must be an int8, int16 or int32 matrix, not {a.dtype}")
         if b.dtype != a.dtype:
-            raise ValueError("a and b must use the same integer dtype")
+            raise ValueError(f"a is {a.dtype} but b is {b.dtype}; both need the same integer type")
         if a.shape[1] != b.shape[0]:
-            raise ValueError("K dimensions do not match")
+            raise ValueError(f"a {tuple(a.shape)} and b {tuple(b.shape)} do not chain over K")
         mods = validate_moduli(moduli)
-        a_res = self.encode_centered(a, mods)
-        b_res = self.encode_centered(b, mods)
-        if decode:
-            return self.matmul_centered_fused(a_res, b_res, mods).clone()
-        return self.matmul_centered_residues(a_res, b_res, mods, kernel=kernel)
+        return self.encode_centered(a, mods), self.encode_centered(b, mods), mods
+
+    def matmul_wide(self, a: torch.Tensor, b: torch.Tensor, moduli: Iterable[int], *,
+                    decode: bool = True, kernel: str = "auto") -> torch.Tensor:
+        """Exact a @ b as int64 (decode) or its centered residues [R, M, N]."""
+        a_res, b_res, mods = self._encode_operands(a, b, moduli)
+        if not decode:
+            return self.matmul_centered_residues(a_res, b_res, mods, kernel=kernel)
+        return self.matmul_centered_fused(a_res, b_res, mods).clone()
 
     def matmul_wide_fused(self, a: torch.Tensor, b: torch.Tensor, moduli: Iterable[int], *,
                           lut_channels: int = 0,
                           workspace: RNSWorkspace | None = None) -> torch.Tensor:
-        self._validate_matrix(a, "a", 2)
-        self._validate_matrix(b, "b", 2)
-        if a.dtype not in (torch.int8, torch.int16, torch.int32):
-            raise ValueError("a must be int8/int16/int32")
-        if b.dtype != a.dtype or a.shape[1] != b.shape[0]:
-            raise ValueError("dtype/K mismatch")
-        mods = validate_moduli(moduli)
-        a_res = self.encode_centered(a, mods)
-        b_res = self.encode_centered(b, mods)
-        return self.matmul_centered_fused(a_res, b_res, mods, lut_channels=lut_channels,
-                                          workspace=workspace)
+        """Exact a @ b into ``workspace.output`` (aliasing it, like
+        ``matmul_centered_fused``)."""
+        a_res, b_res, mods = self._encode_operands(a, b, moduli)
+        return self.matmul_centered_fused(a_res, b_res, mods, lut_channels=lut_channels, workspace=workspace)
 
     def matmul_int8(self, a: torch.Tensor, b: torch.Tensor, moduli: Iterable[int], *,
                     decode: bool = True, kernel: str = "auto") -> torch.Tensor:
-        if a.dtype != torch.int8 or b.dtype != torch.int8:
-            raise ValueError("matmul_int8 expects int8 inputs")
+        """``matmul_wide`` restricted to int8 operands."""
+        if torch.int8 != a.dtype or torch.int8 != b.dtype:
+            raise ValueError(f"matmul_int8 takes int8 operands, got {a.dtype} and {b.dtype}")
         return self.matmul_wide(a, b, moduli, decode=decode, kernel=kernel)
 
 

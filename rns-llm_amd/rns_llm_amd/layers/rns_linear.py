@@ -217,11 +217,13 @@ class RNSLinear(nn.Module):
         self._linear_key = None
 
     def _live_key(self):
-        """What the bound one-call forward depends on: the weight version and
-        the identity of the bias values (their float32 copy is bound)."""
+        """What the bound one-call forward depends on: the weight version, the
+        identity of the bias values (their float32 copy is bound) and the
+        switches that choose the path (a change re-binds or unbinds it)."""
         bias = self.bias
         return (self.weight._version,
-                None if bias is None else (bias.data_ptr(), bias._version, bias.dtype))
+                None if bias is None else (bias.data_ptr(), bias._version, bias.dtype),
+                self.fused, self.fused_epilogue, self.adaptive_channels)
 
     def _bind_linear(self):
         """The backend's one-call forward for the current weight and bias
@@ -261,7 +263,8 @@ class RNSLinear(nn.Module):
     def forward(self, inputs: torch.Tensor) -> torch.Tensor:
         call = self._linear_call
         if (call is not None and self.mode == "rns" and not self.training and inputs.is_cuda
-                and inputs.dtype in _FLOAT_OUT and self._linear_key == self._live_key()):
+                and inputs.dtype in _FLOAT_OUT and inputs.dim() > 0
+                and inputs.shape[-1] == self.in_features and self._linear_key == self._live_key()):
             # prepared weight, unchanged since the call was bound: one library
             # call (quantize, GEMM, dequant epilogue) into a fresh output
             x = inputs if inputs.is_contiguous() else inputs.contiguous()
@@ -285,6 +288,12 @@ class RNSLinear(nn.Module):
         if self.backend is None:
             raise RuntimeError("RNSLinear mode='rns' requires a backend")
 
+        if inputs.dim() == 0 or inputs.shape[-1] != self.in_features:
+            # the reference's flatten-and-restore fails on such inputs (its
+            # final reshape to (*inputs.shape[:-1], out_features) cannot hold
+            # the product's rows); here it fails before anything is computed
+            raise RuntimeError(
+                f"RNSLinear expects inputs of shape (*, {self.in_features}), got {tuple(inputs.shape)}")
         self.prepare_weight()
         original_shape = inputs.shape[:-1]
         flat = inputs.reshape(-1, self.in_features)

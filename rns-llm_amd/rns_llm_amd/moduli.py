@@ -10,6 +10,7 @@ reciprocals, Garner coefficients, prefix products) are built natively by
 """
 from __future__ import annotations
 
+from itertools import accumulate, combinations
 from math import gcd, prod
 from typing import Iterable
 
@@ -37,15 +38,17 @@ _STRATEGIES = {
 
 
 def validate_moduli(moduli: Iterable[int]) -> tuple[int, ...]:
-    mods = tuple(int(m) for m in moduli)
-    if not mods:
-        raise ValueError("moduli must not be empty")
-    if any(not 2 <= m <= 255 for m in mods):
-        raise ValueError("every modulus must be in [2, 255]")
-    for i, left in enumerate(mods):
-        for right in mods[i + 1:]:
-            if gcd(left, right) != 1:
-                raise ValueError(f"moduli are not pairwise coprime: {left}, {right}")
+    """The moduli as a tuple of ints, each in [2, 255] (one residue byte) and
+    coprime to every other; ValueError otherwise."""
+    mods = tuple(map(int, moduli))
+    if len(mods) == 0:
+        raise ValueError("an RNS needs at least one modulus")
+    out_of_range = [m for m in mods if m < 2 or m > 255]
+    if out_of_range:
+        raise ValueError(f"moduli must lie in [2, 255] (residues are bytes): {out_of_range}")
+    shared = next(((x, y) for x, y in combinations(mods, 2) if gcd(x, y) > 1), None)
+    if shared is not None:
+        raise ValueError(f"moduli {shared[0]} and {shared[1]} share a factor; they must be pairwise coprime")
     return mods
 
 
@@ -85,29 +88,35 @@ def choose_moduli_for_dot(k: int, max_abs_a: int, max_abs_b: int, *,
 
 
 def signed_capacity(moduli: Iterable[int]) -> int:
+    """Largest |x| the centered range of the moduli set holds: (P - 1) // 2."""
     return (prod(validate_moduli(moduli)) - 1) // 2
 
 
 def minimal_prefix_channels(moduli: Iterable[int], absolute_bound: int, *,
                             min_channels: int = 2) -> int:
+    """Length of the shortest prefix, at least ``min_channels`` long, whose
+    product P_c holds every value of magnitude up to ``absolute_bound``
+    exactly (strictly: 2 * bound < P_c); OverflowError when the whole set
+    does not."""
     mods = validate_moduli(moduli)
     if absolute_bound < 0:
-        raise ValueError("absolute_bound must be non-negative")
-    if not 2 <= min_channels <= len(mods):
-        raise ValueError("min_channels must be between 2 and len(moduli)")
-    running = 1
-    for count, m in enumerate(mods, start=1):
-        running *= m
-        if count >= min_channels and 2 * absolute_bound < running:
-            return count
+        raise ValueError("absolute_bound cannot be negative")
+    if min_channels < 2 or min_channels > len(mods):
+        raise ValueError(f"min_channels must be in [2, {len(mods)}]")
+    products = list(accumulate(mods, lambda p, m: p * m))
+    for c in range(min_channels, len(mods) + 1):
+        if products[c - 1] > 2 * absolute_bound:
+            return c
     raise OverflowError(
-        f"full moduli set cannot represent bound {absolute_bound}; "
-        f"capacity={signed_capacity(mods)}")
+        f"bound {absolute_bound} exceeds what the full moduli set represents "
+        f"(capacity={signed_capacity(mods)})")
 
 
 def safe_l1_dot_bound(max_row_l1: int, max_abs_weight: int) -> int:
-    if max_row_l1 < 0 or max_abs_weight < 0:
-        raise ValueError("bounds must be non-negative")
+    """|sum_k a_k b_k| <= (sum_k |a_k|) * max|b|: the bound the adaptive
+    prefix must hold."""
+    if min(max_row_l1, max_abs_weight) < 0:
+        raise ValueError("max_row_l1 and max_abs_weight cannot be negative")
     return int(max_row_l1) * int(max_abs_weight)
 
 

@@ -459,6 +459,34 @@ def test_rnslinear_weight_version_invalidates_cache(backend):
     assert torch.equal(y.cpu(), want)
 
 
+def test_rnslinear_rejects_misshaped_inputs_before_and_after_binding(backend):
+    # the reference's flatten-and-restore raises RuntimeError on every input
+    # whose last dimension is not in_features; here that holds on the first
+    # call and on calls after the one-call forward is bound, and the bad call
+    # writes nothing
+    torch.manual_seed(5)
+    lin = nn.Linear(4, 8, device=DEV).eval()
+    layer = RNSLinear.from_linear(lin, backend=backend, mode="rns").eval()
+    bad = [torch.randn(2, 8, device=DEV), torch.randn(3, 2, device=DEV), torch.randn(5, 3, device=DEV),
+           torch.randn((), device=DEV)]
+    for x in bad:  # nothing bound yet
+        with pytest.raises(RuntimeError):
+            layer(x)
+    good = torch.randn(3, 4, device=DEV)
+    y = layer(good)  # binds the one-call path
+    assert layer._linear_call is not None
+    for x in bad:
+        with pytest.raises(RuntimeError):
+            layer(x)
+    want, _ = linear_oracle.linear_forward(good.cpu(), layer.weight.detach().cpu(), layer.bias.detach().cpu())
+    assert torch.equal(y.cpu(), want)
+    assert torch.equal(layer(good).cpu(), want)
+    # a switch of the path's options re-binds (or unbinds) the one-call path
+    layer.fused_epilogue = False
+    assert torch.equal(layer(good).cpu(), want)
+    assert layer._linear_call is None
+
+
 # ---------------------------------------------------------------------------
 # activation quantization (RNSLinear._symmetric_scale / _quantize)
 # ---------------------------------------------------------------------------
@@ -530,3 +558,50 @@ def test_quantize_symmetric_validation(backend):
         backend.quantize_symmetric(torch.ones(4, 4, dtype=torch.int8, device=DEV))
     with pytest.raises(ValueError):
         backend.quantize_symmetric(torch.ones(4, 4, device=DEV), quant_bits=7)
+
+
+@pytest.mark.parametrize("count", [37, 4096, 70_000])  # one-workgroup and two-launch forms
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_quantize_symmetric_non_finite(backend, count, dtype):
+    """Non-finite activations: the scale is what the reference chain's float
+    ops give (torch's amax propagates NaN, clamp keeps it; an infinity makes
+    it +inf), and every element whose quotient is NaN quantizes to 0, so a
+    dequantized output is all NaN, as the reference's is."""
+    eps = torch.finfo(torch.float32).eps
+    gen = torch.Generator().manual_seed(count)
+    base = torch.randn(count, generator=gen).to(dtype)
+    cases = {"nan": (float("nan"), None), "inf": (float("inf"), None), "-inf": (float("-inf"), None),
+             "nan+inf": (float("nan"), float("inf"))}
+    for name, (v0, v1) in cases.items():
+        x = base.clone()
+        x[count // 3] = v0
+        if v1 is not None:
+            x[count // 2] = v1
+        xg = x.to(DEV)
+        q, s = backend.quantize_symmetric(xg, 8)
+        s_ref = torch.clamp(xg.float().abs().amax() / 127.0, min=eps)  # the reference's scale, on the GPU
+        if name.startswith("nan"):
+            assert torch.isnan(s).all() and torch.isnan(s_ref).all(), name
+            assert int(q.abs().sum()) == 0, name  # every quotient is NaN
+        else:
+            assert torch.equal(s.reshape(-1).cpu(), s_ref.reshape(-1).cpu()) and torch.isinf(s).all(), name
+            # finite / inf = 0; inf / inf = NaN -> 0
+            assert int(q.abs().sum()) == 0, name
+    # finite inputs are unchanged by the NaN handling
+    q, s = backend.quantize_symmetric(base.to(DEV), 8)
+    s_or = linear_oracle.symmetric_scale(base.float(), 8)
+    assert torch.equal(s.reshape(-1).cpu().view(torch.int32), s_or.reshape(-1).view(torch.int32))
+    assert torch.equal(q.cpu(), linear_oracle.quantize(base.float(), s_or, 8))
+
+
+def test_rnslinear_nan_input_gives_nan_output(backend):
+    # the reference: scale NaN -> every output int * NaN * s_w + b = NaN
+    torch.manual_seed(6)
+    lin = nn.Linear(64, 32, device=DEV).eval()
+    layer = RNSLinear.from_linear(lin, backend=backend, mode="rns").eval()
+    x = torch.randn(4, 64, device=DEV)
+    x[1, 7] = float("nan")
+    for _ in range(2):  # first call (unbound) and the bound one-call path
+        assert torch.isnan(layer(x)).all()
+    x[1, 7] = float("inf")
+    assert torch.isnan(layer(x)).all()  # 0 * inf

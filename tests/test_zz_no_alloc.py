@@ -45,6 +45,32 @@ def test_noalloc_matches_workspace_entry_on_two_calls(backend):
         assert torch.equal(out.double(), a.double() @ w.double().t())
 
 
+def test_noalloc_drops_a_split_that_does_not_fit(backend):
+    # C5 M=512 with int8 activations: the automatic plan is the LDS kernel's
+    # tail split, whose exchange area alone is 16 MiB; unsplit the call needs
+    # a few KB, so the no-allocation entry point runs it unsplit
+    m, k, n = 512, 4096, 12288
+    auto = _native.Plan()
+    _native.check(backend._lib.rnsmx_gemm_plan(m, n, k, 4, 1, ctypes.byref(auto)))
+    need_auto = backend._lib.rnsmx_prepared_workspace_bytes(m, k, n, 4, None)
+    gen = torch.Generator(device=DEV).manual_seed(91)
+    w = torch.randint(-127, 128, (n, k), generator=gen, device=DEV, dtype=torch.int8)
+    a = torch.randint(-127, 128, (m, k), generator=gen, device=DEV, dtype=torch.int8)
+    prepared = backend.prepare_weight_nk(w, DENSE4)
+    want = backend.matmul_prepared_fused(a, prepared).clone()
+    for mm in (m, 300):  # the second call smaller
+        out = torch.full((mm, n), -1, dtype=torch.int64, device=DEV)
+        _native.check(noalloc_call(backend, a[:mm].contiguous(), prepared, out))
+        torch.cuda.synchronize()
+        assert torch.equal(out, want[:mm])
+    # the case is the one described: the automatic plan splits and needs more
+    # than the static scratch
+    assert auto.splits > 1 and need_auto > 16 << 20
+    rows = torch.arange(0, m, 37, device=DEV)
+    exact = a[rows].double() @ w.double().t()
+    assert torch.equal(want[rows].double(), exact)
+
+
 def test_noalloc_rejects_oversize_without_launch(backend):
     # int16 activations need R * M * kp bytes of residue planes: 4 * 8192 *
     # 1024 = 32 MiB > 16 MiB
