@@ -85,7 +85,8 @@ typedef struct rnsmx_moduli {
  * capacity, K a multiple of 256; mb, nb, ks ignored), 4 = the stream kernel
  * loading chunks of up to 8 K steps per wave (16 x 16 tiles, up to 4
  * channels), 5 = the MFMA kernel with three column waves (tile 16*mb x
- * 48*nb; int8 activations read in place, up to 4 channels).
+ * 48*nb; int8 activations read in place, up to 4 channels), 7 = the
+ * LDS-staged kernel with 256 x 96 tiles (same conditions as 3).
  * splits: workgroups splitting K per output tile (0 or 1 = none; up to 4
  * channels, and for the stream kernel ks = 1): each reduces its partial
  * sums to residues, and the last to finish a tile reconstructs it.  tail:

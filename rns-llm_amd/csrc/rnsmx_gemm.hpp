@@ -132,7 +132,8 @@ inline GemmArgsK<RCAP> compact_args(const GemmArgs &g) {
 // kStreamWide: the stream kernel with chunks of up to 8 K steps (long K).
 // kMfma3: the MFMA kernel with three column waves (48*nb-column tiles).
 // kRows: packed weights at decode (rows_packed_kernel: MFMA rows are channels).
-enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kLds = 3, kStreamWide = 4, kMfma3 = 5, kRows = 6 };
+// kLdsWide: the LDS-staged kernel with 256 x 96 tiles (lds_wide_kernel).
+enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kLds = 3, kStreamWide = 4, kMfma3 = 5, kRows = 6, kLdsWide = 7 };
 
 // ks: waves splitting K (stream kernel) or ring depth, 0 = automatic (MFMA
 // kernel); splits: workgroups splitting K (1 = none); tail: only the tiles
@@ -161,7 +162,7 @@ constexpr int kGemmParts = 6;
 inline int gemm_part_of(const GemmChoice &c, bool araw, bool packed = false) {
   if (packed) return 5;
   if (c.kind == kStream || c.kind == kStreamWide) return 0;
-  if (c.kind == kLds) return 4;
+  if (c.kind == kLds || c.kind == kLdsWide) return 4;
   if (!araw) return 3;
   return c.nb == 1 ? 1 : 2;
 }
@@ -662,6 +663,39 @@ __device__ __forceinline__ void with_epilogue(const Epi<RCAP> &e, int c_act, F &
 // offset with a quarter-rate vector multiply-add), and a tile that lies
 // wholly inside the output (nearly every tile) runs a copy of the loop with
 // no per-element bounds test.
+// The lane's value exchanged with its neighbour (lane ^ 1), by DPP.
+__device__ __forceinline__ int64_t swap_adjacent(int64_t v) {
+  constexpr int kQuadSwap = 0xB1;  // quad_perm [1, 0, 3, 2]
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), kQuadSwap, 0xF, 0xF, false));
+  const uint32_t hi =
+      static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v >> 32), kQuadSwap, 0xF, 0xF, false));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Int64 outputs of one 16 x 16 block whose four rows per lane are y[0..3]
+// (rows 4 (lane >> 4) + t of column lane & 15), written two columns per
+// lane: neighbouring lanes swap half their values, so the even lane holds
+// rows t = 0 and 2 and the odd lane rows 1 and 3, each at the two columns
+// (lane & 14), (lane & 14) + 1 — one 16-byte store per row.  Half the store
+// instructions of one store per element: the output writes are bound by the
+// store instructions a CU has in flight, not by their bytes.  `at` points to
+// the element (4 (lane >> 4), lane & 14) of the block; ld is even and `at`
+// 16-byte aligned.
+__device__ __forceinline__ void store_int64_pairs(const int64_t (&y)[4], gptr<int64_t> at, int64_t ld) {
+  typedef int64_t i64x2 __attribute__((ext_vector_type(2)));
+  const bool odd = (threadIdx.x & 1) != 0;
+  const int64_t ra = swap_adjacent(odd ? y[0] : y[1]);
+  const int64_t rb = swap_adjacent(odd ? y[2] : y[3]);
+  i64x2 v0, v1;
+  v0.x = odd ? ra : y[0];
+  v0.y = odd ? y[1] : ra;
+  v1.x = odd ? rb : y[2];
+  v1.y = odd ? y[3] : rb;
+  gptr<int64_t> p = at + (odd ? ld : 0);
+  __builtin_nontemporal_store(v0, reinterpret_cast<__attribute__((address_space(1))) i64x2 *>(p));
+  __builtin_nontemporal_store(v1, reinterpret_cast<__attribute__((address_space(1))) i64x2 *>(p + 2 * ld));
+}
+
 template <int RCAP, int MI, int NJ>
 __device__ __forceinline__ void register_epilogue(KArgs<RCAP> &g, const Epi<RCAP> &e, int c_act,
                                                   const i32x4 (&acc)[RCAP][MI][NJ], int r0, int c0,
@@ -669,6 +703,29 @@ __device__ __forceinline__ void register_epilogue(KArgs<RCAP> &g, const Epi<RCAP
   const int lane = threadIdx.x & 63;
   const int64_t idx0 = static_cast<int64_t>(r0 + 4 * (lane >> 4)) * e.out_ld + c0 + (lane & 15);
   const bool interior = r0 + 16 * MI <= m_lim && c0 + 16 * NJ <= n_lim;
+  // int64 interior tiles with 16-byte aligned rows: two columns per store
+  const bool pairs = interior && e.out_dtype == RNSMX_INT64 && c_act == RCAP && (e.out_ld & 1) == 0 &&
+                     (reinterpret_cast<uintptr_t>(e.out) & 15) == 0 && (c0 & 1) == 0;
+  if (pairs) {
+    const int64_t pidx0 = static_cast<int64_t>(r0 + 4 * (lane >> 4)) * e.out_ld + c0 + (lane & 14);
+    static_for<MI>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      int64_t roff = i * 16 * e.out_ld;
+      pin_sgpr(roff);
+      static_for<NJ>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        int64_t y[4];
+        static_for<4>([&](auto T) {
+          constexpr int t = decltype(T)::value;
+          int32_t v[RCAP];
+          static_for<RCAP>([&](auto C) { v[decltype(C)::value] = acc[decltype(C)::value][i][j][t]; });
+          y[t] = garner_from_sums<RCAP>(e, v, RCAP);
+        });
+        store_int64_pairs(y, as_global<int64_t>(e.out) + pidx0 + roff + j * 16, e.out_ld);
+      });
+    });
+    return;
+  }
   auto run = [&](auto FAST, auto OUT, auto INTERIOR) {
     static_for<MI>([&](auto I) {
       constexpr int i = decltype(I)::value;
@@ -915,6 +972,32 @@ __device__ __forceinline__ bool split_exchange(KArgs<RCAP> &g, const Epi<RCAP> &
   // read G splits at a time, every load of a group issued before the first
   // is used (own split and splits past S read a valid slot and are masked).
   asm volatile("" ::: "memory");
+  if constexpr (CH > 8) {
+    // large wave tiles (192 accumulators): one row of NJ chunks in flight,
+    // so the loads need few registers next to the accumulators
+    for (int s = 0; s < S; ++s) {
+      if (s == split) continue;
+      static_for<MI>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        i32x4 w[NJ];
+        static_for<NJ>([&](auto J) {
+          w[J] = load_coherent(base + (static_cast<int64_t>(s) * CH + i * NJ + decltype(J)::value) * 1024);
+        });
+        static_for<NJ>([&](auto J) {
+          constexpr int j = decltype(J)::value;
+          static_for<4>([&](auto T) {
+            constexpr int t = decltype(T)::value;
+            static_for<RCAP>([&](auto C) {
+              constexpr int c = decltype(C)::value;
+              acc[c][i][j][t] += static_cast<int32_t>(byte_of(static_cast<uint32_t>(w[j][t]), c));
+            });
+          });
+        });
+      });
+    }
+    if (lane == 0) __hip_atomic_store(g.tickets + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+  }
   constexpr int G = CH >= 4 ? 1 : 4 / CH;  // at most 4 chunks (16 registers) in flight, or one split
   for (int s0 = 0; s0 < S; s0 += G) {
     i32x4 w[G][MI][NJ];
@@ -1782,6 +1865,238 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgsK<RCAP> args
 }
 
 // ---------------------------------------------------------------------------
+// Wide LDS-staged GEMM: 256 x 96 tiles, 4 channels, 8 waves (4 x 2, each
+// 64 x 48 x 4 channels: 192 accumulator registers), four 40 KB stages (all
+// of the CU's 160 KB of LDS).  Against the 256 x 64 tile it stages 25 %
+// fewer bytes per MFMA, and its tile count fits the chip better on the
+// OPT-6.7B projection: N = 12288 is 128 tiles wide, so M = 512 is exactly
+// one round of 256 workgroups (the 64-column tile needs 1.5 rounds) and
+// M = 2048 four rounds (against six).
+//
+// The register file holds the accumulators only with single-buffered
+// fragments, so the schedule differs from lds_kernel's:
+//  * the B fragments of one channel are read while the MFMAs of the
+//    channel before run (two buffers of NJ fragments, alternating), and
+//    those of the next step's first channel during the last channel;
+//  * the A fragments of the next step are read one by one during the last
+//    channel's MFMAs, each right after the last MFMA that uses it (that
+//    channel runs row by row);
+//  * A pairs of K steps are loaded at even steps, two steps ahead, into the
+//    stage pair of the previous two steps: every wave has finished those
+//    steps' MFMAs (and so their fragment reads) at the barrier that starts
+//    the step, so no wave waits for its LDS reads before a barrier.  B is
+//    loaded three steps ahead as before.  Per step a wave waits only for
+//    the loads that the next step needs (vmcnt BU: the last step's B loads
+//    may stay in flight).
+// CA: channels computed (the adaptive prefix, fixed per launch: the MFMAs
+// and fragment reads of channels past it are not issued at all; their B
+// loads re-read channel 0's plane so every wave issues the same loads).
+// ---------------------------------------------------------------------------
+constexpr int kLdsWBN = 96;
+
+template <int RCAP, int CA>
+__device__ __forceinline__ void lds_wide_body(KArgs<RCAP> &g, int8_t *smem, const int c_act, const WorkUnit wu) {
+  static_assert(RCAP == 4 && CA >= 1 && CA <= RCAP, "4-channel capacity");
+  constexpr int NW = 8, S = kLdsStages, BN = kLdsWBN;
+  constexpr int AF = kLdsBM / 16;             // A fragments per stage
+  constexpr int NB = BN / 16;                 // column blocks of the tile
+  constexpr int BF = RCAP * NB;               // B fragments per stage
+  constexpr int ASTAGE = AF * 1024, BSTAGE = BF * 1024;
+  constexpr int BAREA = S * ASTAGE;           // the B stages follow the four A stages
+  constexpr int WN = 2, WM = NW / WN;         // wave grid
+  constexpr int MI = AF / WM, NJ = NB / WN;   // a wave's fragments: 4 x 3
+  constexpr int BU = BF / NW;                 // B loads per wave per step
+  constexpr int ABLK = kLdsBM / 8;            // A blocks (8 rows x 128 bytes) per pair of steps
+  constexpr int AU2 = ABLK / NW;              // A loads per wave per pair
+  static_assert(BF % NW == 0 && ABLK % NW == 0 && 16 % NW == 0 && ABLK == 2 * AF, "loads split evenly");
+  static_assert(S == 4, "A pairs alternate between the two stage pairs");
+  // LDS read offsets are 16-bit immediates: the A area (64 KB) is addressed
+  // from one base per step parity, the B area from one base per stage pair
+  static_assert(S * ASTAGE <= 65536 && 2 * BSTAGE <= 65536, "immediate read offsets");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int mt = wu.mt, nt = wu.nt, split = wu.split;
+  const int m0 = mt * kLdsBM, n0 = nt * BN;
+  const KRange kr = k_range(g, split);
+  const int nk = kr.nk;  // a multiple of S (the launcher sizes kchunk so)
+
+  // A: block b = wave + NW u of a pair of steps (e, e + 1) lands in A stage
+  // e % S + b / 16, slot b % 16; its 16-byte chunk s holds row 8 b + (s >> 3),
+  // bytes 16 ((s & 7) ^ (s >> 3)) of the row's 128-byte segment (as lds_kernel).
+  uint32_t aoff[AU2];
+  static_for<AU2>([&](auto U) {
+    constexpr int u = decltype(U)::value;
+    const int row = min(m0 + (wave + NW * u) * 8 + (lane >> 3), g.m - 1);
+    aoff[u] = static_cast<uint32_t>(row * g.a_ld + ((lane & 7) ^ (lane >> 3)) * 16);
+  });
+  // B: fragment q = wave + NW u is channel q / NB, column block q % NB
+  // (clamped to the last), one contiguous 1 KB per K step
+  const int8_t *bbase[BU];
+  const int nblk = (g.n + 15) >> 4;
+  static_for<BU>([&](auto U) {
+    constexpr int u = decltype(U)::value;
+    const int q = wave + NW * u, c = q / NB;
+    const int jb = min((n0 >> 4) + q % NB, nblk - 1);
+    bbase[u] = g.b + plane_off(c, c_act, g.b_cs) + static_cast<int64_t>(jb) * g.b_ld + kr.ks0 * 1024;
+  });
+  const uint32_t boff = static_cast<uint32_t>(lane * 16);
+  const int8_t *abase = g.a + kr.ks0 * 64;
+  const uint32_t sbase = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t *)(smem))) +
+      wave * 1024);
+  auto dma_b = [&](auto ST, auto L, int ks) {
+    constexpr int st = decltype(ST)::value, l = decltype(L)::value;
+    const int kc = min(ks, nk - 1);
+    lds_dma16<BAREA + st * BSTAGE + NW * l * 1024>(bbase[l] + static_cast<int64_t>(kc) * 1024, boff, sbase);
+  };
+  auto dma_a = [&](auto ST, auto U, int ks) {  // ks: the pair's first step (even)
+    constexpr int st = decltype(ST)::value, u = decltype(U)::value;
+    const int kc = min(ks, nk - 2);
+    lds_dma16<(st + (NW * u) / 16) * ASTAGE + ((NW * u) % 16) * 1024>(abase + kc * 64, aoff[u], sbase);
+  };
+
+  // fragment reads
+  i32x4 fa[MI], fb[2][NJ];
+  const int f0 = wm * MI;
+  const int8_t *rabase[2];
+  static_for<2>([&](auto P) {
+    constexpr int p = decltype(P)::value;
+    rabase[p] = smem + ((2 * f0) / 16) * ASTAGE + ((2 * f0) % 16) * 1024 + ((lane >> 3) & 1) * 1024 +
+                ((lane & 7) * 8 + ((4 * p + (lane >> 4)) ^ (lane & 7))) * 16;
+  });
+  const int8_t *rbbase[2];
+  static_for<2>([&](auto P) {
+    rbbase[decltype(P)::value] = smem + BAREA + decltype(P)::value * 2 * BSTAGE + wn * NJ * 1024 + lane * 16;
+  });
+  auto read_a = [&](auto H, auto I) {  // A fragment i of the step at stage h
+    constexpr int h = decltype(H)::value, i = decltype(I)::value;
+    fa[i] = *reinterpret_cast<const i32x4 *>(rabase[h & 1] + (h & ~1) * ASTAGE + 2 * i * 1024);
+  };
+  auto read_b = [&](auto H, auto C, auto BUF, auto J) {
+    constexpr int h = decltype(H)::value, c = decltype(C)::value, buf = decltype(BUF)::value,
+                  j = decltype(J)::value;
+    fb[buf][j] = *reinterpret_cast<const i32x4 *>(rbbase[h >> 1] + (h & 1) * BSTAGE + (c * NB + j) * 1024);
+  };
+
+  i32x4 acc[RCAP][MI][NJ];
+  static_for<RCAP>([&](auto C) {
+    static_for<MI>([&](auto I) {
+      static_for<NJ>([&](auto J) {
+        if constexpr (decltype(C)::value < CA)
+          acc[C][I][J] = acc_zero();
+        else
+          acc[C][I][J] = i32x4{0, 0, 0, 0};
+      });
+    });
+  });
+
+  // one K step k at stage h: own loads of step k + 1 landed, then
+  // everyone's (and everyone is done with step k - 1); this step's loads
+  // (even steps: the A pair k + 2, k + 3 first, then B of step k + 3; odd
+  // steps: B of step k + 3), spread over the (channel, row) groups; the
+  // MFMAs channel by channel with the next fragments read between them
+  auto step = [&](auto H, int k) {
+    constexpr int h = decltype(H)::value, nxt = (h + 1) % S;
+    constexpr int nl = (h & 1) ? BU : AU2 + BU;
+    constexpr int slots = CA * MI;
+    wait_vmcnt<BU>();
+    __builtin_amdgcn_s_barrier();
+    static_for<CA>([&](auto C) {
+      constexpr int c = decltype(C)::value;
+      constexpr int buf = (h * CA + c) & 1;
+      // the next channel's B fragments (the next step's first channel)
+      static_for<NJ>([&](auto J) {
+        if constexpr (c + 1 < CA)
+          read_b(std::integral_constant<int, h>{}, std::integral_constant<int, c + 1>{},
+                 std::integral_constant<int, buf ^ 1>{}, J);
+        else
+          read_b(std::integral_constant<int, nxt>{}, std::integral_constant<int, 0>{},
+                 std::integral_constant<int, buf ^ 1>{}, J);
+      });
+      static_for<MI>([&](auto I) {
+        constexpr int i = decltype(I)::value, slot = c * MI + i;
+        static_for<nl>([&](auto L) {
+          constexpr int l = decltype(L)::value;
+          if constexpr ((l * slots) / nl == slot) {
+            if constexpr (!(h & 1) && l < AU2)
+              dma_a(std::integral_constant<int, (h + 2) % S>{}, std::integral_constant<int, l>{}, k + 2);
+            else
+              dma_b(std::integral_constant<int, (h + S - 1) % S>{},
+                    std::integral_constant<int, (h & 1) ? l : l - AU2>{}, k + S - 1);
+          }
+        });
+        static_for<NJ>([&](auto J) {
+          constexpr int j = decltype(J)::value;
+          acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[buf][j], acc[c][i][j], 0, 0, 0);
+        });
+        if constexpr (c == CA - 1) read_a(std::integral_constant<int, nxt>{}, I);
+        // keep the reads where they are: the scheduler otherwise sinks each
+        // one to just before its first use, which exposes its latency
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    });
+  };
+
+  // prologue: the A pair (0, 1) and B of steps 0 .. 2 in flight
+  static_for<AU2>([&](auto U) { dma_a(std::integral_constant<int, 0>{}, U, 0); });
+  static_for<BU>([&](auto L) { dma_b(std::integral_constant<int, 0>{}, L, 0); });
+  static_for<BU>([&](auto L) { dma_b(std::integral_constant<int, 1>{}, L, 1); });
+  static_for<BU>([&](auto L) { dma_b(std::integral_constant<int, 2>{}, L, 2); });
+  Epi<RCAP> e;
+  load_epi<RCAP>(g, e, c_act);
+  pin_epi<RCAP>(e);
+  int m_lim = g.m, n_lim = g.n;
+  pin_sgpr(m_lim);
+  pin_sgpr(n_lim);
+  const int rw0 = m0 + wm * (MI * 16), cw0 = n0 + wn * (NJ * 16);
+  ColScale cs[NJ];
+  static_for<NJ>([&](auto J) { cs[J] = col_scale<RCAP>(e, cw0 + decltype(J)::value * 16 + (lane & 15), n_lim); });
+  // step 0 landed (the column factors, when loaded, were issued after the
+  // loads and are waited for too)
+  wait_vmcnt<2 * BU>();
+  __builtin_amdgcn_s_barrier();
+  static_for<MI>([&](auto I) { read_a(std::integral_constant<int, 0>{}, I); });
+  static_for<NJ>([&](auto J) {
+    read_b(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, J);
+  });
+  __builtin_amdgcn_sched_barrier(0);
+
+  for (int ks0 = 0; ks0 < nk; ks0 += S) {
+    static_for<S>([&](auto H) { step(H, ks0 + decltype(H)::value); });
+  }
+  // the loads issued for steps past K land before the workgroup ends
+  wait_vmcnt<0>();
+
+  if (split >= 0 &&
+      !split_exchange<RCAP, MI, NJ>(g, e, acc, static_cast<int64_t>(wu.split_tile) * NW + wave, split))
+    return;
+  register_epilogue<RCAP, MI, NJ>(g, e, c_act, acc, rw0, cw0, m_lim, n_lim, cs);
+}
+
+template <int RCAP>
+__global__ __launch_bounds__(512) void lds_wide_kernel(const GemmArgsK<RCAP> args) {
+  static_assert(RCAP == 4, "the 256 x 96 x 4 tile");
+  constexpr int ASTAGE = (kLdsBM / 16) * 1024, BSTAGE = RCAP * (kLdsWBN / 16) * 1024;
+  KArgs<RCAP> &g = kernel_args<GemmArgsK<RCAP>>();
+  prefetch_kernel_args<kGemmArgBytes<RCAP>>();
+  __shared__ __attribute__((aligned(1024))) int8_t smem[kLdsStages * (ASTAGE + BSTAGE)];
+  // the adaptive check's reduction slots use the last B stage: the loads of
+  // step 0 first write it, after two barriers that every wave reaches only
+  // after it has read the broadcast channel count
+  int8_t *spare = smem + kLdsStages * ASTAGE + (kLdsStages - 1) * BSTAGE;
+  const int c_act = active_channels<RCAP>(g, reinterpret_cast<int64_t *>(spare), reinterpret_cast<int *>(spare + 64),
+                                          512);
+  const WorkUnit wu = work_of(g);
+  if (c_act == RCAP)
+    lds_wide_body<RCAP, RCAP>(g, smem, RCAP, wu);
+  else if (c_act == RCAP - 1)
+    lds_wide_body<RCAP, RCAP - 1>(g, smem, RCAP - 1, wu);
+  else
+    lds_wide_body<RCAP, RCAP>(g, smem, c_act, wu);  // every channel computed, the prefix's used
+}
+
+// ---------------------------------------------------------------------------
 // Launchers for one channel capacity (instantiated per translation unit).
 // ---------------------------------------------------------------------------
 template <int RCAP, bool ARAW>
@@ -1882,10 +2197,11 @@ inline GemmGrid gemm_grid(const GemmChoice &c, int64_t m, int64_t n) {
     r.tiles = cdiv(n, 16);
     r.waves = c.ks < 1 ? 1 : c.ks;
     r.chunks = c.mb;
-  } else if (c.kind == kLds) {
-    r.tiles = cdiv(m, kLdsBM) * cdiv(n, kLdsBN);
+  } else if (c.kind == kLds || c.kind == kLdsWide) {
+    const int bn = c.kind == kLds ? kLdsBN : kLdsWBN;
+    r.tiles = cdiv(m, kLdsBM) * cdiv(n, bn);
     r.waves = 8;
-    r.chunks = (kLdsBM / 16 / 4) * (kLdsBN / 16 / 2);
+    r.chunks = (kLdsBM / 16 / 4) * (bn / 16 / 2);
   } else {
     const int nwv = c.kind == kMfma3 ? 3 : 4;
     r.tiles = cdiv(m, 16 * c.mb) * cdiv(n, 16 * nwv * c.nb);
@@ -1896,16 +2212,20 @@ inline GemmGrid gemm_grid(const GemmChoice &c, int64_t m, int64_t n) {
 }
 
 template <int RCAP>
-bool launch_lds(const GemmArgs &host, bool araw, hipStream_t st) {
+bool launch_lds(const GemmArgs &host, bool araw, bool wide, hipStream_t st) {
   if constexpr (RCAP != 4) {
     return false;
   } else {
     if (!lds_kernel_fits(host, araw, RCAP)) return false;
     GemmArgsK<RCAP> g = compact_args<RCAP>(host);
+    const int bn = wide ? kLdsWBN : kLdsBN;
     g.tiles_m = (g.m + kLdsBM - 1) / kLdsBM;
-    g.tiles_n = (g.n + kLdsBN - 1) / kLdsBN;
+    g.tiles_n = (g.n + bn - 1) / bn;
     const dim3 grid(static_cast<unsigned>(g.split_from + (g.tiles_m * g.tiles_n - g.split_from) * g.splits));
-    hipLaunchKernelGGL((lds_kernel<RCAP, 8>), grid, dim3(512), 0, st, g);
+    if (wide)
+      hipLaunchKernelGGL((lds_wide_kernel<RCAP>), grid, dim3(512), 0, st, g);
+    else
+      hipLaunchKernelGGL((lds_kernel<RCAP, 8>), grid, dim3(512), 0, st, g);
     return true;
   }
 }
@@ -1970,7 +2290,7 @@ bool launch_gemm_part(const GemmArgs &g, bool araw, const GemmChoice &c, hipStre
   if constexpr (PART == 5) {
     return launch_packed<RCAP>(compact_args<RCAP>(g), c, st);
   } else if constexpr (PART == 4) {
-    return gemm_part_of(c, araw) == PART && launch_lds<RCAP>(g, araw, st);
+    return gemm_part_of(c, araw) == PART && launch_lds<RCAP>(g, araw, c.kind == kLdsWide, st);
   } else {
     if (gemm_part_of(c, araw) != PART) return false;
     if constexpr (PART == 0) {

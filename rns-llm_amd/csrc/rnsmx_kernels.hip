@@ -479,6 +479,8 @@ static int rcap_for(int channels) {
   return 10;
 }
 
+static bool is_lds(int kind) { return kind == kLds || kind == kLdsWide; }
+
 static int32_t check_launch(const char *what) {
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
@@ -546,12 +548,27 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   // more, it wins only when its tiles fill whole rounds of the chip's 256
   // CUs (measured at K = 768-1024: 3 and 1 full rounds faster than the
   // MFMA kernel by 7 % and 30 %; 2.25 rounds slower by 6 %).
-  const int64_t lds_tiles = tiles(kLdsBM, kLdsBN);
+  // Two LDS tile widths: 256 x 96 stages 25 % fewer bytes per MFMA, and a
+  // round of its workgroups takes 1.38 times as long as one of 256 x 64
+  // tiles at K = 4096 (C5: M=2048 6 rounds of 64 columns 358 us against 4
+  // of 96 columns 328 us; M=1024 3 rounds 177 against 2 rounds 170; M=512
+  // 1.5 rounds with the tail split 102 against one round 87.6; N=4096
+  // M=2048 2 rounds 114 against 1.34 rounds 145).  Cost: rounds of 256
+  // workgroups times that factor, a tail round the 64-column kernel splits
+  // over K counted as 0.7.
+  const int64_t t64 = tiles(kLdsBM, kLdsBN), t96 = tiles(kLdsBM, kLdsWBN);
+  auto lds_cost = [&](int64_t t, int per_round, bool tail_split) {
+    const int64_t last = t % 256;
+    const int64_t last_cost = last == 0 ? 0 : (tail_split && last <= 128 && nk >= 32) ? 70 : 100;
+    return (t / 256 * 100 + last_cost) * per_round;
+  };
+  const bool wide = t96 >= 256 && lds_cost(t96, 138, false) < lds_cost(t64, 100, true);
+  const int64_t lds_tiles = wide ? t96 : t64;
   const int64_t rounds = (lds_tiles + 255) / 256;
   const bool full_rounds = 8 * lds_tiles >= 7 * 256 * rounds;
   c.splits = 1;
   if (g.m > 128 && lds_kernel_fits(g, araw, rcap) && lds_tiles >= 256 && (g.kp >= 2048 || full_rounds)) {
-    c.kind = kLds;
+    c.kind = wide ? kLdsWide : kLds;
     return c;
   }
   c.kind = kMfma;
@@ -620,7 +637,7 @@ static constexpr int64_t kTicketBytes = int64_t{RNSMX_SPLIT_TICKETS} * 4;
 // runs whole trips of its stages), and the split count that leaves no
 // split empty.
 static void split_steps(const GemmChoice &c, int nk, int &splits, int &kchunk) {
-  const int unit = c.kind == kLds ? kLdsStages : 1;
+  const int unit = is_lds(c.kind) ? kLdsStages : 1;
   const int s = std::max(1, std::min(c.splits, nk / unit));
   kchunk = ((nk + s - 1) / s + unit - 1) / unit * unit;
   splits = (nk + kchunk - 1) / kchunk;
@@ -646,7 +663,7 @@ static bool split_fits(const GemmChoice &c, const GemmArgs &g) {
   bool built;
   if (c.kind == kStream || c.kind == kStreamWide)
     built = stream_splits(rcap, c.mb, c.nb) && c.ks == 1;
-  else if (c.kind == kLds)
+  else if (is_lds(c.kind))
     built = rcap <= 4;
   else
     built = mfma_splits(rcap, c.mb, c.nb);
@@ -697,7 +714,8 @@ static int choose_splits(const GemmChoice &c, const GemmArgs &g) {
   const int64_t tiles = gemm_grid(c, g.m, g.n).tiles;
   const bool stream = c.kind == kStream || c.kind == kStreamWide;
   int s = 1;
-  if (c.kind == kLds && tiles >= 256) {
+  if (c.kind == kLdsWide) return 1;  // chosen only where no tail split pays
+  if (is_lds(c.kind) && tiles >= 256) {
     const int64_t last = tiles - (tiles - 1) / 256 * 256;  // tiles of the last round
     if (last <= 128 && nk >= 32) {
       const int64_t cap = std::min<int64_t>(4, 256 / last);
@@ -723,7 +741,7 @@ static GemmChoice auto_plan(const GemmArgs &g, bool araw, bool allow_split) {
   GemmChoice t = c;
   if (t.kind == kStream || t.kind == kStreamWide) t.ks = 1;
   t.splits = choose_splits(c, g);
-  t.tail = t.kind == kLds && gemm_grid(t, g.m, g.n).tiles >= 256;
+  t.tail = is_lds(t.kind) && gemm_grid(t, g.m, g.n).tiles >= 256;
   if (t.splits > 1 && split_fits(t, g)) return t;
   return c;
 }
@@ -735,9 +753,11 @@ static int32_t plan_from(const rnsmx_plan_t *plan, const GemmArgs &g, bool araw,
     return RNSMX_OK;
   }
   const int k = plan->kind;
-  if (k != kStream && k != kMfma && k != kLds && k != kStreamWide && k != kMfma3)
-    return fail(RNSMX_EINVAL, "plan kind must be 0 (auto), 1 (stream), 2 (mfma), 3 (lds), 4 (wide stream) or 5 (3-wave mfma)");
-  if (k != kLds && (plan->mb < 1 || plan->nb < 1)) return fail(RNSMX_EINVAL, "tile blocks must be positive");
+  if (k != kStream && k != kMfma && k != kLds && k != kStreamWide && k != kMfma3 && k != kLdsWide)
+    return fail(RNSMX_EINVAL,
+                "plan kind must be 0 (auto), 1 (stream), 2 (mfma), 3 (lds), 4 (wide stream), 5 (3-wave mfma) "
+                "or 7 (wide lds)");
+  if (!is_lds(k) && (plan->mb < 1 || plan->nb < 1)) return fail(RNSMX_EINVAL, "tile blocks must be positive");
   c = GemmChoice{k, plan->mb, plan->nb, plan->ks, std::max(1, plan->splits), plan->tail != 0};
   if (c.splits > 1 && (!allow_split || !split_fits(c, g)))
     return fail(RNSMX_EINVAL, "this plan cannot split K over workgroups (channels, stream waves, or counters)");
@@ -765,7 +785,7 @@ static int32_t launch_gemm(GemmArgs g, bool araw, const GemmChoice &c, uint32_t 
   const int64_t tiles = gemm_grid(c, g.m, g.n).tiles;
   g.split_from = static_cast<int32_t>(tiles);
   if (c.splits > 1) {
-    if (c.kind == kLds && !lds_kernel_fits(g, araw, rcap)) {
+    if (is_lds(c.kind) && !lds_kernel_fits(g, araw, rcap)) {
       set_error("no GEMM kernel for kind %d, tile %d x %d, %d channels", c.kind, c.mb, c.nb, g.mods.channels);
       return RNSMX_EINVAL;
     }
@@ -790,7 +810,7 @@ static int32_t launch_gemm(GemmArgs g, bool araw, const GemmChoice &c, uint32_t 
     return RNSMX_EINVAL;
   }
   return check_launch(c.kind == kStream || c.kind == kStreamWide ? "gemm_stream"
-                      : c.kind == kLds                           ? "gemm_lds"
+                      : is_lds(c.kind)                           ? "gemm_lds"
                                                                  : "gemm_mfma");
 }
 

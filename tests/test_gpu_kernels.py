@@ -135,16 +135,21 @@ def test_mfma_kernel_instances(backend, r, mb, nb, p):
     run_case(backend, mods, 40, 150, 70, dtype=torch.int16, seed=r + 1, plan=plan)
 
 
+LDS_KINDS = [3, 7]  # 256 x 64 and 256 x 96 tiles
+
+
+@pytest.mark.parametrize("kind", LDS_KINDS)
 @pytest.mark.parametrize("m,k,n", [(256 * 2 + 37, 256, 64 * 3 + 5), (300, 512, 100), (17, 1024, 64),
-                                   (256, 768, 2304)])
-def test_lds_kernel(backend, m, k, n):
-    # 256 x 64 tiles, four stages of direct-to-LDS loads: ragged M and N,
+                                   (256, 768, 2304), (256 * 3, 1024, 96 * 5 - 40), (200, 256, 96 + 1)])
+def test_lds_kernel(backend, kind, m, k, n):
+    # 256-row tiles, four stages of direct-to-LDS loads: ragged M and N,
     # one and several trips round the stages
-    run_case(backend, DENSE4, m, k, n, seed=m + k, plan=(3, 0, 0, 0))
+    run_case(backend, DENSE4, m, k, n, seed=m + k, plan=(kind, 0, 0, 0))
 
 
-def test_lds_kernel_rejects_unfit_shapes(backend):
-    lds = (3, 0, 0, 0)
+@pytest.mark.parametrize("kind", LDS_KINDS)
+def test_lds_kernel_rejects_unfit_shapes(backend, kind):
+    lds = (kind, 0, 0, 0)
     prepared = backend.prepare_weight(torch.ones((320, 16), dtype=torch.int8, device=DEV), DENSE4)
     with pytest.raises(ValueError, match="no GEMM kernel"):  # K not a multiple of 256
         backend.matmul_prepared_fused(torch.ones((4, 320), dtype=torch.int8, device=DEV), prepared, plan=lds)
@@ -154,7 +159,8 @@ def test_lds_kernel_rejects_unfit_shapes(backend):
 
 
 @pytest.mark.parametrize("kind,mb,nb,ks,k", [(1, 1, 1, 4, 320), (1, 1, 2, 2, 320), (1, 2, 1, 1, 320),
-                                             (2, 8, 2, 0, 320), (2, 2, 1, 0, 320), (3, 0, 0, 0, 512)])
+                                             (2, 8, 2, 0, 320), (2, 2, 1, 0, 320), (3, 0, 0, 0, 512),
+                                             (7, 0, 0, 0, 512)])
 def test_kernel_adaptive_prefix(backend, kind, mb, nb, ks, k):
     plan = (kind, mb, nb, ks)
     run_case(backend, DENSE4, 50, k, 90, seed=5, adaptive=True, plan=plan)
@@ -163,7 +169,7 @@ def test_kernel_adaptive_prefix(backend, kind, mb, nb, ks, k):
 
 
 @pytest.mark.parametrize("kind,mb,nb,ks", [(1, 1, 2, 2), (1, 4, 1, 4), (1, 2, 1, 1), (2, 8, 2, 0), (2, 2, 1, 0),
-                                           (3, 0, 0, 0)])
+                                           (3, 0, 0, 0), (7, 0, 0, 0)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_kernel_float_epilogue(backend, kind, mb, nb, ks, out_dtype):
     run_case(backend, DENSE4, 45, 256, 77, seed=9, out_dtype=out_dtype, plan=(kind, mb, nb, ks))
@@ -219,26 +225,31 @@ def test_split_k_instances(backend, plan, r):
 
 @pytest.mark.parametrize("m,k,n,splits", [(512 + 37, 1024, 64 * 5 + 3, 2), (300, 2048, 100, 3),
                                           (256, 4096, 64, 4), (17, 512, 64, 2)])
-def test_split_k_lds_kernel(backend, m, k, n, splits):
+@pytest.mark.parametrize("kind", LDS_KINDS)
+def test_split_k_lds_kernel(backend, m, k, n, splits, kind):
     # whole trips of four stages per split
-    run_case(backend, DENSE4, m, k, n, seed=m + splits, plan=(3, 0, 0, 0, splits), repeat=2)
+    run_case(backend, DENSE4, m, k, n, seed=m + splits, plan=(kind, 0, 0, 0, splits), repeat=2)
 
 
 @pytest.mark.parametrize("m,n,splits", [(517, 64 * 90 - 3, 2), (256 * 2 + 9, 64 * 100 + 5, 4), (300, 64 * 160, 2)])
-def test_tail_split_lds_kernel(backend, m, n, splits):
-    # tiles past the last full round of 256 split (270, 300 and 320 tiles:
-    # 14, 44 and 64 split tiles), the others whole; ragged M and N
-    run_case(backend, DENSE4, m, 1024, n, seed=m + n, plan=(3, 0, 0, 0, splits, 1), repeat=2)
+@pytest.mark.parametrize("kind", LDS_KINDS)
+def test_tail_split_lds_kernel(backend, m, n, splits, kind):
+    # tiles past the last full round of 256 split (64-column tiles: 270, 300
+    # and 320 tiles, 14, 44 and 64 of them split; 96-column tiles: 180, 201
+    # and 214 tiles, all in one round, all split), the others whole; ragged
+    # M and N
+    run_case(backend, DENSE4, m, 1024, n, seed=m + n, plan=(kind, 0, 0, 0, splits, 1), repeat=2)
 
 
-@pytest.mark.parametrize("plan", [(1, 1, 1, 1, 4), (2, 3, 1, 4, 2), (5, 2, 1, 4, 2), (3, 0, 0, 0, 2)])
+@pytest.mark.parametrize("plan", [(1, 1, 1, 1, 4), (2, 3, 1, 4, 2), (5, 2, 1, 4, 2), (3, 0, 0, 0, 2),
+                                  (7, 0, 0, 0, 2)])
 def test_split_k_adaptive_prefix(backend, plan):
     k = 512
     run_case(backend, DENSE4, 50, k, 90, seed=15, adaptive=True, plan=plan, repeat=2)
     run_case(backend, DENSE4, 3, k, 90, seed=16, adaptive=True, plan=plan)
 
 
-@pytest.mark.parametrize("plan", [(1, 1, 1, 1, 3), (2, 4, 1, 3, 2), (3, 0, 0, 0, 2)])
+@pytest.mark.parametrize("plan", [(1, 1, 1, 1, 3), (2, 4, 1, 3, 2), (3, 0, 0, 0, 2), (7, 0, 0, 0, 2)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_split_k_float_epilogue(backend, plan, out_dtype):
     run_case(backend, DENSE4, 45, 512, 77, seed=19, out_dtype=out_dtype, plan=plan)

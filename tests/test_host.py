@@ -49,7 +49,8 @@ def gemm_plan(m, n, k, channels=4, raw_a=1):
 
 
 # (M, N, K, channels) -> (kind, mb, nb, ks, splits): kind 1 stream, 2 MFMA,
-# 3 LDS-staged, 4 stream with 8-step chunks, 5 MFMA with 48-column tiles;
+# 3 LDS-staged (256 x 64), 4 stream with 8-step chunks, 5 MFMA with 48-column
+# tiles, 7 LDS-staged (256 x 96);
 # splits: workgroups sharing each output tile's K range
 PLANS = [
     ((1, 2304, 768, 4), (1, 1, 1, 3, 1, 0)),       # decode: stream, 3 waves split 12 K steps
@@ -76,8 +77,10 @@ PLANS = [
     ((48, 12288, 4096, 4), (2, 3, 1, 4, 1, 0)),
     ((64, 12288, 4096, 4), (2, 4, 1, 0, 1, 0)),
     ((128, 12288, 4096, 4), (2, 4, 1, 0, 1, 0)),   # 32 rows would need 768 tiles
-    ((512, 12288, 4096, 4), (3, 0, 0, 0, 2, 1)),   # LDS-staged, 256 x 64 tiles: 384 = 256 whole + 128 split in 2
-    ((2048, 12288, 4096, 4), (3, 0, 0, 0, 1, 0)),
+    ((512, 12288, 4096, 4), (7, 0, 0, 0, 1, 0)),   # LDS-staged, 256 x 96 tiles: 256, one round
+    ((2048, 12288, 4096, 4), (7, 0, 0, 0, 1, 0)),  # 4 rounds of 96 columns against 6 of 64
+    ((1024, 12288, 4096, 4), (7, 0, 0, 0, 1, 0)),
+    ((2048, 4096, 4096, 4), (3, 0, 0, 0, 1, 0)),   # 2 rounds of 64 columns against 1.34 of 96
     ((2048, 12288, 4096, 6), (2, 4, 1, 0, 1, 0)),  # the LDS kernel holds at most 4 channels
     # K split over workgroups: few tiles and long K
     ((1, 768, 16384, 4), (4, 1, 1, 1, 8, 0)),    # decode: 8 one-wave workgroups per 16 x 16 tile
@@ -91,7 +94,10 @@ PLANS = [
     ((256, 256, 8192, 6), (2, 2, 1, 4, 1, 0)),   # the exchange holds at most 4 channels
     ((640, 12288, 4096, 4), (3, 0, 0, 0, 4, 1)),    # 576 LDS tiles: the last 64 split in 4
     ((1280, 12288, 4096, 4), (3, 0, 0, 0, 1, 0)),   # 960 tiles: 192 in the last round, not split
-    ((512, 12288, 1024, 4), (2, 4, 1, 0, 1, 0)),    # short K: LDS only for full rounds, MFMA unsplit
+    ((512, 12288, 1024, 4), (7, 0, 0, 0, 1, 0)),    # short K: LDS only for full rounds (256 x 96: one)
+    ((384, 12288, 1024, 4), (7, 0, 0, 0, 1, 0)),    # 2 x 128 tiles of 256 x 96 (the second row half padding)
+    ((384, 12288, 768, 4), (7, 0, 0, 0, 1, 0)),
+    ((256, 12288, 1024, 4), (2, 4, 1, 0, 1, 0)),    # 128 tiles of 256 x 96: MFMA
 ]
 
 
