@@ -101,11 +101,19 @@ def make_weights(backend, k, n_each, parts, count, seed, device, adaptive=False)
     return prepared, first
 
 
-def make_tokens(m, k, seed, device):
+def make_tokens(m, k, seed, device, outliers=False):
+    """Per-token int8 quantization of seeded N(0, 1) rows.  outliers: 16
+    feature dimensions (the same in every token) scaled by 24, the few
+    large-magnitude features of transformer activations; each token's scale
+    is then set by them and the other values quantize small, so the device
+    prefix picks 3 of the 4 channels."""
     import torch
 
     gen = torch.Generator(device=device).manual_seed(seed)
     x = torch.randn((m, k), generator=gen, device=device)
+    if outliers:
+        dims = torch.randperm(k, generator=gen, device=device)[:16]
+        x[:, dims] *= 24.0
     return quant_rows_int8(x).contiguous()
 
 
@@ -208,7 +216,7 @@ def measure_shape(backend, name, m, k, n_each, parts, steps, warmup, rotate_byte
     r = len(DENSE4)
     count = rotation_count(k, n, rotate_bytes)
     prepared, w0 = make_weights(backend, k, n_each, parts, count, seed, device, adaptive)
-    a = make_tokens(m, k, seed + 1, device)
+    a = make_tokens(m, k, seed + 1, device, outliers="outlier" in name)
     ws = backend.create_workspace(device=device, channels=r, m=m, n=n, k=k)
     if adaptive:
         by_channels = {r: ws}  # the full-set workspace serves every prefix
@@ -567,6 +575,8 @@ def measure_c4(backend, device, steps, warmup):
 # The reference's fused-QKV RNSLinear p50 on its Tesla T4 run
 # (results/v0.5/qkv_fusion.json:20-22, 53-55, 86-88, 119-121), in ms.
 REFERENCE_T4_QKV_P50_MS = {1: 0.859, 16: 0.592, 128: 0.635, 256: 0.702}
+# merged-batch p50 of the reference on a T4 (results/v0.5/concurrency_v05_m1.json)
+REFERENCE_T4_BATCH_P50_MS = {1: 0.2941, 2: 0.3430, 4: 0.4075}
 
 
 def measure_qkv_layer(backend, device, tokens_list=(1, 16, 128, 256), warmup=20, iterations=80):
@@ -619,6 +629,168 @@ def measure_qkv_layer(backend, device, tokens_list=(1, 16, 128, 256), warmup=20,
             "rows": rows}
 
 
+def host_wall(fn, warmup, iterations, sync):
+    """The reference benchmarks' host timing: time.perf_counter around each
+    call (and, with sync, a device synchronisation), p50 / p95 in us."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(iterations):
+        t0 = time.perf_counter()
+        fn()
+        if sync:
+            torch.cuda.synchronize()
+        samples.append((time.perf_counter() - t0) * 1e6)
+    samples.sort()
+    return statistics.median(samples), samples[min(len(samples) - 1, math.ceil(0.95 * len(samples)) - 1)]
+
+
+def device_time(fn, calls=200):
+    """Device time per call of fn (no arguments): calls captured in one graph,
+    replayed once untimed and once timed between events on the launching
+    stream (operands MALL-resident: these rows are a few MB)."""
+    import torch
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(calls):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+    del graph
+    return start.elapsed_time(end) * 1e3 / calls
+
+
+def measure_adaptive_protocol(backend, device, stds=(8, 16, 32, 64), warmup=20, iterations=60):
+    """The reference's adaptive-channel benchmark
+    (benchmarks/benchmark_adaptive_channels.py:34-129): M=128, K=N=768,
+    moduli choose_moduli_for_dot(768, 127, 127, dense_coprime), weights
+    clamp(round(N(0,1) * 28), +-127) int8 [K, N], activations
+    clamp(round(N(0,1) * std), +-127) int8, min_channels 3; the full-set
+    fused call against the adaptive one, host wall time per call with a
+    synchronisation (the reference's measure) and device time per call
+    (graph-replayed).  The adaptive output must equal the full-set output
+    and the exact product."""
+    import torch
+
+    from rns_llm_amd import choose_moduli_for_dot
+
+    m, k, n = 128, 768, 768
+    moduli = choose_moduli_for_dot(k, 127, 127, strategy="dense_coprime")
+    gen = torch.Generator(device=device).manual_seed(29)
+    weight = torch.clamp(torch.round(torch.randn(k, n, generator=gen, device=device) * 28), -127, 127).to(torch.int8)
+    full = backend.prepare_weight(weight, moduli)
+    adaptive = backend.prepare_weight_adaptive(weight, moduli, min_channels=3)
+    ws_full = backend.create_workspace(device=device, channels=len(moduli), m=m, n=n)
+    ws_adaptive = {c: backend.create_workspace(device=device, channels=c, m=m, n=n) for c in adaptive.variants}
+    rows = []
+    for std in stds:
+        act = torch.clamp(torch.round(torch.randn(m, k, generator=gen, device=device) * std), -127, 127).to(torch.int8)
+        out_full = backend.matmul_prepared_fused(act, full, workspace=ws_full, lut_channels=2).clone()
+        out_ad, meta = backend.matmul_prepared_adaptive_fused(act, adaptive, workspace_by_channels=ws_adaptive,
+                                                             lut_channels=2, return_metadata=True)
+        out_ad = out_ad.clone()
+        exact = act.cpu().to(torch.int64) @ weight.cpu().to(torch.int64)
+        if not (torch.equal(out_ad, out_full) and torch.equal(out_full.cpu(), exact)):
+            raise SystemExit(f"parity failure: adaptive prefix at std {std}")
+
+        def call_full():
+            backend.matmul_prepared_fused(act, full, workspace=ws_full, lut_channels=2)
+
+        def call_adaptive():
+            backend.matmul_prepared_adaptive_fused(act, adaptive, workspace_by_channels=ws_adaptive, lut_channels=2)
+
+        f50, f95 = host_wall(call_full, warmup, iterations, sync=True)
+        a50, a95 = host_wall(call_adaptive, warmup, iterations, sync=True)
+        fd, ad = device_time(call_full), device_time(call_adaptive)
+        rows.append({"activation_std": std, "selected_channels": int(meta["channels"]),
+                     "safe_bound": int(meta["bound"]), "capacity": int(meta["capacity"]),
+                     "full_host_p50_us": f50, "full_host_p95_us": f95,
+                     "adaptive_host_p50_us": a50, "adaptive_host_p95_us": a95,
+                     "full_device_us": fd, "adaptive_device_us": ad,
+                     "speedup_host": f50 / a50, "speedup_device": fd / ad})
+    return {"config": "adaptive channel prefix, reference protocol: M=128, K=N=768, weights round(N(0,1)*28), "
+                      "activation std 8/16/32/64, min_channels 3",
+            "moduli": list(moduli), "rows": rows}
+
+
+def measure_requests_protocol(backend, device, warmup=20, iterations=100):
+    """The reference's continuous-batching benchmark
+    (benchmarks/benchmark_concurrency.py:45-117) at M=1 per request
+    (results/v0.5/concurrency_v05_m1.json): K=N=768, int8 U[-127,127]
+    weights and requests, 1, 2 and 4 requests; one stream per request (each
+    with its own workspace, every stream synchronised) against
+    matmul_prepared_fused_requests (the rows gathered into the staging
+    buffer, one fused call, a device synchronisation), host wall time per
+    batch; and the merged call's device time (gather included,
+    graph-replayed).  Merged outputs must equal the per-request ones and the
+    exact product."""
+    import torch
+
+    from rns_llm_amd import choose_moduli_for_dot
+
+    k = n = 768
+    moduli = choose_moduli_for_dot(k, 127, 127, strategy="dense_coprime")
+    gen = torch.Generator(device=device).manual_seed(37)
+    weight = torch.randint(-127, 128, (k, n), generator=gen, device=device, dtype=torch.int8)
+    prepared = backend.prepare_weight(weight, moduli)
+    rows = []
+    for q in (1, 2, 4):
+        acts = [torch.randint(-127, 128, (1, k), generator=gen, device=device, dtype=torch.int8) for _ in range(q)]
+        ws = [backend.create_workspace(device=device, channels=len(moduli), m=1, n=n) for _ in range(q)]
+        streams = [torch.cuda.Stream() for _ in range(q)]
+        batch_ws = backend.create_request_batch_workspace(device=device, dtype=torch.int8, rows_per_request=[1] * q,
+                                                          k=k, channels=len(moduli), n=n)
+
+        def independent():
+            outs = []
+            for i, st in enumerate(streams):
+                with torch.cuda.stream(st):
+                    outs.append(backend.matmul_prepared_fused(acts[i], prepared, lut_channels=2, workspace=ws[i]))
+            for st in streams:
+                st.synchronize()
+            return outs
+
+        def merged_call():
+            return backend.matmul_prepared_fused_requests(acts, prepared, lut_channels=2, workspace=batch_ws)
+
+        def merged():
+            outs = merged_call()
+            torch.cuda.synchronize()
+            return outs
+
+        ind = [o.clone() for o in independent()]
+        mer = [o.clone() for o in merged()]
+        for a, x, y in zip(acts, ind, mer):
+            if not (torch.equal(x, y) and torch.equal(y.cpu(), a.cpu().to(torch.int64) @ weight.cpu().to(torch.int64))):
+                raise SystemExit(f"parity failure: continuous batch of {q} requests")
+        i50, i95 = host_wall(independent, warmup, iterations, sync=False)
+        m50, m95 = host_wall(merged, warmup, iterations, sync=False)
+        dev = device_time(merged_call)
+        rows.append({"requests": q, "independent_streams_p50_us": i50, "independent_streams_p95_us": i95,
+                     "continuous_batch_p50_us": m50, "continuous_batch_p95_us": m95,
+                     "continuous_batch_device_us": dev,
+                     "throughput_requests_per_s": q / (m50 * 1e-6),
+                     "continuous_batch_speedup": i50 / m50,
+                     "reference_t4_continuous_batch_p50_us": REFERENCE_T4_BATCH_P50_MS[q] * 1e3})
+    return {"config": "C3 continuous batching, reference protocol: 1/2/4 requests of M=1, K=N=768",
+            "moduli": list(moduli), "rows": rows}
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -669,6 +841,7 @@ def main():
         extra += [(f"C3 decode {q} requests", q, 768, 768, 1, 33) for q in (1, 2, 4)]
         extra += [("C5 OPT-6.7B QKV", m, 4096, 4096, 3, 67) for m in (1, 512, 2048)]
         extra += [("C5 OPT-6.7B QKV adaptive", m, 4096, 4096, 3, 67) for m in (1, 2048)]
+        extra += [("C5 OPT-6.7B QKV adaptive, outlier tokens", m, 4096, 4096, 3, 67) for m in (1, 512, 2048)]
         for name, m, k, n_each, parts, seed in extra:
             rows.append(measure_shape(backend, name, m, k, n_each, parts, args.steps, args.warmup,
                                       rot, seed, device, adaptive="adaptive" in name))
@@ -683,6 +856,20 @@ def main():
                     f"({rows[-1]['weight_bytes'] / 1e6:.1f} MB) M={m}: {rows[-1]['us_per_call_graph']:.2f} us/step, "
                     f"{rows[-1]['eff_tops']:.1f} eff TOPS, {rows[-1]['gbs_alg']:.0f} GB/s alg, "
                     f"{rows[-1]['bound']} roofline {rows[-1]['roofline_frac']:.3f}")
+        adaptive_rows = measure_adaptive_protocol(backend, device)
+        rows.append(adaptive_rows)
+        for r in adaptive_rows["rows"]:
+            log(f"bench: adaptive (reference protocol) std {r['activation_std']}: {r['selected_channels']} channels, "
+                f"device {r['full_device_us']:.2f} -> {r['adaptive_device_us']:.2f} us "
+                f"(x{r['speedup_device']:.2f}), host p50 {r['full_host_p50_us']:.1f} -> "
+                f"{r['adaptive_host_p50_us']:.1f} us")
+        batching = measure_requests_protocol(backend, device)
+        rows.append(batching)
+        for r in batching["rows"]:
+            log(f"bench: C3 requests (reference protocol) {r['requests']}: merged p50 "
+                f"{r['continuous_batch_p50_us']:.1f} us (device {r['continuous_batch_device_us']:.2f} us), "
+                f"streams p50 {r['independent_streams_p50_us']:.1f} us, "
+                f"reference T4 merged {r['reference_t4_continuous_batch_p50_us']:.0f} us")
         layer = measure_qkv_layer(backend, device)
         rows.append(layer)
         for r in layer["rows"]:

@@ -92,6 +92,7 @@ struct GemmArgsOf {
   int8_t *xchg;       // partial residues, [tile * waves + wave][split][MI * NJ][4 words][64 lanes] x 4 bytes
   // adaptive prefix
   int32_t min_channels;  // 0: all channels
+  int32_t l1_rows;       // row norms at row_l1 to fold (1: their maximum, folded by the encoder)
   const int64_t *row_l1;
   const int32_t *w_absmax;
   int64_t *meta;
@@ -278,7 +279,8 @@ __device__ __forceinline__ int64_t prefix_at(const Mods &mods, int idx) {
 
 // Number of moduli channels to use.  Without the adaptive prefix this is the
 // full set.  With it, every workgroup derives the same answer from the row
-// L1 norms (written by the encoder, or, when row_l1 is null, summed here
+// L1 norms (their maximum, one word written by the encoder; or l1_rows
+// norms to fold; or, when row_l1 is null, summed here
 // from the raw int8 activations: the launcher does so for a few rows only,
 // since every workgroup reads them) and max|B| written at weight preparation:
 // bound = max_i sum_k |a_ik| * max|B| (adaptive.py:44-52); the answer is the
@@ -292,9 +294,11 @@ __device__ __forceinline__ int active_channels(KArgs<RCAP> &g, int64_t *red, int
   if (g.min_channels <= 0) return full;
   const int nw = nthreads >> 6;
   int64_t best = 0;  // max_i sum_k |a_ik|, in thread 0
+  // max|B| in flight with the row norms, not after them
+  const int64_t wmax = threadIdx.x == 0 ? *g.w_absmax : 0;
   if (g.row_l1 != nullptr) {
     int64_t mx = 0;
-    for (int r = threadIdx.x; r < g.m; r += nthreads) {
+    for (int r = threadIdx.x; r < g.l1_rows; r += nthreads) {
       const int64_t v = g.row_l1[r];
       mx = v > mx ? v : mx;
     }
@@ -304,7 +308,8 @@ __device__ __forceinline__ int active_channels(KArgs<RCAP> &g, int64_t *red, int
     if (threadIdx.x == 0)
       for (int w = 0; w < nw; ++w) best = red[w] > best ? red[w] : best;
   } else {
-    // raw int8 rows of a_ld bytes, a_k of them read (a multiple of 16)
+    // raw int8 rows of a_ld bytes, a_k of them read (a multiple of 16); the
+    // launcher does this for a few rows only
     for (int r = 0; r < g.m; ++r) {
       int64_t sum = 0;
       for (int k0 = threadIdx.x * 16; k0 < g.a_k; k0 += nthreads * 16) {
@@ -327,7 +332,6 @@ __device__ __forceinline__ int active_channels(KArgs<RCAP> &g, int64_t *red, int
     }
   }
   if (threadIdx.x == 0) {
-    const int64_t wmax = *g.w_absmax;
     const int64_t bound = (wmax != 0 && best > LLONG_MAX / wmax) ? LLONG_MAX : best * wmax;
     int c = full, overflow = 1;
     static_for<RCAP + 1>([&](auto I) {
@@ -1056,22 +1060,23 @@ constexpr int stream_u_of(int rcap, bool araw, int mb, int nb, int ucap = 4, boo
 }
 
 // PK: packed weights (two byte planes; activations as 2R residue planes).
-template <int RCAP, int MB, int NB, bool ARAW, int UCAP, bool PK>
-__device__ __forceinline__ void stream_body() {
-  KArgs<RCAP> &g = kernel_args<GemmArgsK<RCAP>>();
-  load_hot_args(g);
+// CA: channels computed (the adaptive prefix when it is shorter than the
+// capacity: loads and MFMAs of the channels past it are not issued; the
+// packed form computes every channel).
+template <int RCAP, int MB, int NB, bool ARAW, int UCAP, bool PK, int CA>
+__device__ __forceinline__ void stream_main(KArgs<RCAP> &g, const int c_act) {
   static_assert(!(PK && ARAW), "packed weights take residue-plane activations");
+  static_assert(CA >= 1 && CA <= RCAP && (!PK || CA == RCAP), "channels computed");
   constexpr int BM = 16 * MB, BN = 16 * NB, TILE = BM * BN;
   constexpr int AP = PK ? 2 * RCAP : ARAW ? 1 : RCAP;  // activation planes per K step
   constexpr int BP = PK ? 2 : RCAP;                    // weight planes per K step
+  constexpr int APE = PK ? 2 * RCAP : ARAW ? 1 : CA;   // ... of them loaded
+  constexpr int BPE = PK ? 2 : CA;
   constexpr int U = stream_u_of(RCAP, ARAW, MB, NB, UCAP, PK);
   extern __shared__ __attribute__((aligned(16))) int32_t sacc[];  // [RCAP][TILE] when KS > 1
-  __shared__ int64_t red[4];
-  __shared__ int bcast;
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nthreads = g.threads, ks_n = nthreads >> 6;
-  const int c_act = active_channels<RCAP>(g, red, &bcast, nthreads);
   const WorkUnit wu = work_of(g);
   const int mt = wu.mt, nt = wu.nt, split = wu.split;
   const int m0 = mt * BM, n0 = nt * BN;
@@ -1105,7 +1110,9 @@ __device__ __forceinline__ void stream_body() {
   const i32x4 zero = {0, 0, 0, 0};
   i32x4 acc[RCAP][MB][NB];
   static_for<RCAP>([&](auto C) {
-    static_for<MB>([&](auto I) { static_for<NB>([&](auto J) { acc[C][I][J] = acc_zero(); }); });
+    static_for<MB>([&](auto I) {
+      static_for<NB>([&](auto J) { acc[C][I][J] = decltype(C)::value < CA ? acc_zero() : zero; });
+    });
   });
 
   i32x4 fa[U][AP][MB], fb[U][BP][NB];
@@ -1116,14 +1123,14 @@ __device__ __forceinline__ void stream_body() {
       const int ka = ks * 64 + kofs;
       const bool av = (q + u < nk) && (ka < a_k);
       const int kac = min(ka, a_k - 16);
-      static_for<AP>([&](auto PP) {
+      static_for<APE>([&](auto PP) {
         constexpr int p = decltype(PP)::value;
         static_for<MB>([&](auto I) {
           constexpr int i = decltype(I)::value;
           fa[u][p][i] = select16(av, load16(ap[i] + aoff[p] + kac));
         });
       });
-      static_for<BP>([&](auto C) {
+      static_for<BPE>([&](auto C) {
         constexpr int c = decltype(C)::value;
         static_for<NB>([&](auto J) {
           constexpr int j = decltype(J)::value;
@@ -1135,9 +1142,10 @@ __device__ __forceinline__ void stream_body() {
   auto mfma_chunk = [&]() {
     static_for<U>([&](auto UU) {
       constexpr int u = decltype(UU)::value;
-      // every channel, with no branch (inactive channels read channel 0's
-      // plane; their sums are dropped by the epilogue)
-      static_for<RCAP>([&](auto C) {
+      // every computed channel, with no branch (with CA = RCAP, channels
+      // past the prefix read channel 0's plane; their sums are dropped by
+      // the epilogue)
+      static_for<CA>([&](auto C) {
         constexpr int c = decltype(C)::value;
         static_for<MB>([&](auto I) {
           constexpr int i = decltype(I)::value;
@@ -1280,6 +1288,24 @@ __device__ __forceinline__ void stream_body() {
       });
     }
   });
+}
+
+template <int RCAP, int MB, int NB, bool ARAW, int UCAP, bool PK>
+__device__ __forceinline__ void stream_body() {
+  KArgs<RCAP> &g = kernel_args<GemmArgsK<RCAP>>();
+  load_hot_args(g);
+  __shared__ int64_t red[4];
+  __shared__ int bcast;
+  const int c_act = active_channels<RCAP>(g, red, &bcast, g.threads);
+  // a prefix one channel short of the capacity runs a body without that
+  // channel's loads and MFMAs (C5-shaped decode: 3 of 4 weight planes)
+  if constexpr (!PK && (RCAP == 4 || RCAP == 6)) {
+    if (c_act == RCAP - 1) {
+      stream_main<RCAP, MB, NB, ARAW, UCAP, PK, RCAP - 1>(g, c_act);
+      return;
+    }
+  }
+  stream_main<RCAP, MB, NB, ARAW, UCAP, PK, RCAP>(g, c_act);
 }
 
 template <int RCAP, int MB, int NB, bool ARAW, int UCAP>
@@ -1648,13 +1674,13 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-template <int RCAP, int NW>
-__global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgsK<RCAP> args) {
+// CA: channels computed (as lds_wide_body).
+template <int RCAP, int NW, int CA>
+__device__ __forceinline__ void lds_body(KArgs<RCAP> &g, int8_t *smem, const int c_act, const WorkUnit wu) {
   static_assert(RCAP <= 4, "the 256 x 64 x R tile holds R <= 4 channels");
   static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  static_assert(CA >= 1 && CA <= RCAP, "channels computed");
   constexpr int S = kLdsStages;               // even: each step's stage is a constant in a trip
-  KArgs<RCAP> &g = kernel_args<GemmArgsK<RCAP>>();
-  prefetch_kernel_args<kGemmArgBytes<RCAP>>();
   constexpr int AF = kLdsBM / 16;             // A fragments per stage
   constexpr int BF = RCAP * (kLdsBN / 16);    // B fragments per stage
   constexpr int STAGE = (AF + BF) * 1024;
@@ -1662,14 +1688,9 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgsK<RCAP> args
   constexpr int MI = AF / WM, NJ = kLdsBN / 16 / WN;  // fragments of a wave's tile
   constexpr int BU = BF / NW;                 // B loads per wave per step
   static_assert(BF % NW == 0, "B fragments split evenly over the waves");
-  __shared__ __attribute__((aligned(1024))) int8_t smem[S * STAGE];
-  __shared__ int64_t red[NW];
-  __shared__ int bcast;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
-  const int c_act = active_channels<RCAP>(g, red, &bcast, 64 * NW);
-  const WorkUnit wu = work_of(g);
   const int mt = wu.mt, nt = wu.nt, split = wu.split;
   const int m0 = mt * kLdsBM, n0 = nt * kLdsBN;
   const KRange kr = k_range(g, split);
@@ -1763,7 +1784,14 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgsK<RCAP> args
   };
   i32x4 acc[RCAP][MI][NJ];
   static_for<RCAP>([&](auto C) {
-    static_for<MI>([&](auto I) { static_for<NJ>([&](auto J) { acc[C][I][J] = acc_zero(); }); });
+    static_for<MI>([&](auto I) {
+      static_for<NJ>([&](auto J) {
+        if constexpr (decltype(C)::value < CA)
+          acc[C][I][J] = acc_zero();
+        else
+          acc[C][I][J] = i32x4{0, 0, 0, 0};
+      });
+    });
   });
   // one K step k at stage h: wait until step k + 1 landed (own loads, then
   // everyone's, which also frees the stage of k - 1 and, at odd k with the
@@ -1772,8 +1800,8 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgsK<RCAP> args
   // inactive channels' sums are dropped by the epilogue) with the reads of
   // step k + 1's fragments between them.  The loads of step k - 1 may still
   // be in flight: NLO of them after an odd step, NLE after an even one.
-  static_assert(RCAP * NJ >= MI, "the A reads ride on the first MI (c, j) groups");
-  static_assert(RCAP * NJ >= NLO, "a step's loads fit one per (c, j) group");
+  static_assert(CA * NJ >= MI, "the A reads ride on the first MI (c, j) groups");
+  static_assert(CA * NJ >= NLO, "a step's loads fit one per (c, j) group");
   auto step = [&](auto H, int k) {
     constexpr int h = decltype(H)::value;
     constexpr int nxt = (h + 1) % S, buf = h & 1, nl = (h & 1) ? NLO : NLE;
@@ -1786,19 +1814,19 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgsK<RCAP> args
     // stricter: while any is outstanding it counts toward LAFTER, so fewer
     // LDS reads are left in flight, never more (and the compiled loop issues
     // none).
-    constexpr int LAFTER = RCAP * NJ - MI;
+    constexpr int LAFTER = CA * NJ - MI;
     static_assert(LAFTER >= 0 && LAFTER < 16, "lgkmcnt is 4 bits");
     if constexpr (h & 1) __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (LAFTER << 8) | (0x3 << 14));
     wait_vmcnt<(h & 1) ? NLE : NLO>();
     __builtin_amdgcn_s_barrier();
-    static_for<RCAP>([&](auto C) {
+    static_for<CA>([&](auto C) {
       constexpr int c = decltype(C)::value;
       static_for<NJ>([&](auto J) {
         constexpr int j = decltype(J)::value, q = c * NJ + j;
         // load L at group (L * groups) / nl
         static_for<nl>([&](auto L) {
           constexpr int l = decltype(L)::value;
-          if constexpr ((l * RCAP * NJ) / nl == q) dma_part(H, L, k);
+          if constexpr ((l * CA * NJ) / nl == q) dma_part(H, L, k);
         });
         static_for<MI>([&](auto I) {
           constexpr int i = decltype(I)::value;
@@ -1840,7 +1868,7 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgsK<RCAP> args
   __builtin_amdgcn_s_barrier();
   // the loop's read order, so the wait counts at the loop head are the
   // same whether it is entered from here or from the last step of a trip
-  static_for<RCAP>([&](auto C) {
+  static_for<CA>([&](auto C) {
     static_for<NJ>([&](auto J) {
       constexpr int q = decltype(C)::value * NJ + decltype(J)::value;
       read_b(std::integral_constant<int, 0>{}, C, J);
@@ -1862,6 +1890,25 @@ __global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgsK<RCAP> args
       !split_exchange<RCAP, MI, NJ>(g, e, acc, static_cast<int64_t>(wu.split_tile) * NW + wave, split))
     return;
   register_epilogue<RCAP, MI, NJ>(g, e, c_act, acc, rw0, cw0, m_lim, n_lim, cs);
+}
+
+template <int RCAP, int NW>
+__global__ __launch_bounds__(64 * NW) void lds_kernel(const GemmArgsK<RCAP> args) {
+  constexpr int STAGE = (kLdsBM / 16 + RCAP * (kLdsBN / 16)) * 1024;
+  KArgs<RCAP> &g = kernel_args<GemmArgsK<RCAP>>();
+  prefetch_kernel_args<kGemmArgBytes<RCAP>>();
+  __shared__ __attribute__((aligned(1024))) int8_t smem[kLdsStages * STAGE];
+  __shared__ int64_t red[NW];
+  __shared__ int bcast;
+  const int c_act = active_channels<RCAP>(g, red, &bcast, 64 * NW);
+  const WorkUnit wu = work_of(g);
+  if constexpr (RCAP == 4) {
+    if (c_act == RCAP - 1) {
+      lds_body<RCAP, NW, RCAP - 1>(g, smem, RCAP - 1, wu);
+      return;
+    }
+  }
+  lds_body<RCAP, NW, RCAP>(g, smem, c_act, wu);  // every channel computed, the prefix's used
 }
 
 // ---------------------------------------------------------------------------

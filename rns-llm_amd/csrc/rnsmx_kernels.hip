@@ -30,6 +30,8 @@ struct EncodeArgs {
   int64_t rows, cols, out_ld, plane;
   int8_t *out;
   int64_t *row_l1;
+  int64_t *row_l1_max;  // with l1_ticket: max_i row_l1[i], one word
+  uint32_t *l1_ticket;  // arrival counter of the row workgroups (zero between calls), or null
   int32_t *absmax;
   rnsmx_moduli_t mods;
 };
@@ -145,7 +147,43 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(const EncodeArgs e) {
   }
   if (lead && e.row_l1 != nullptr) {
     l1 = block_sum_i64(l1, sh);
-    if (threadIdx.x == 0) e.row_l1[row] = l1;
+    if (e.l1_ticket == nullptr) {
+      if (threadIdx.x == 0) e.row_l1[row] = l1;
+    } else {
+      // The adaptive bound needs only the largest norm: the last row
+      // workgroup to finish folds them into one word, so that every GEMM
+      // workgroup reads that word instead of all M norms.  The handoff is
+      // split_exchange's: agent-scope stores and loads of the norms, the
+      // store complete before the ticket is taken, a self-resetting counter.
+      __shared__ int last;
+      if (threadIdx.x == 0) {
+        __hip_atomic_store(reinterpret_cast<uint64_t *>(e.row_l1 + row), static_cast<uint64_t>(l1),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wait_vm_all();
+        const uint32_t old = __hip_atomic_fetch_add(e.l1_ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = old == static_cast<uint32_t>(e.rows - 1);
+      }
+      __syncthreads();
+      if (last) {
+        asm volatile("" ::: "memory");
+        int64_t mx = 0;
+        for (int64_t r = threadIdx.x; r < e.rows; r += blockDim.x) {
+          const int64_t v = static_cast<int64_t>(__hip_atomic_load(reinterpret_cast<uint64_t *>(e.row_l1 + r),
+                                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+          mx = v > mx ? v : mx;
+        }
+        mx = wave_max_i64(mx);
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = mx;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+          for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) mx = sh[w] > mx ? sh[w] : mx;
+          __hip_atomic_store(reinterpret_cast<uint64_t *>(e.row_l1_max), static_cast<uint64_t>(mx), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(e.l1_ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
   }
   if (lead && e.absmax != nullptr) {
     const int64_t am = wave_max_i64(static_cast<int64_t>(static_cast<uint32_t>(amax)));
@@ -494,8 +532,12 @@ static constexpr int kStreamLdsMax = 65536;
 
 // Up to this many raw int8 rows, the adaptive prefix's row norms are summed
 // inside the GEMM (every workgroup reads all the rows) instead of by a
-// separate encoder launch.
+// separate encoder launch.  Beyond it the encoder sums them; up to
+// kAdaptiveFoldInGemm rows every GEMM workgroup folds the norms (a few KB),
+// beyond that the encoder folds their maximum into one word (C5 M=2048:
+// 2048 norms re-read by each of 1024 workgroups before their first load).
 static constexpr int kAdaptiveRowsInGemm = 4;
+static constexpr int kAdaptiveFoldInGemm = 256;
 
 static int stream_ks_cap(int rcap, int mb, int nb) {
   const int per_ws = rcap * 256 * mb * nb * 4;  // int32 partial sums in LDS
@@ -632,6 +674,9 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
 // ---------------------------------------------------------------------------
 // Bytes of the arrival counters at the start of every workspace.
 static constexpr int64_t kTicketBytes = int64_t{RNSMX_SPLIT_TICKETS} * 4;
+// The last counter serves the adaptive row-norm fold (encode_rows_kernel);
+// the splits use the ones before it.
+static constexpr int kL1Ticket = RNSMX_SPLIT_TICKETS - 1;
 
 // Steps per split for `splits` workgroups over nk K steps (the LDS kernel
 // runs whole trips of its stages), and the split count that leaves no
@@ -667,7 +712,7 @@ static bool split_fits(const GemmChoice &c, const GemmArgs &g) {
     built = rcap <= 4;
   else
     built = mfma_splits(rcap, c.mb, c.nb);
-  return built && (gr.tiles - whole_tiles(c, gr.tiles)) * gr.waves <= RNSMX_SPLIT_TICKETS;
+  return built && (gr.tiles - whole_tiles(c, gr.tiles)) * gr.waves <= kL1Ticket;
 }
 
 // Exchange-area bytes of a choice (0 without a split).
@@ -1313,7 +1358,7 @@ static PreparedLayout prepared_layout(bool araw, int64_t m, int64_t kp, int32_t 
   PreparedLayout l{};
   l.a_res = kTicketBytes;
   l.row_l1 = l.a_res + (araw ? 0 : round_up(channels * m * kp, 256));
-  l.xchg = l.row_l1 + round_up(8 * m, 256);
+  l.xchg = l.row_l1 + round_up(8 * (m + 1), 256);  // the norms, then their maximum
   l.total = l.xchg + xchg;
   return l;
 }
@@ -1328,7 +1373,7 @@ static PreparedLayout packed_layout(int64_t m, int64_t kp, int32_t channels) {
   const int64_t planes = 2 * channels * m * kp + 4 * channels * packed_corr_ld(m);
   const int64_t rows = m <= kRowsMaxBlocks * 4 ? int64_t{kRowsMaxBlocks} * 2 * kp * 16 : 0;
   l.row_l1 = l.a_res + round_up(std::max(planes, rows), 256);
-  l.xchg = l.row_l1 + round_up(8 * m, 256);
+  l.xchg = l.row_l1 + round_up(8 * (m + 1), 256);  // the norms, then their maximum
   l.total = l.xchg;
   return l;
 }
@@ -1412,6 +1457,7 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
   // themselves (each reads the rows: a few KB from L2), which saves the
   // encoder launch: C5 adaptive M=1 44 -> 39 us.
   const bool l1_in_gemm = araw && min_ch != 0 && m <= kAdaptiveRowsInGemm;
+  const bool l1_fold = m > kAdaptiveFoldInGemm;
   EncodeArgs e{};
   e.values = a_dev;
   e.rows = m;
@@ -1420,6 +1466,8 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
   e.plane = static_cast<int64_t>(m) * kp;
   e.out = araw ? nullptr : a_res;
   e.row_l1 = min_ch != 0 ? row_l1 : nullptr;
+  e.row_l1_max = row_l1 + m;
+  e.l1_ticket = l1_fold ? reinterpret_cast<uint32_t *>(ws) + kL1Ticket : nullptr;
   e.absmax = nullptr;
   e.mods = *mods;
   const bool rows = packed && c.kind == kRows;
@@ -1463,7 +1511,9 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
   g.b_ld = kp * 16;
   g.b_cs = kp * 16 * ((n + 15) / 16);  // per channel, or per byte plane of packed weights
   g.min_channels = min_ch;
-  g.row_l1 = l1_in_gemm ? nullptr : row_l1;
+  // the norms, or the maximum the encoder folded
+  g.row_l1 = l1_in_gemm ? nullptr : l1_fold ? row_l1 + m : row_l1;
+  g.l1_rows = l1_fold ? 1 : m;
   g.w_absmax = min_ch != 0 ? adaptive->w_absmax_dev : nullptr;
   g.meta = min_ch != 0 ? adaptive->meta_dev : nullptr;
   g.out = out_dev;

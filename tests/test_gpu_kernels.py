@@ -168,6 +168,32 @@ def test_kernel_adaptive_prefix(backend, kind, mb, nb, ks, k):
     run_case(backend, DENSE4, 3, k, 90, seed=6, adaptive=True, plan=plan)
 
 
+@pytest.mark.parametrize("plan", [(1, 1, 1, 4), (1, 2, 1, 1), (1, 1, 1, 1, 4), (4, 1, 1, 4), (2, 4, 1, 0),
+                                  (2, 2, 1, 0, 2), (3, 0, 0, 0), (3, 0, 0, 0, 2), (7, 0, 0, 0), (7, 0, 0, 0, 2)])
+@pytest.mark.parametrize("dtype", [torch.int8, torch.int16])
+@pytest.mark.parametrize("m", [3, 70, 600])  # row norms summed in the GEMM / folded there / folded to one word
+def test_kernel_adaptive_three_of_four_channels(backend, plan, dtype, m):
+    # the device picks 3 of the 4 channels: the stream and LDS kernels then
+    # run a body without the fourth channel's loads and MFMAs; exact against
+    # the full set and the product, twice on one workspace
+    if dtype == torch.int16 and plan[0] in (3, 4, 7):
+        pytest.skip("the LDS and wide-chunk kernels take raw int8 activations")
+    gen = torch.Generator().manual_seed(sum(plan) + dtype.itemsize + m)
+    k, n = 512, 200
+    a = torch.randint(-8, 9, (m, k), generator=gen).to(dtype)
+    b = torch.randint(-127, 128, (k, n), generator=gen).to(torch.int8)
+    want = ro.exact_matmul(a.numpy(), b.numpy())
+    prepared = backend.prepare_weight_adaptive(b.to(DEV), DENSE4, min_channels=3)
+    ws = {4: backend.create_workspace(device=torch.device(DEV), channels=4, m=m, n=n, k=k)}
+    for _ in range(2):
+        out, meta = backend.matmul_prepared_adaptive_fused(a.to(DEV), prepared, workspace_by_channels=ws,
+                                                          return_metadata=True, plan=plan)
+        assert meta["channels"] == 3
+        np.testing.assert_array_equal(out.cpu().numpy(), want)
+    full = backend.matmul_prepared_fused(a.to(DEV), prepared.variants[4], plan=plan)
+    np.testing.assert_array_equal(full.cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("kind,mb,nb,ks", [(1, 1, 2, 2), (1, 4, 1, 4), (1, 2, 1, 1), (2, 8, 2, 0), (2, 2, 1, 0),
                                            (3, 0, 0, 0), (7, 0, 0, 0)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])

@@ -46,10 +46,11 @@ def test_noalloc_matches_workspace_entry_on_two_calls(backend):
 
 
 def test_noalloc_drops_a_split_that_does_not_fit(backend):
-    # C5 M=512 with int8 activations: the automatic plan is the LDS kernel's
-    # tail split, whose exchange area alone is 16 MiB; unsplit the call needs
-    # a few KB, so the no-allocation entry point runs it unsplit
-    m, k, n = 512, 4096, 12288
+    # M=640 on the C5 projection with int8 activations: the automatic plan is
+    # the 256 x 64 LDS kernel's tail split (576 tiles, the last 64 split in
+    # 4), whose exchange area alone is 16 MiB; unsplit the call needs a few
+    # KB, so the no-allocation entry point runs it unsplit
+    m, k, n = 640, 4096, 12288
     auto = _native.Plan()
     _native.check(backend._lib.rnsmx_gemm_plan(m, n, k, 4, 1, ctypes.byref(auto)))
     need_auto = backend._lib.rnsmx_prepared_workspace_bytes(m, k, n, 4, None)
