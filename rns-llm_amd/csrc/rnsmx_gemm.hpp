@@ -292,6 +292,28 @@ template <int RCAP>
 __device__ __forceinline__ int active_channels(KArgs<RCAP> &g, int64_t *red, int *bcast, int nthreads) {
   const int full = g.mods.channels;
   if (g.min_channels <= 0) return full;
+  if (g.row_l1 != nullptr && g.l1_rows == 1) {
+    // one word (the maximum the encoder folded): every wave reads it and
+    // max|B| with scalar loads and decides alone, with no barrier
+    const int64_t best = *g.row_l1, wmax = *g.w_absmax;
+    int64_t bound;
+    if (__builtin_mul_overflow(best, wmax, &bound)) bound = LLONG_MAX;
+    int c = full, overflow = 1;
+    static_for<RCAP + 1>([&](auto I) {
+      constexpr int i = decltype(I)::value;
+      if (overflow && i >= g.min_channels && i <= full && bound <= (g.mods.prefix[i] - 1) / 2) {
+        c = i;
+        overflow = 0;
+      }
+    });
+    if (g.meta != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+      g.meta[0] = c;
+      g.meta[1] = bound;
+      g.meta[2] = (prefix_at<RCAP>(g.mods, c) - 1) / 2;
+      g.meta[3] = overflow;
+    }
+    return __builtin_amdgcn_readfirstlane(c);
+  }
   const int nw = nthreads >> 6;
   int64_t best = 0;  // max_i sum_k |a_ik|, in thread 0
   // max|B| in flight with the row norms, not after them
@@ -332,7 +354,8 @@ __device__ __forceinline__ int active_channels(KArgs<RCAP> &g, int64_t *red, int
     }
   }
   if (threadIdx.x == 0) {
-    const int64_t bound = (wmax != 0 && best > LLONG_MAX / wmax) ? LLONG_MAX : best * wmax;
+    int64_t bound;
+    if (__builtin_mul_overflow(best, wmax, &bound)) bound = LLONG_MAX;
     int c = full, overflow = 1;
     static_for<RCAP + 1>([&](auto I) {
       constexpr int i = decltype(I)::value;

@@ -30,8 +30,8 @@ struct EncodeArgs {
   int64_t rows, cols, out_ld, plane;
   int8_t *out;
   int64_t *row_l1;
-  int64_t *row_l1_max;  // with l1_ticket: max_i row_l1[i], one word
-  uint32_t *l1_ticket;  // arrival counter of the row workgroups (zero between calls), or null
+  int64_t *row_l1_max;  // row_l1_max_kernel: max_i row_l1[i], one word
+  uint32_t *l1_ticket;  // row_l1_max_kernel: arrival counter (zero between calls)
   int32_t *absmax;
   rnsmx_moduli_t mods;
 };
@@ -147,43 +147,7 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(const EncodeArgs e) {
   }
   if (lead && e.row_l1 != nullptr) {
     l1 = block_sum_i64(l1, sh);
-    if (e.l1_ticket == nullptr) {
-      if (threadIdx.x == 0) e.row_l1[row] = l1;
-    } else {
-      // The adaptive bound needs only the largest norm: the last row
-      // workgroup to finish folds them into one word, so that every GEMM
-      // workgroup reads that word instead of all M norms.  The handoff is
-      // split_exchange's: agent-scope stores and loads of the norms, the
-      // store complete before the ticket is taken, a self-resetting counter.
-      __shared__ int last;
-      if (threadIdx.x == 0) {
-        __hip_atomic_store(reinterpret_cast<uint64_t *>(e.row_l1 + row), static_cast<uint64_t>(l1),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        wait_vm_all();
-        const uint32_t old = __hip_atomic_fetch_add(e.l1_ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = old == static_cast<uint32_t>(e.rows - 1);
-      }
-      __syncthreads();
-      if (last) {
-        asm volatile("" ::: "memory");
-        int64_t mx = 0;
-        for (int64_t r = threadIdx.x; r < e.rows; r += blockDim.x) {
-          const int64_t v = static_cast<int64_t>(__hip_atomic_load(reinterpret_cast<uint64_t *>(e.row_l1 + r),
-                                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-          mx = v > mx ? v : mx;
-        }
-        mx = wave_max_i64(mx);
-        __syncthreads();
-        if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = mx;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-          for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) mx = sh[w] > mx ? sh[w] : mx;
-          __hip_atomic_store(reinterpret_cast<uint64_t *>(e.row_l1_max), static_cast<uint64_t>(mx), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(e.l1_ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-    }
+    if (threadIdx.x == 0) e.row_l1[row] = l1;
   }
   if (lead && e.absmax != nullptr) {
     const int64_t am = wave_max_i64(static_cast<int64_t>(static_cast<uint32_t>(amax)));
@@ -196,6 +160,67 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(const EncodeArgs e) {
       reinterpret_cast<int32_t *>(e.out + 2 * R * e.plane)[c * packed_corr_ld(e.rows) + row] =
           static_cast<int32_t>(t < 0 ? t + m : t);
     }
+  }
+}
+
+// The adaptive bound's max_i sum_k |a_ik| of raw int8 rows (cols a multiple
+// of 16), folded into one word so that every GEMM workgroup reads that word
+// instead of all M norms (C5 M=2048: 2048 norms re-read by each of 1024
+// workgroups before their first load).  Each wave sums whole rows (a lane
+// 16 bytes per 1 KB of the row), a workgroup keeps the largest of its rows
+// in row_l1[blockIdx.x], and the last workgroup to finish folds those into
+// row_l1_max.  At most 256 workgroups: the arrivals on the one counter are
+// serialised at the memory side (one workgroup per row, 2048 arrivals,
+// measured some 20 us).  The handoff is split_exchange's: agent-scope stores
+// and loads, the store complete before the ticket is taken, a
+// self-resetting counter.
+__global__ __launch_bounds__(256) void row_l1_max_kernel(const EncodeArgs e) {
+  __shared__ int64_t sh[4];
+  __shared__ int last;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int8_t *src = static_cast<const int8_t *>(e.values);
+  int64_t best = 0;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + wv; r < e.rows; r += static_cast<int64_t>(gridDim.x) * 4) {
+    int32_t sum = 0;  // |a| <= 128 and K < 2^24: no overflow
+    for (int64_t k0 = lane * 16; k0 < e.cols; k0 += 64 * 16) {
+      const i32x4 w = *reinterpret_cast<const i32x4 *>(src + r * e.cols + k0);
+      static_for<16>([&](auto Q) {
+        constexpr int q = decltype(Q)::value;
+        const int32_t b = static_cast<int8_t>((static_cast<uint32_t>(w[q >> 2]) >> (8 * (q & 3))) & 0xFFu);
+        sum += b < 0 ? -b : b;
+      });
+    }
+    const int64_t row = wave_sum_i64(sum);
+    best = row > best ? row : best;
+  }
+  if (lane == 0) sh[wv] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w) best = sh[w] > best ? sh[w] : best;
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(e.row_l1 + blockIdx.x), static_cast<uint64_t>(best),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wait_vm_all();
+    const uint32_t old = __hip_atomic_fetch_add(e.l1_ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  asm volatile("" ::: "memory");
+  int64_t mx = 0;
+  for (unsigned b = threadIdx.x; b < gridDim.x; b += blockDim.x) {
+    const int64_t v = static_cast<int64_t>(
+        __hip_atomic_load(reinterpret_cast<uint64_t *>(e.row_l1 + b), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    mx = v > mx ? v : mx;
+  }
+  mx = wave_max_i64(mx);
+  __syncthreads();
+  if (lane == 0) sh[wv] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w) mx = sh[w] > mx ? sh[w] : mx;
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(e.row_l1_max), static_cast<uint64_t>(mx), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(e.l1_ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1457,7 +1482,7 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
   // themselves (each reads the rows: a few KB from L2), which saves the
   // encoder launch: C5 adaptive M=1 44 -> 39 us.
   const bool l1_in_gemm = araw && min_ch != 0 && m <= kAdaptiveRowsInGemm;
-  const bool l1_fold = m > kAdaptiveFoldInGemm;
+  const bool l1_fold = araw && min_ch != 0 && !l1_in_gemm && m > kAdaptiveFoldInGemm;
   EncodeArgs e{};
   e.values = a_dev;
   e.rows = m;
@@ -1467,7 +1492,7 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
   e.out = araw ? nullptr : a_res;
   e.row_l1 = min_ch != 0 ? row_l1 : nullptr;
   e.row_l1_max = row_l1 + m;
-  e.l1_ticket = l1_fold ? reinterpret_cast<uint32_t *>(ws) + kL1Ticket : nullptr;
+  e.l1_ticket = reinterpret_cast<uint32_t *>(ws) + kL1Ticket;
   e.absmax = nullptr;
   e.mods = *mods;
   const bool rows = packed && c.kind == kRows;
@@ -1496,6 +1521,10 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
     }
   } else if (packed) {
     if (int32_t rc = launch_encode_rows(a_dtype, e, st, true)) return rc;
+  } else if (l1_fold) {
+    const unsigned groups = static_cast<unsigned>(std::min<int64_t>((m + 3) / 4, 256));
+    hipLaunchKernelGGL(row_l1_max_kernel, dim3(groups), dim3(256), 0, st, e);
+    if (int32_t rc = check_launch("row_l1_max")) return rc;
   } else if (!araw || (min_ch != 0 && !l1_in_gemm)) {
     if (int32_t rc = launch_encode_rows(a_dtype, e, st)) return rc;
   }
