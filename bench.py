@@ -322,13 +322,17 @@ PMC_SHAPES = {
     "headline": [("C2", None, 768, 768, 3, 12)],
     "all": [("C2", 256, 768, 768, 3, 6), ("C3", 1, 768, 768, 1, 6), ("C5", 1, 4096, 4096, 3, 4),
             ("C5", 512, 4096, 4096, 3, 3), ("C5", 2048, 4096, 4096, 3, 3)],
+    # the int16 6-channel path on the C5 shape: residue planes and packed weights
+    "wide": [("planes", 16, 4096, 4096, 3, 3), ("planes", 512, 4096, 4096, 3, 2), ("packed", 1, 4096, 4096, 3, 3),
+             ("packed", 16, 4096, 4096, 3, 3), ("packed", 512, 4096, 4096, 3, 2)],
 }
 
 
 def pmc_child(args):
     """Workload of one counter pass: a 64 MiB device copy (calibration) and
-    GEMM calls on rotated weights (the headline shape, or with
-    --pmc-shapes all the C2 M=256, C3, C5 M=1 and C5 M=2048 shapes)."""
+    GEMM calls on rotated weights (the headline shape; with --pmc-shapes
+    all the C2 M=256, C3, C5 M=1, 512 and 2048 shapes; with wide the int16
+    6-channel path on the C5 shape)."""
     import torch
 
     from rns_llm_amd import HipRNSBackend
@@ -343,6 +347,20 @@ def pmc_child(args):
     for name, m, k, n_each, parts, calls in PMC_SHAPES[args.pmc_shapes]:
         m = args.m if m is None else m
         n = n_each * parts
+        if name in ("planes", "packed"):  # int16 weights and activations, 6 channels
+            gen = torch.Generator(device=device).manual_seed(19)
+            prep = backend.prepare_weight_packed_nk if name == "packed" else backend.prepare_weight_nk
+            count = 2
+            prepared = [prep(torch.randint(-32767, 32768, (n, k), generator=gen, device=device,
+                                           dtype=torch.int32).to(torch.int16), DENSE6) for _ in range(count)]
+            a = torch.randint(-32767, 32768, (m, k), generator=gen, device=device, dtype=torch.int32).to(torch.int16)
+            ws = backend.create_workspace(device=device, channels=len(DENSE6), m=m, n=n)
+            for i in range(calls):
+                backend.matmul_prepared_fused(a, prepared[(i + 1) % count], workspace=ws)
+            torch.cuda.synchronize()
+            del prepared, ws
+            torch.cuda.empty_cache()
+            continue
         count = rotation_count(k, n, int(min(args.rotate_mb, 450.0) * 1e6))
         prepared, _ = make_weights(backend, k, n_each, parts, count, 17, device)
         a = make_tokens(m, k, 18, device)
