@@ -86,7 +86,10 @@ typedef struct rnsmx_moduli {
  * loading chunks of up to 8 K steps per wave (16 x 16 tiles, up to 4
  * channels), 5 = the MFMA kernel with three column waves (tile 16*mb x
  * 48*nb; int8 activations read in place, up to 4 channels), 7 = the
- * LDS-staged kernel with 256 x 96 tiles (same conditions as 3).
+ * LDS-staged kernel with 256 x 96 tiles (same conditions as 3), 8 = the
+ * LDS-staged kernel for residue-plane activations (int16 / int32 inputs;
+ * 128 x 128 tiles, 4- or 6-channel capacity, K a multiple of 256, never
+ * split; mb, nb, ks ignored).
  * splits: workgroups splitting K per output tile (0 or 1 = none; up to 4
  * channels, and for the stream kernel ks = 1): each reduces its partial
  * sums to residues, and the last to finish a tile reconstructs it.  tail:
@@ -323,7 +326,7 @@ int32_t rnsmx_packed_plan(int64_t m, int64_t n, int64_t k, int32_t channels,
 
 /*
  * The plan rnsmx_matmul_prepared_fused chooses by itself for an M x N x K
- * product with `channels` moduli (kind 1-5, tile, ks, splits as in
+ * product with `channels` moduli (kind 1-8, tile, ks, splits as in
  * rnsmx_plan_t).  raw_a != 0: int8 activations read in place, as the fused
  * entry points do for int8 sources with K a multiple of 16 whose
  * accumulators fit int32; 0: residue planes.  Host code only (no GPU call,

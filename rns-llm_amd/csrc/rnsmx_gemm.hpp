@@ -134,7 +134,17 @@ inline GemmArgsK<RCAP> compact_args(const GemmArgs &g) {
 // kMfma3: the MFMA kernel with three column waves (48*nb-column tiles).
 // kRows: packed weights at decode (rows_packed_kernel: MFMA rows are channels).
 // kLdsWide: the LDS-staged kernel with 256 x 96 tiles (lds_wide_kernel).
-enum GemmKind { kAuto = 0, kStream = 1, kMfma = 2, kLds = 3, kStreamWide = 4, kMfma3 = 5, kRows = 6, kLdsWide = 7 };
+enum GemmKind {
+  kAuto = 0,
+  kStream = 1,
+  kMfma = 2,
+  kLds = 3,
+  kStreamWide = 4,
+  kMfma3 = 5,
+  kRows = 6,
+  kLdsWide = 7,
+  kLdsPlanes = 8
+};
 
 // ks: waves splitting K (stream kernel) or ring depth, 0 = automatic (MFMA
 // kernel); splits: workgroups splitting K (1 = none); tail: only the tiles
@@ -163,7 +173,7 @@ constexpr int kGemmParts = 6;
 inline int gemm_part_of(const GemmChoice &c, bool araw, bool packed = false) {
   if (packed) return 5;
   if (c.kind == kStream || c.kind == kStreamWide) return 0;
-  if (c.kind == kLds || c.kind == kLdsWide) return 4;
+  if (c.kind == kLds || c.kind == kLdsWide || c.kind == kLdsPlanes) return 4;
   if (!araw) return 3;
   return c.nb == 1 ? 1 : 2;
 }
@@ -753,7 +763,10 @@ __device__ __forceinline__ void register_epilogue(KArgs<RCAP> &g, const Epi<RCAP
     });
     return;
   }
-  auto run = [&](auto FAST, auto OUT, auto INTERIOR) {
+  // always inlined: a call would pass the accumulators by reference, i.e.
+  // through memory for the whole kernel (the inliner gives up on the
+  // generic variant's size once a wave holds 64 x 64 x 6 channels)
+  auto run = [&](auto FAST, auto OUT, auto INTERIOR) __attribute__((always_inline)) {
     static_for<MI>([&](auto I) {
       constexpr int i = decltype(I)::value;
       static_for<4>([&](auto T) {
@@ -774,7 +787,7 @@ __device__ __forceinline__ void register_epilogue(KArgs<RCAP> &g, const Epi<RCAP
       });
     });
   };
-  with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) {
+  with_epilogue<RCAP>(e, c_act, [&](auto FAST, auto OUT) __attribute__((always_inline)) {
     if (interior)
       run(FAST, OUT, std::true_type{});
     else
@@ -2167,6 +2180,201 @@ __global__ __launch_bounds__(512) void lds_wide_kernel(const GemmArgsK<RCAP> arg
 }
 
 // ---------------------------------------------------------------------------
+// LDS-staged GEMM for residue-plane activations (int16 / int32 inputs, each
+// channel its own A plane), 128 x 128 tiles, 4 or 6 channels.  With raw
+// int8 A one staged A tile serves every channel; here each channel has its
+// own A, so the staging unit is one channel over a pair of K steps: A (128
+// rows x 128 bytes, loaded as whole row segments and XOR-swizzled as in
+// lds_kernel) and B (8 column blocks x 2 steps of 1 KB), 32 KB.  Four such
+// slots (128 KB) form the ring; a trip runs lcm(R, 4) units (R = 6: two
+// pairs of K steps, 12 units), so every unit's slot and channel are
+// constants in the unrolled trip.  8 waves (2 x 4), each 64 x 32 x R
+// channels: 32 R accumulator registers (192 at R = 6), fragments single-
+// buffered as in lds_wide_kernel.  Per unit t, slot t % 4:
+//  * wait for the own loads of unit t + 1, barrier (everyone's have landed
+//    and everyone is done with unit t - 1), then the loads of unit t + 3
+//    into the slot of unit t - 1, spread over the MFMAs;
+//  * step 0 of the pair row by row, each A fragment of step 1 read right
+//    after the last MFMA that uses its register; then the next unit's step-0
+//    B fragments; step 1, each of the next unit's step-0 A fragments read
+//    after its row; then the next unit's step-1 B fragments.
+// A wave's LDS reads per MFMA are those of a 64 x 32 tile (6 KB per 8
+// MFMAs, against 16 KB per 48 with raw int8 A): this kernel is bound by LDS
+// bandwidth and the MFMAs together, not by HBM or L2.
+// ---------------------------------------------------------------------------
+constexpr int kPlBM = 128, kPlBN = 128;
+
+template <int RCAP>
+__device__ __forceinline__ void lds_planes_body(KArgs<RCAP> &g, int8_t *smem, const int c_act, const WorkUnit wu) {
+  static_assert(RCAP == 4 || RCAP == 6, "32 R accumulator registers");
+  // (four waves of 64 x 64, one per SIMD with 512 registers, read 25 % fewer
+  // LDS bytes per MFMA, but the compiler then moves the 384 accumulators
+  // between register files and scratch memory inside the loop)
+  constexpr int NW = 8, S = 4, WN = NW / 2, MI = 4, NJ = 8 / WN;
+  constexpr int DU = 16 / NW, LU = 2 * DU;       // A (and B) loads per wave per unit; all loads
+  constexpr int UA = 16 * 1024, UB = 16 * 1024;  // A and B parts of one unit
+  constexpr int BAREA = S * UA;                  // the A parts of all slots, then the B parts
+  constexpr int TRIP = RCAP == 6 ? 12 : 4;       // lcm(R, S) units
+  constexpr int PAIRS = TRIP / RCAP;             // pairs of K steps per trip
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int m0 = wu.mt * kPlBM, n0 = wu.nt * kPlBN;
+  const KRange kr = k_range(g, wu.split);
+  const int npairs = kr.nk >> 1;  // a multiple of PAIRS (the launcher requires K % 256 == 0)
+
+  // A block b = wave + NW u (rows 8 b .. 8 b + 7 of the tile): lane l loads
+  // row 8 b + (l >> 3), bytes 16 ((l & 7) ^ (l >> 3)) of the pair's 128-byte
+  // row segment, into chunk l of the block.
+  uint32_t aoff[DU];
+  static_for<DU>([&](auto U) {
+    constexpr int u = decltype(U)::value;
+    const int row = min(m0 + (wave + NW * u) * 8 + (lane >> 3), g.m - 1);
+    aoff[u] = static_cast<uint32_t>(row * g.a_ld + ((lane & 7) ^ (lane >> 3)) * 16);
+  });
+  // B fragment f = wave + NW u: step f / 8 = (NW u) / 8 of the pair, column
+  // block f % 8 = wave + (NW u) % 8 (clamped to the last), 1 KB contiguous
+  const int nblk = (g.n + 15) >> 4;
+  const int8_t *bcol[DU];
+  static_for<DU>([&](auto U) {
+    constexpr int u = decltype(U)::value;
+    bcol[u] = g.b + static_cast<int64_t>(min((n0 >> 4) + wave + (NW * u) % 8, nblk - 1)) * g.b_ld + kr.ks0 * 1024;
+  });
+  const int8_t *acol = g.a + kr.ks0 * 64;
+  int64_t aplane[RCAP], bplane[RCAP];
+  static_for<RCAP>([&](auto C) {
+    constexpr int c = decltype(C)::value;
+    aplane[c] = plane_off(c, c_act, g.a_cs);
+    bplane[c] = plane_off(c, c_act, g.b_cs);
+  });
+  const uint32_t boff = static_cast<uint32_t>(lane * 16);
+  const uint32_t sbase = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t *)(smem))) +
+      wave * 1024);
+  // load L (A blocks for L < DU, then B fragments) of unit (pair e,
+  // channel c) into slot sl; pairs past K load the last pair again into a
+  // slot never read
+  auto dma = [&](auto SL, auto C, auto L, int e) {
+    constexpr int sl = decltype(SL)::value, c = decltype(C)::value, l = decltype(L)::value;
+    const int ec = min(e, npairs - 1);
+    if constexpr (l < DU) {
+      lds_dma16<sl * UA + NW * l * 1024>(acol + aplane[c] + ec * 128, aoff[l], sbase);
+    } else {
+      constexpr int u = l - DU, step = (NW * u) / 8;
+      lds_dma16<BAREA + sl * UB + NW * u * 1024>(bcol[u] + bplane[c] + static_cast<int64_t>(2 * ec + step) * 1024,
+                                                boff, sbase);
+    }
+  };
+
+  // fragment reads: A fragment i of step p at slot sl (rows 16 (4 wm + i) +
+  // (lane & 15): block 2 (4 wm + i) + ((lane >> 3) & 1), chunk 4 p + (lane >>
+  // 4) of row lane & 7); B fragment j of step s (column block 2 wn + j)
+  i32x4 fa[MI], fb[2][NJ];
+  const int8_t *rabase[2];
+  static_for<2>([&](auto P) {
+    constexpr int p = decltype(P)::value;
+    rabase[p] = smem + (2 * MI * wm) * 1024 + ((lane >> 3) & 1) * 1024 +
+                ((lane & 7) * 8 + ((4 * p + (lane >> 4)) ^ (lane & 7))) * 16;
+  });
+  const int8_t *rbbase = smem + BAREA + wn * NJ * 1024 + lane * 16;
+  auto read_a = [&](auto SL, auto P, auto I) {
+    constexpr int sl = decltype(SL)::value, p = decltype(P)::value, i = decltype(I)::value;
+    fa[i] = *reinterpret_cast<const i32x4 *>(rabase[p] + sl * UA + 2 * i * 1024);
+  };
+  auto read_b = [&](auto SL, auto ST, auto J) {
+    constexpr int sl = decltype(SL)::value, st = decltype(ST)::value, j = decltype(J)::value;
+    fb[st][j] = *reinterpret_cast<const i32x4 *>(rbbase + sl * UB + (st * 8 + j) * 1024);
+  };
+
+  i32x4 acc[RCAP][MI][NJ];
+  static_for<RCAP>([&](auto C) {
+    static_for<MI>([&](auto I) { static_for<NJ>([&](auto J) { acc[C][I][J] = acc_zero(); }); });
+  });
+
+  // unit t of the trip starting at pair e0
+  auto unit = [&](auto T, int e0) {
+    constexpr int t = decltype(T)::value, sl = t % S, c = t % RCAP, nsl = (t + 1) % S;
+    constexpr int t3 = t + 3, sl3 = t3 % S, c3 = t3 % RCAP, pe3 = t3 / RCAP;
+    wait_vmcnt<LU>();
+    __builtin_amdgcn_s_barrier();
+    static_for<2>([&](auto ST) {
+      constexpr int st = decltype(ST)::value;
+      static_for<MI>([&](auto I) {
+        constexpr int i = decltype(I)::value, grp = st * MI + i;
+        // the LU loads of unit t + 3, spread over the 8 row groups
+        static_for<LU>([&](auto L) {
+          if constexpr ((decltype(L)::value * 2 * MI) / LU == grp)
+            dma(std::integral_constant<int, sl3>{}, std::integral_constant<int, c3>{}, L, e0 + pe3);
+        });
+        static_for<NJ>([&](auto J) {
+          constexpr int j = decltype(J)::value;
+          acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[st][j], acc[c][i][j], 0, 0, 0);
+        });
+        // the read below reuses fa[i]'s register only if it stays after
+        // the MFMAs that consume the old value
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (st == 0)
+          read_a(std::integral_constant<int, sl>{}, std::integral_constant<int, 1>{}, I);
+        else
+          read_a(std::integral_constant<int, nsl>{}, std::integral_constant<int, 0>{}, I);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      static_for<NJ>([&](auto J) { read_b(std::integral_constant<int, nsl>{}, ST, J); });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // prologue: units 0, 1, 2 in flight
+  static_for<3>([&](auto T) {
+    constexpr int t = decltype(T)::value;
+    static_for<LU>([&](auto L) {
+      dma(std::integral_constant<int, t % S>{}, std::integral_constant<int, t % RCAP>{}, L, t / RCAP);
+    });
+  });
+  // unit 0 landed
+  wait_vmcnt<2 * LU>();
+  __builtin_amdgcn_s_barrier();
+  static_for<MI>([&](auto I) { read_a(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, I); });
+  static_for<2>([&](auto ST) {
+    static_for<NJ>([&](auto J) { read_b(std::integral_constant<int, 0>{}, ST, J); });
+  });
+  __builtin_amdgcn_sched_barrier(0);
+
+  for (int e0 = 0; e0 < npairs; e0 += PAIRS) {
+    static_for<TRIP>([&](auto T) { unit(T, e0); });
+  }
+  // the loads issued for units past K land before the workgroup ends
+  wait_vmcnt<0>();
+  // The epilogue's constants and column factors are read only now: with
+  // 6 channels they would hold some 110 scalar registers (and the column
+  // factors 4 vector registers) through the loop, which the accumulators
+  // leave no room for.  The scalar ones hit the constant cache (the
+  // argument block was read at entry).
+  Epi<RCAP> e;
+  load_epi<RCAP>(g, e, c_act);
+  const int m_lim = g.m, n_lim = g.n;
+  const int rw0 = m0 + wm * (MI * 16), cw0 = n0 + wn * (NJ * 16);
+  ColScale cs[NJ];
+  static_for<NJ>([&](auto J) { cs[J] = col_scale<RCAP>(e, cw0 + decltype(J)::value * 16 + (lane & 15), n_lim); });
+  register_epilogue<RCAP, MI, NJ>(g, e, c_act, acc, rw0, cw0, m_lim, n_lim, cs);
+}
+
+template <int RCAP>
+__global__ __launch_bounds__(512) void lds_planes_kernel(const GemmArgsK<RCAP> args) {
+  constexpr int SLOTS = kLdsStages * 32 * 1024;
+  KArgs<RCAP> &g = kernel_args<GemmArgsK<RCAP>>();
+  prefetch_kernel_args<kGemmArgBytes<RCAP>>();
+  __shared__ __attribute__((aligned(1024))) int8_t smem[SLOTS];
+  // the adaptive check's reduction slots use the last slot's B part: the
+  // loads of unit 3 first write it, after the barrier of unit 0, which every
+  // wave reaches only after it has read the broadcast channel count
+  int8_t *spare = smem + SLOTS - 16 * 1024;
+  const int c_act = __builtin_amdgcn_readfirstlane(
+      active_channels<RCAP>(g, reinterpret_cast<int64_t *>(spare), reinterpret_cast<int *>(spare + 64), 512));
+  lds_planes_body<RCAP>(g, smem, c_act, work_of(g));
+}
+
+// ---------------------------------------------------------------------------
 // Launchers for one channel capacity (instantiated per translation unit).
 // ---------------------------------------------------------------------------
 template <int RCAP, bool ARAW>
@@ -2272,6 +2480,10 @@ inline GemmGrid gemm_grid(const GemmChoice &c, int64_t m, int64_t n) {
     r.tiles = cdiv(m, kLdsBM) * cdiv(n, bn);
     r.waves = 8;
     r.chunks = (kLdsBM / 16 / 4) * (bn / 16 / 2);
+  } else if (c.kind == kLdsPlanes) {
+    r.tiles = cdiv(m, kPlBM) * cdiv(n, kPlBN);
+    r.waves = 8;
+    r.chunks = (kPlBM / 16 / 2) * (kPlBN / 16 / 4);
   } else {
     const int nwv = c.kind == kMfma3 ? 3 : 4;
     r.tiles = cdiv(m, 16 * c.mb) * cdiv(n, 16 * nwv * c.nb);
@@ -2281,8 +2493,29 @@ inline GemmGrid gemm_grid(const GemmChoice &c, int64_t m, int64_t n) {
   return r;
 }
 
+// The residue-plane LDS kernel: activations as per-channel planes (not raw
+// int8), 4 or 6 channels, K a multiple of 256 (whole trips), rows addressed
+// through 32-bit per-lane offsets within a plane.
+inline bool lds_planes_fits(const GemmArgs &g, bool araw, int rcap) {
+  const bool a_offsets_fit = static_cast<int64_t>(g.m) * g.a_ld < (int64_t{1} << 32) - 256;
+  return !araw && (rcap == 4 || rcap == 6) && g.a_k == g.kp && g.kp % (64 * kLdsStages) == 0 && a_offsets_fit;
+}
+
 template <int RCAP>
-bool launch_lds(const GemmArgs &host, bool araw, bool wide, hipStream_t st) {
+bool launch_lds(const GemmArgs &host, bool araw, int kind, hipStream_t st) {
+  if (kind == kLdsPlanes) {
+    if constexpr (RCAP == 4 || RCAP == 6) {
+      if (!lds_planes_fits(host, araw, RCAP) || host.splits > 1) return false;
+      GemmArgsK<RCAP> g = compact_args<RCAP>(host);
+      g.tiles_m = (g.m + kPlBM - 1) / kPlBM;
+      g.tiles_n = (g.n + kPlBN - 1) / kPlBN;
+      const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));
+      hipLaunchKernelGGL((lds_planes_kernel<RCAP>), grid, dim3(512), 0, st, g);
+      return true;
+    }
+    return false;
+  }
+  const bool wide = kind == kLdsWide;
   if constexpr (RCAP != 4) {
     return false;
   } else {
@@ -2360,7 +2593,7 @@ bool launch_gemm_part(const GemmArgs &g, bool araw, const GemmChoice &c, hipStre
   if constexpr (PART == 5) {
     return launch_packed<RCAP>(compact_args<RCAP>(g), c, st);
   } else if constexpr (PART == 4) {
-    return gemm_part_of(c, araw) == PART && launch_lds<RCAP>(g, araw, c.kind == kLdsWide, st);
+    return gemm_part_of(c, araw) == PART && launch_lds<RCAP>(g, araw, c.kind, st);
   } else {
     if (gemm_part_of(c, araw) != PART) return false;
     if constexpr (PART == 0) {

@@ -542,7 +542,7 @@ static int rcap_for(int channels) {
   return 10;
 }
 
-static bool is_lds(int kind) { return kind == kLds || kind == kLdsWide; }
+static bool is_lds(int kind) { return kind == kLds || kind == kLdsWide || kind == kLdsPlanes; }
 
 static int32_t check_launch(const char *what) {
   const hipError_t err = hipGetLastError();
@@ -636,6 +636,12 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   c.splits = 1;
   if (g.m > 128 && lds_kernel_fits(g, araw, rcap) && lds_tiles >= 256 && (g.kp >= 2048 || full_rounds)) {
     c.kind = wide ? kLdsWide : kLds;
+    return c;
+  }
+  // Residue-plane activations with 6 channels (int16 / int32 inputs): the
+  // 128 x 128 LDS-staged kernel once its tiles fill a round of the CUs.
+  if (g.m > 128 && rcap == 6 && lds_planes_fits(g, araw, rcap) && tiles(kPlBM, kPlBN) >= 256) {
+    c.kind = kLdsPlanes;
     return c;
   }
   c.kind = kMfma;
@@ -734,7 +740,7 @@ static bool split_fits(const GemmChoice &c, const GemmArgs &g) {
   if (c.kind == kStream || c.kind == kStreamWide)
     built = stream_splits(rcap, c.mb, c.nb) && c.ks == 1;
   else if (is_lds(c.kind))
-    built = rcap <= 4;
+    built = c.kind != kLdsPlanes && rcap <= 4;
   else
     built = mfma_splits(rcap, c.mb, c.nb);
   return built && (gr.tiles - whole_tiles(c, gr.tiles)) * gr.waves <= kL1Ticket;
@@ -784,7 +790,7 @@ static int choose_splits(const GemmChoice &c, const GemmArgs &g) {
   const int64_t tiles = gemm_grid(c, g.m, g.n).tiles;
   const bool stream = c.kind == kStream || c.kind == kStreamWide;
   int s = 1;
-  if (c.kind == kLdsWide) return 1;  // chosen only where no tail split pays
+  if (c.kind == kLdsWide || c.kind == kLdsPlanes) return 1;  // never split (the wide one: where no tail split pays)
   if (is_lds(c.kind) && tiles >= 256) {
     const int64_t last = tiles - (tiles - 1) / 256 * 256;  // tiles of the last round
     if (last <= 128 && nk >= 32) {
@@ -823,10 +829,11 @@ static int32_t plan_from(const rnsmx_plan_t *plan, const GemmArgs &g, bool araw,
     return RNSMX_OK;
   }
   const int k = plan->kind;
-  if (k != kStream && k != kMfma && k != kLds && k != kStreamWide && k != kMfma3 && k != kLdsWide)
+  if (k != kStream && k != kMfma && k != kLds && k != kStreamWide && k != kMfma3 && k != kLdsWide &&
+      k != kLdsPlanes)
     return fail(RNSMX_EINVAL,
-                "plan kind must be 0 (auto), 1 (stream), 2 (mfma), 3 (lds), 4 (wide stream), 5 (3-wave mfma) "
-                "or 7 (wide lds)");
+                "plan kind must be 0 (auto), 1 (stream), 2 (mfma), 3 (lds), 4 (wide stream), 5 (3-wave mfma), "
+                "7 (wide lds) or 8 (residue-plane lds)");
   if (!is_lds(k) && (plan->mb < 1 || plan->nb < 1)) return fail(RNSMX_EINVAL, "tile blocks must be positive");
   c = GemmChoice{k, plan->mb, plan->nb, plan->ks, std::max(1, plan->splits), plan->tail != 0};
   if (c.splits > 1 && (!allow_split || !split_fits(c, g)))

@@ -158,6 +158,58 @@ def test_lds_kernel_rejects_unfit_shapes(backend, kind):
         backend.matmul_prepared_fused(torch.ones((4, 256), dtype=torch.int8, device=DEV), prepared, plan=lds)
 
 
+# residue-plane LDS kernel (kind 8): 128 x 128 tiles, one staging unit per
+# channel and pair of K steps, 4 or 6 channels
+PLANE_SHAPES = [(128 * 2 + 37, 256, 128 * 3 + 5), (300, 512, 100), (17, 1024, 64), (128 * 3, 768, 128 * 2),
+                (129, 256, 129), (640, 1024, 300)]
+
+
+@pytest.mark.parametrize("r", [4, 6])
+@pytest.mark.parametrize("m,k,n", PLANE_SHAPES)
+def test_lds_planes_kernel(backend, r, m, k, n):
+    # ragged M and N, one and several trips round the four slots (a trip is
+    # lcm(R, 4) units: one pair of K steps at R = 4, two at R = 6)
+    run_case(backend, SETS[r], m, k, n, dtype=torch.int16, seed=m + k + r, plan=(8, 0, 0, 0), repeat=2)
+
+
+def test_lds_planes_kernel_full_int16(backend):
+    # int16 x int16 over the whole range on the 6-channel set (the wide
+    # path's operands): exact int64 product
+    gen = torch.Generator().manual_seed(816)
+    m, k, n = 300, 1024, 260
+    a = torch.randint(-32767, 32768, (m, k), generator=gen, dtype=torch.int32).to(torch.int16)
+    b = torch.randint(-32767, 32768, (k, n), generator=gen, dtype=torch.int32).to(torch.int16)
+    prepared = backend.prepare_weight(b.to(DEV), SETS[6])
+    out = backend.matmul_prepared_fused(a.to(DEV), prepared, plan=(8, 0, 0, 0))
+    np.testing.assert_array_equal(out.cpu().numpy(), ro.exact_matmul(a.numpy(), b.numpy()))
+
+
+@pytest.mark.parametrize("r", [4, 6])
+def test_lds_planes_kernel_adaptive_prefix(backend, r):
+    # the device picks fewer channels: the loads of the rest re-read channel
+    # 0's planes and the epilogue reconstructs from the prefix
+    run_case(backend, SETS[r], 300, 512, 200, dtype=torch.int16, seed=r, adaptive=True, plan=(8, 0, 0, 0),
+             repeat=2)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_lds_planes_kernel_float_epilogue(backend, out_dtype):
+    run_case(backend, SETS[6], 300, 512, 130, dtype=torch.int16, seed=9, out_dtype=out_dtype, plan=(8, 0, 0, 0))
+
+
+def test_lds_planes_kernel_rejects_unfit_shapes(backend):
+    planes = (8, 0, 0, 0)
+    prepared = backend.prepare_weight(torch.ones((256, 16), dtype=torch.int8, device=DEV), SETS[6])
+    with pytest.raises(ValueError, match="no GEMM kernel"):  # raw int8 activations
+        backend.matmul_prepared_fused(torch.ones((4, 256), dtype=torch.int8, device=DEV), prepared, plan=planes)
+    prepared = backend.prepare_weight(torch.ones((320, 16), dtype=torch.int8, device=DEV), SETS[6])
+    with pytest.raises(ValueError, match="no GEMM kernel"):  # K not a multiple of 256
+        backend.matmul_prepared_fused(torch.ones((4, 320), dtype=torch.int16, device=DEV), prepared, plan=planes)
+    prepared = backend.prepare_weight(torch.ones((256, 16), dtype=torch.int8, device=DEV), SETS[3])
+    with pytest.raises(ValueError, match="no GEMM kernel"):  # 3-channel capacity
+        backend.matmul_prepared_fused(torch.ones((4, 256), dtype=torch.int16, device=DEV), prepared, plan=planes)
+
+
 @pytest.mark.parametrize("kind,mb,nb,ks,k", [(1, 1, 1, 4, 320), (1, 1, 2, 2, 320), (1, 2, 1, 1, 320),
                                              (2, 8, 2, 0, 320), (2, 2, 1, 0, 320), (3, 0, 0, 0, 512),
                                              (7, 0, 0, 0, 512)])

@@ -110,9 +110,22 @@ def test_gemm_plan_rules(shape, plan):
     assert gemm_plan(m, n, k, channels) == plan
 
 
+def test_gemm_plan_residue_plane_activations():
+    # int16 / int32 activations (encoded per channel) with 6 channels: the
+    # 128 x 128 LDS kernel once its tiles fill a round of the CUs
+    assert gemm_plan(512, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 1, 0)
+    assert gemm_plan(2048, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 1, 0)
+    assert gemm_plan(256, 16384, 1024, 5, raw_a=0) == (8, 0, 0, 0, 1, 0)   # 5 channels: capacity 6
+    assert gemm_plan(512, 12288, 4096, 6)[0] == 2                          # raw int8: MFMA kernel
+    assert gemm_plan(512, 4096, 4096, 6, raw_a=0)[0] == 2                  # 128 tiles: MFMA kernel
+    assert gemm_plan(128, 12288, 4096, 6, raw_a=0)[0] == 2                 # 128 rows or fewer
+    assert gemm_plan(512, 12288, 4096, 4, raw_a=0)[0] == 2                 # 4 channels: MFMA kernel
+
+
 def test_gemm_plan_rejects_bad_shapes():
     # residue-plane activations (K not a multiple of 16): never the LDS kernel
     assert gemm_plan(2048, 12288, 4104, raw_a=0)[0] == 2
+    assert gemm_plan(2048, 12288, 4104, 6, raw_a=0)[0] == 2
     for bad in ((0, 8, 8, 4), (8, 8, 8, 1), (8, 8, 8, 11)):
         with pytest.raises(ValueError):
             gemm_plan(*bad)
