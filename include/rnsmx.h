@@ -87,11 +87,11 @@ typedef struct rnsmx_moduli {
  * channels), 5 = the MFMA kernel with three column waves (tile 16*mb x
  * 48*nb; int8 activations read in place, up to 4 channels), 7 = the
  * LDS-staged kernel with 256 x 96 tiles (same conditions as 3), 8 = the
- * LDS-staged kernel for residue-plane activations (int16 / int32 inputs;
- * 128 x 128 tiles, 4- or 6-channel capacity, K a multiple of 256, never
- * split; mb, nb, ks ignored).
+ * LDS-staged kernel for residue-plane activations (int16 / int32 inputs,
+ * and packed weights; 128 x 128 tiles, 4- or 6-channel capacity, K a
+ * multiple of 256; mb, nb, ks ignored; splits and tail as for kind 3).
  * splits: workgroups splitting K per output tile (0 or 1 = none; up to 4
- * channels, and for the stream kernel ks = 1): each reduces its partial
+ * channels, 6 for kind 8, and for the stream kernel ks = 1): each reduces its partial
  * sums to residues, and the last to finish a tile reconstructs it.  tail:
  * split only the tiles past the last full round of 256 (the others run
  * whole, first).  A plan
@@ -301,16 +301,23 @@ int32_t rnsmx_matmul_residues_prepared(
  * two MFMAs per channel (activation residues of d_c a against hi, of a
  * against lo) and add 128 sum_k a_k per row.  Accumulators: 2 K 128
  * max(floor(m/2)) + 255 < 2^31 (else RNSMX_ERANGE).  Plans: kind 1 (stream,
- * mb 1 or 2, nb 1, ks 1-4) or 2 (MFMA, mb 2 or 4, nb 1), never split; NULL
+ * mb 1 or 2, nb 1, ks 1-4), 2 (MFMA, mb 2 or 4, nb 1) or 6 (channel rows,
+ * mb 1, 2, 4 or 8 token blocks), never split, or 8 (the residue-plane LDS
+ * kernel, K a multiple of 256, split as for the residue-plane entry); NULL
  * for the automatic one (rnsmx_packed_plan).  The workspace holds the
- * encoded activations (rnsmx_packed_workspace_bytes).
+ * encoded activations and the split exchange of the automatic plan
+ * (rnsmx_packed_workspace_bytes).
  */
 int32_t rnsmx_prepare_weight_packed(const void *b_nk_dev, int32_t dtype,
                                     int32_t n, int32_t k, int8_t *packed_dev,
                                     int32_t *absmax_dev, void *stream);
 
+/* Bytes of workspace rnsmx_matmul_packed_fused needs for an M x N x K
+ * product with `channels` moduli under `plan` (NULL: the automatic plan);
+ * -1 for a bad shape or a plan the call would reject. */
 int64_t rnsmx_packed_workspace_bytes(int64_t m, int64_t k, int64_t n,
-                                     int32_t channels);
+                                     int32_t channels,
+                                     const rnsmx_plan_t *plan);
 
 int32_t rnsmx_matmul_packed_fused(
     const void *a_dev, int32_t a_dtype, int32_t m, int32_t k, int32_t n,

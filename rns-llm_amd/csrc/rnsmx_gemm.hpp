@@ -974,33 +974,47 @@ constexpr bool stream_splits(int rcap, int mb, int nb) { return rcap <= 4 && nb 
 constexpr bool mfma_splits(int rcap, int mb, int nb) { return rcap <= 4 && nb == 1; }
 
 // One wave's part of the exchange, for a (16 MI) x (16 NJ) block of
-// accumulators per channel (RCAP <= 4).  slot = tile * waves + wave.
+// accumulators per channel: one residue byte per channel, four channels per
+// 32-bit word, XW = ceil(R / 4) words per element (chunk (i, j) of split s
+// is XW consecutive 1 KB blocks, word-major).  slot = tile * waves + wave.
 // Returns true in the wave that finishes the tile, whose acc then holds
 // sums congruent to the whole-K accumulators.
+template <int RCAP>
+constexpr int xchg_words() {
+  return (RCAP + 3) / 4;
+}
+
 template <int RCAP, int MI, int NJ>
 __device__ __forceinline__ bool split_exchange(KArgs<RCAP> &g, const Epi<RCAP> &e, i32x4 (&acc)[RCAP][MI][NJ],
                                                int64_t slot, int split) {
-  static_assert(RCAP <= 4, "one byte per channel in a 32-bit word");
-  constexpr int CH = MI * NJ;  // 1 KB chunks per wave and split
+  static_assert(RCAP <= 8, "at most two words of residue bytes per element");
+  constexpr int XW = xchg_words<RCAP>();
+  constexpr int CH = MI * NJ * XW;  // 1 KB blocks per wave and split
   const int lane = threadIdx.x & 63;
   const int S = g.splits;
   int8_t *base = g.xchg + slot * S * CH * 1024 + lane * 4;
+  auto block = [&](int s, int i, int j, int wd) {
+    return base + (static_cast<int64_t>(s) * CH + (i * NJ + j) * XW + wd) * 1024;
+  };
   // canonical residues of this split's partial sums
   static_for<MI>([&](auto I) {
     constexpr int i = decltype(I)::value;
     static_for<NJ>([&](auto J) {
       constexpr int j = decltype(J)::value;
-      i32x4 w;
-      static_for<4>([&](auto T) {
-        constexpr int t = decltype(T)::value;
-        uint32_t packed = 0;
-        static_for<RCAP>([&](auto C) {
-          constexpr int c = decltype(C)::value;
-          packed |= (reduce_acc<RCAP>(e, c, acc[c][i][j][t]) & 0xFFu) << (8 * c);
+      static_for<XW>([&](auto WD) {
+        constexpr int wd = decltype(WD)::value;
+        i32x4 w;
+        static_for<4>([&](auto T) {
+          constexpr int t = decltype(T)::value;
+          uint32_t packed = 0;
+          static_for<4>([&](auto B) {
+            constexpr int c = 4 * wd + decltype(B)::value;
+            if constexpr (c < RCAP) packed |= (reduce_acc<RCAP>(e, c, acc[c][i][j][t]) & 0xFFu) << (8 * (c % 4));
+          });
+          w[t] = static_cast<int32_t>(packed);
         });
-        w[t] = static_cast<int32_t>(packed);
+        store_coherent(block(split, i, j, wd), w);
       });
-      store_coherent(base + (static_cast<int64_t>(split) * CH + i * NJ + j) * 1024, w);
     });
   });
   wait_vm_all();
@@ -1012,25 +1026,25 @@ __device__ __forceinline__ bool split_exchange(KArgs<RCAP> &g, const Epi<RCAP> &
   // read G splits at a time, every load of a group issued before the first
   // is used (own split and splits past S read a valid slot and are masked).
   asm volatile("" ::: "memory");
+  auto add_word = [&](auto I, auto J, auto WD, auto T, uint32_t word) {
+    constexpr int i = decltype(I)::value, j = decltype(J)::value, wd = decltype(WD)::value, t = decltype(T)::value;
+    static_for<4>([&](auto B) {
+      constexpr int c = 4 * wd + decltype(B)::value;
+      if constexpr (c < RCAP) acc[c][i][j][t] += static_cast<int32_t>(byte_of(word, c % 4));
+    });
+  };
   if constexpr (CH > 8) {
-    // large wave tiles (192 accumulators): one row of NJ chunks in flight,
+    // large wave tiles (192 accumulators): one row of NJ blocks in flight,
     // so the loads need few registers next to the accumulators
     for (int s = 0; s < S; ++s) {
       if (s == split) continue;
       static_for<MI>([&](auto I) {
         constexpr int i = decltype(I)::value;
-        i32x4 w[NJ];
-        static_for<NJ>([&](auto J) {
-          w[J] = load_coherent(base + (static_cast<int64_t>(s) * CH + i * NJ + decltype(J)::value) * 1024);
-        });
-        static_for<NJ>([&](auto J) {
-          constexpr int j = decltype(J)::value;
-          static_for<4>([&](auto T) {
-            constexpr int t = decltype(T)::value;
-            static_for<RCAP>([&](auto C) {
-              constexpr int c = decltype(C)::value;
-              acc[c][i][j][t] += static_cast<int32_t>(byte_of(static_cast<uint32_t>(w[j][t]), c));
-            });
+        static_for<XW>([&](auto WD) {
+          i32x4 w[NJ];
+          static_for<NJ>([&](auto J) { w[J] = load_coherent(block(s, i, decltype(J)::value, decltype(WD)::value)); });
+          static_for<NJ>([&](auto J) {
+            static_for<4>([&](auto T) { add_word(I, J, WD, T, static_cast<uint32_t>(w[J][decltype(T)::value])); });
           });
         });
       });
@@ -1038,16 +1052,18 @@ __device__ __forceinline__ bool split_exchange(KArgs<RCAP> &g, const Epi<RCAP> &
     if (lane == 0) __hip_atomic_store(g.tickets + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return true;
   }
-  constexpr int G = CH >= 4 ? 1 : 4 / CH;  // at most 4 chunks (16 registers) in flight, or one split
+  constexpr int G = CH >= 4 ? 1 : 4 / CH;  // at most 4 blocks (16 registers) in flight, or one split
   for (int s0 = 0; s0 < S; s0 += G) {
-    i32x4 w[G][MI][NJ];
+    i32x4 w[G][MI][NJ][XW];
     static_for<G>([&](auto U) {
       constexpr int u = decltype(U)::value;
       const int s = min(s0 + u, S - 1);
       static_for<MI>([&](auto I) {
         static_for<NJ>([&](auto J) {
-          constexpr int i = decltype(I)::value, j = decltype(J)::value;
-          w[u][i][j] = load_coherent(base + (static_cast<int64_t>(s) * CH + i * NJ + j) * 1024);
+          static_for<XW>([&](auto WD) {
+            constexpr int i = decltype(I)::value, j = decltype(J)::value, wd = decltype(WD)::value;
+            w[u][i][j][wd] = load_coherent(block(s, i, j, wd));
+          });
         });
       });
     });
@@ -1056,13 +1072,10 @@ __device__ __forceinline__ bool split_exchange(KArgs<RCAP> &g, const Epi<RCAP> &
       const bool use = s0 + u < S && s0 + u != split;
       static_for<MI>([&](auto I) {
         static_for<NJ>([&](auto J) {
-          constexpr int i = decltype(I)::value, j = decltype(J)::value;
-          static_for<4>([&](auto T) {
-            constexpr int t = decltype(T)::value;
-            const uint32_t word = use ? static_cast<uint32_t>(w[u][i][j][t]) : 0u;
-            static_for<RCAP>([&](auto C) {
-              constexpr int c = decltype(C)::value;
-              acc[c][i][j][t] += static_cast<int32_t>(byte_of(word, c));
+          static_for<XW>([&](auto WD) {
+            static_for<4>([&](auto T) {
+              const i32x4 &x = w[u][decltype(I)::value][decltype(J)::value][decltype(WD)::value];
+              add_word(I, J, WD, T, use ? static_cast<uint32_t>(x[decltype(T)::value]) : 0u);
             });
           });
         });
@@ -2201,10 +2214,14 @@ __global__ __launch_bounds__(512) void lds_wide_kernel(const GemmArgsK<RCAP> arg
 // A wave's LDS reads per MFMA are those of a 64 x 32 tile (6 KB per 8
 // MFMAs, against 16 KB per 48 with raw int8 A): this kernel is bound by LDS
 // bandwidth and the MFMAs together, not by HBM or L2.
+// PK (packed weights): each channel takes two units per pair of K steps,
+// (a' planes, hi plane) then (a planes, lo plane), both accumulating into
+// the channel's sums (a' x hi + a x lo, as mfma_packed_kernel), so a trip is
+// lcm(2 R, 4) units; the row terms are added once before the epilogue.
 // ---------------------------------------------------------------------------
 constexpr int kPlBM = 128, kPlBN = 128;
 
-template <int RCAP>
+template <int RCAP, bool PK>
 __device__ __forceinline__ void lds_planes_body(KArgs<RCAP> &g, int8_t *smem, const int c_act, const WorkUnit wu) {
   static_assert(RCAP == 4 || RCAP == 6, "32 R accumulator registers");
   // (four waves of 64 x 64, one per SIMD with 512 registers, read 25 % fewer
@@ -2214,8 +2231,9 @@ __device__ __forceinline__ void lds_planes_body(KArgs<RCAP> &g, int8_t *smem, co
   constexpr int DU = 16 / NW, LU = 2 * DU;       // A (and B) loads per wave per unit; all loads
   constexpr int UA = 16 * 1024, UB = 16 * 1024;  // A and B parts of one unit
   constexpr int BAREA = S * UA;                  // the A parts of all slots, then the B parts
-  constexpr int TRIP = RCAP == 6 ? 12 : 4;       // lcm(R, S) units
-  constexpr int PAIRS = TRIP / RCAP;             // pairs of K steps per trip
+  constexpr int VC = PK ? 2 * RCAP : RCAP;       // units per pair of K steps
+  constexpr int TRIP = VC % S == 0 ? VC : (VC % 2 == 0 ? 2 * VC : 4 * VC);  // lcm(VC, S) units
+  constexpr int PAIRS = TRIP / VC;               // pairs of K steps per trip
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
@@ -2241,11 +2259,18 @@ __device__ __forceinline__ void lds_planes_body(KArgs<RCAP> &g, int8_t *smem, co
     bcol[u] = g.b + static_cast<int64_t>(min((n0 >> 4) + wave + (NW * u) % 8, nblk - 1)) * g.b_ld + kr.ks0 * 1024;
   });
   const int8_t *acol = g.a + kr.ks0 * 64;
-  int64_t aplane[RCAP], bplane[RCAP];
-  static_for<RCAP>([&](auto C) {
-    constexpr int c = decltype(C)::value;
-    aplane[c] = plane_off(c, c_act, g.a_cs);
-    bplane[c] = plane_off(c, c_act, g.b_cs);
+  // the planes of unit v of a pair: channel v (or, packed, channel v / 2
+  // with (a', hi) for even v and (a, lo) for odd v)
+  int64_t aplane[VC], bplane[VC];
+  static_for<VC>([&](auto V) {
+    constexpr int v = decltype(V)::value;
+    if constexpr (PK) {
+      aplane[v] = packed_plane_off<RCAP>(v % 2 == 0 ? RCAP + v / 2 : v / 2, c_act, g.mods.channels, g.a_cs);
+      bplane[v] = (v % 2) * g.b_cs;
+    } else {
+      aplane[v] = plane_off(v, c_act, g.a_cs);
+      bplane[v] = plane_off(v, c_act, g.b_cs);
+    }
   });
   const uint32_t boff = static_cast<uint32_t>(lane * 16);
   const uint32_t sbase = __builtin_amdgcn_readfirstlane(
@@ -2293,8 +2318,8 @@ __device__ __forceinline__ void lds_planes_body(KArgs<RCAP> &g, int8_t *smem, co
 
   // unit t of the trip starting at pair e0
   auto unit = [&](auto T, int e0) {
-    constexpr int t = decltype(T)::value, sl = t % S, c = t % RCAP, nsl = (t + 1) % S;
-    constexpr int t3 = t + 3, sl3 = t3 % S, c3 = t3 % RCAP, pe3 = t3 / RCAP;
+    constexpr int t = decltype(T)::value, sl = t % S, c = PK ? (t % VC) / 2 : t % VC, nsl = (t + 1) % S;
+    constexpr int t3 = t + 3, sl3 = t3 % S, c3 = t3 % VC, pe3 = t3 / VC;
     wait_vmcnt<LU>();
     __builtin_amdgcn_s_barrier();
     static_for<2>([&](auto ST) {
@@ -2328,7 +2353,7 @@ __device__ __forceinline__ void lds_planes_body(KArgs<RCAP> &g, int8_t *smem, co
   static_for<3>([&](auto T) {
     constexpr int t = decltype(T)::value;
     static_for<LU>([&](auto L) {
-      dma(std::integral_constant<int, t % S>{}, std::integral_constant<int, t % RCAP>{}, L, t / RCAP);
+      dma(std::integral_constant<int, t % S>{}, std::integral_constant<int, t % VC>{}, L, t / VC);
     });
   });
   // unit 0 landed
@@ -2345,6 +2370,10 @@ __device__ __forceinline__ void lds_planes_body(KArgs<RCAP> &g, int8_t *smem, co
   }
   // the loads issued for units past K land before the workgroup ends
   wait_vmcnt<0>();
+  const int rw0 = m0 + wm * (MI * 16), cw0 = n0 + wn * (NJ * 16);
+  if constexpr (PK) {
+    if (wu.split <= 0) add_packed_rows<RCAP, MI, NJ>(g, acc, rw0, c_act);
+  }
   // The epilogue's constants and column factors are read only now: with
   // 6 channels they would hold some 110 scalar registers (and the column
   // factors 4 vector registers) through the loop, which the accumulators
@@ -2353,13 +2382,52 @@ __device__ __forceinline__ void lds_planes_body(KArgs<RCAP> &g, int8_t *smem, co
   Epi<RCAP> e;
   load_epi<RCAP>(g, e, c_act);
   const int m_lim = g.m, n_lim = g.n;
-  const int rw0 = m0 + wm * (MI * 16), cw0 = n0 + wn * (NJ * 16);
+  if (wu.split >= 0 &&
+      !split_exchange<RCAP, MI, NJ>(g, e, acc, static_cast<int64_t>(wu.split_tile) * NW + wave, wu.split))
+    return;
   ColScale cs[NJ];
   static_for<NJ>([&](auto J) { cs[J] = col_scale<RCAP>(e, cw0 + decltype(J)::value * 16 + (lane & 15), n_lim); });
   register_epilogue<RCAP, MI, NJ>(g, e, c_act, acc, rw0, cw0, m_lim, n_lim, cs);
 }
 
-template <int RCAP>
+// Work unit of workgroup blockIdx.x for the residue-plane kernel.  Tile t
+// maps to (mt, nt) in groups of 4 row tiles: t walks the 4 rows of one
+// column tile, then the next column.  With each XCD's contiguous run of
+// units (xcd_order) a round of 32 workgroups on one XCD reads 4 A row tiles
+// and 8 B column tiles (12 x 3 MB over K at 6 channels) instead of, M-block
+// fastest at M = 2048, 16 and 2 (18): each A row tile is as large as a B
+// column tile here.  Tail split (as work_of): workgroups [0, split_from)
+// take the whole tiles; the others take (tile, split) units split-minor,
+// so both halves of a tile run on one XCD and exchange through its L2.
+template <typename G>
+__device__ __forceinline__ WorkUnit planes_work(G &g) {
+  constexpr int RG = 4;
+  const int tiles_m = g.tiles_m, tiles_n = g.tiles_n, whole = g.split_from;
+  const int b = blockIdx.x;
+  WorkUnit w{0, 0, -1, 0};
+  int t;
+  if (b < whole) {
+    t = xcd_order(b, whole);
+  } else {
+    const int u = xcd_order(b - whole, (tiles_m * tiles_n - whole) * g.splits);
+    w.split = u % g.splits;
+    t = whole + u / g.splits;
+  }
+  w.split_tile = t - whole;
+  const int grouped = tiles_m / RG * RG;  // rows in full groups
+  if (t < grouped * tiles_n) {
+    const int r = t % (RG * tiles_n);
+    w.nt = r / RG;
+    w.mt = t / (RG * tiles_n) * RG + r % RG;
+  } else {
+    const int r = t - grouped * tiles_n, h = tiles_m - grouped;
+    w.nt = r / h;
+    w.mt = grouped + r % h;
+  }
+  return w;
+}
+
+template <int RCAP, bool PK>
 __global__ __launch_bounds__(512) void lds_planes_kernel(const GemmArgsK<RCAP> args) {
   constexpr int SLOTS = kLdsStages * 32 * 1024;
   KArgs<RCAP> &g = kernel_args<GemmArgsK<RCAP>>();
@@ -2371,7 +2439,7 @@ __global__ __launch_bounds__(512) void lds_planes_kernel(const GemmArgsK<RCAP> a
   int8_t *spare = smem + SLOTS - 16 * 1024;
   const int c_act = __builtin_amdgcn_readfirstlane(
       active_channels<RCAP>(g, reinterpret_cast<int64_t *>(spare), reinterpret_cast<int *>(spare + 64), 512));
-  lds_planes_body<RCAP>(g, smem, c_act, work_of(g));
+  lds_planes_body<RCAP, PK>(g, smem, c_act, planes_work(g));
 }
 
 // ---------------------------------------------------------------------------
@@ -2496,7 +2564,8 @@ inline GemmGrid gemm_grid(const GemmChoice &c, int64_t m, int64_t n) {
 // The residue-plane LDS kernel: activations as per-channel planes (not raw
 // int8), 4 or 6 channels, K a multiple of 256 (whole trips), rows addressed
 // through 32-bit per-lane offsets within a plane.
-inline bool lds_planes_fits(const GemmArgs &g, bool araw, int rcap) {
+template <typename G>
+inline bool lds_planes_fits(const G &g, bool araw, int rcap) {
   const bool a_offsets_fit = static_cast<int64_t>(g.m) * g.a_ld < (int64_t{1} << 32) - 256;
   return !araw && (rcap == 4 || rcap == 6) && g.a_k == g.kp && g.kp % (64 * kLdsStages) == 0 && a_offsets_fit;
 }
@@ -2505,12 +2574,12 @@ template <int RCAP>
 bool launch_lds(const GemmArgs &host, bool araw, int kind, hipStream_t st) {
   if (kind == kLdsPlanes) {
     if constexpr (RCAP == 4 || RCAP == 6) {
-      if (!lds_planes_fits(host, araw, RCAP) || host.splits > 1) return false;
+      if (!lds_planes_fits(host, araw, RCAP)) return false;
       GemmArgsK<RCAP> g = compact_args<RCAP>(host);
       g.tiles_m = (g.m + kPlBM - 1) / kPlBM;
       g.tiles_n = (g.n + kPlBN - 1) / kPlBN;
-      const dim3 grid(static_cast<unsigned>(g.tiles_m * g.tiles_n));
-      hipLaunchKernelGGL((lds_planes_kernel<RCAP>), grid, dim3(512), 0, st, g);
+      const dim3 grid(static_cast<unsigned>(g.split_from + (g.tiles_m * g.tiles_n - g.split_from) * g.splits));
+      hipLaunchKernelGGL((lds_planes_kernel<RCAP, false>), grid, dim3(512), 0, st, g);
       return true;
     }
     return false;
@@ -2535,13 +2604,22 @@ bool launch_lds(const GemmArgs &host, bool araw, int kind, hipStream_t st) {
 
 // Packed-weight kernels: stream tiles of 16 or 32 rows, MFMA tiles of 32 or
 // 64 rows x 64 columns (ring depth 3 or 2: the 2R activation planes double
-// the register ring of A chunks), up to 6 channels.  Not split over
+// the register ring of A chunks), the residue-plane LDS kernel with two
+// units per channel; up to 6 channels.  Only the LDS kernel splits K over
 // workgroups.
 template <int RCAP>
 bool launch_packed(GemmArgsK<RCAP> g, const GemmChoice &c, hipStream_t st) {
   if constexpr (RCAP != 4 && RCAP != 6) {
     return false;
   } else {
+    if (c.kind == kLdsPlanes) {  // the one packed kernel that may split K
+      if (!lds_planes_fits(g, false, RCAP)) return false;
+      g.tiles_m = (g.m + kPlBM - 1) / kPlBM;
+      g.tiles_n = (g.n + kPlBN - 1) / kPlBN;
+      const dim3 grid(static_cast<unsigned>(g.split_from + (g.tiles_m * g.tiles_n - g.split_from) * g.splits));
+      hipLaunchKernelGGL((lds_planes_kernel<RCAP, true>), grid, dim3(512), 0, st, g);
+      return true;
+    }
     if (c.splits > 1) return false;
     if (c.kind == kRows && c.ks >= 1 && c.ks <= 4) {
       g.tiles_m = 1;
@@ -2572,6 +2650,7 @@ bool launch_packed(GemmArgsK<RCAP> g, const GemmChoice &c, hipStream_t st) {
 #undef RNSMX_STREAM_PK
       return false;
     }
+
     if (c.kind == kMfma && c.nb == 1 && (c.mb == 2 || c.mb == 4)) {
       g.tiles_m = (g.m + 16 * c.mb - 1) / (16 * c.mb);
       g.tiles_n = (g.n + 63) / 64;

@@ -739,8 +739,10 @@ static bool split_fits(const GemmChoice &c, const GemmArgs &g) {
   bool built;
   if (c.kind == kStream || c.kind == kStreamWide)
     built = stream_splits(rcap, c.mb, c.nb) && c.ks == 1;
+  else if (c.kind == kLdsPlanes)
+    built = rcap == 4 || rcap == 6;
   else if (is_lds(c.kind))
-    built = c.kind != kLdsPlanes && rcap <= 4;
+    built = rcap <= 4;
   else
     built = mfma_splits(rcap, c.mb, c.nb);
   return built && (gr.tiles - whole_tiles(c, gr.tiles)) * gr.waves <= kL1Ticket;
@@ -754,7 +756,8 @@ static int64_t xchg_bytes(const GemmChoice &c, const GemmArgs &g) {
   if (splits <= 1) return 0;
   const GemmGrid gr = gemm_grid(c, g.m, g.n);
   const int64_t parted = gr.tiles - whole_tiles(c, gr.tiles);
-  return round_up(parted * gr.waves * splits * gr.chunks * 1024, 256);
+  const int words = (rcap_for(g.mods.channels) + 3) / 4;  // residue words per element (xchg_words)
+  return round_up(parted * gr.waves * splits * gr.chunks * words * 1024, 256);
 }
 
 // The automatic split count for a choice of kernel and tile, from sweeps on
@@ -790,7 +793,7 @@ static int choose_splits(const GemmChoice &c, const GemmArgs &g) {
   const int64_t tiles = gemm_grid(c, g.m, g.n).tiles;
   const bool stream = c.kind == kStream || c.kind == kStreamWide;
   int s = 1;
-  if (c.kind == kLdsWide || c.kind == kLdsPlanes) return 1;  // never split (the wide one: where no tail split pays)
+  if (c.kind == kLdsWide) return 1;  // chosen only where no tail split pays
   if (is_lds(c.kind) && tiles >= 256) {
     const int64_t last = tiles - (tiles - 1) / 256 * 256;  // tiles of the last round
     if (last <= 128 && nk >= 32) {
@@ -813,7 +816,7 @@ static int choose_splits(const GemmChoice &c, const GemmArgs &g) {
 // stream choice that splits over workgroups runs one wave per workgroup.
 static GemmChoice auto_plan(const GemmArgs &g, bool araw, bool allow_split) {
   GemmChoice c = choose_gemm(g, araw);
-  if (!allow_split || rcap_for(g.mods.channels) > 4) return c;
+  if (!allow_split || (rcap_for(g.mods.channels) > 4 && c.kind != kLdsPlanes)) return c;
   GemmChoice t = c;
   if (t.kind == kStream || t.kind == kStreamWide) t.ks = 1;
   t.splits = choose_splits(c, g);
@@ -862,7 +865,8 @@ static int32_t launch_gemm(GemmArgs g, bool araw, const GemmChoice &c, uint32_t 
   const int64_t tiles = gemm_grid(c, g.m, g.n).tiles;
   g.split_from = static_cast<int32_t>(tiles);
   if (c.splits > 1) {
-    if (is_lds(c.kind) && !lds_kernel_fits(g, araw, rcap)) {
+    if (is_lds(c.kind) &&
+        !(c.kind == kLdsPlanes ? lds_planes_fits(g, araw, rcap) : lds_kernel_fits(g, araw, rcap))) {
       set_error("no GEMM kernel for kind %d, tile %d x %d, %d channels", c.kind, c.mb, c.nb, g.mods.channels);
       return RNSMX_EINVAL;
     }
@@ -941,6 +945,16 @@ static GemmChoice packed_auto(const GemmArgs &g) {
   GemmChoice c = choose_gemm(g, false);
   c.splits = 1;
   c.tail = 0;
+  // the residue-plane LDS kernel with two units per channel (a' x hi, a x
+  // lo) where its tiles fill a round of the CUs, with the residue-plane
+  // kernel's tail split
+  if (g.m > 128 && lds_planes_fits(g, false, rcap) &&
+      static_cast<int64_t>((g.m + kPlBM - 1) / kPlBM) * ((g.n + kPlBN - 1) / kPlBN) >= 256) {
+    GemmChoice t{kLdsPlanes, 0, 0, 0, 1, 1};
+    t.splits = choose_splits(t, g);
+    if (t.splits > 1 && split_fits(t, g)) return t;
+    return GemmChoice{kLdsPlanes, 0, 0, 0, 1, 0};
+  }
   c.nb = 1;
   if (c.kind == kStream || c.kind == kStreamWide) {
     c.kind = kStream;
@@ -968,17 +982,21 @@ static int32_t packed_plan_from(const rnsmx_plan_t *plan, const GemmArgs &g, Gem
   const bool mfma = plan->kind == kMfma && (plan->mb == 2 || plan->mb == 4) && plan->nb == 1;
   const bool rows = plan->kind == kRows && (plan->mb == 1 || plan->mb == 2 || plan->mb == 4 || plan->mb == 8) &&
                     plan->nb == 1 && plan->ks >= 1 && plan->ks <= 4;
-  if (!(stream || mfma || rows) || plan->splits > 1 || plan->tail != 0)
+  const bool lds = plan->kind == kLdsPlanes;
+  if (!(stream || mfma || rows || lds) || (!lds && (plan->splits > 1 || plan->tail != 0)))
     return fail(RNSMX_EINVAL, "packed weights run the stream kernel (16- or 32-row tiles), the MFMA kernel "
-                              "(32- or 64-row tiles) or the channel-row kernel (1, 2, 4 or 8 token blocks), one "
-                              "column block, K not split over workgroups");
+                              "(32- or 64-row tiles), the channel-row kernel (1, 2, 4 or 8 token blocks) or the "
+                              "residue-plane LDS kernel (kind 8), one column block, K split over "
+                              "workgroups only by the LDS kernel");
   if (rows) {
     const int tpb = 16 / (g.mods.channels <= 4 ? 4 : 6);
     if (g.m > plan->mb * tpb) return fail(RNSMX_EINVAL, "channel-row plan: more tokens than its blocks hold");
     if (g.kp * int64_t{384} * max_half(g.mods) > INT32_MAX)
       return fail(RNSMX_ERANGE, "channel-row plan: K * 384 * max(floor(m/2)) exceeds the int32 sums");
   }
-  c = GemmChoice{plan->kind, plan->mb, 1, stream || rows ? plan->ks : 0, 1, 0};
+  c = GemmChoice{plan->kind, plan->mb, 1, stream || rows ? plan->ks : 0, std::max(1, plan->splits), plan->tail != 0};
+  if (c.splits > 1 && !split_fits(c, g))
+    return fail(RNSMX_EINVAL, "this plan cannot split K over workgroups (channels or counters)");
   return RNSMX_OK;
 }
 
@@ -1398,7 +1416,7 @@ static PreparedLayout prepared_layout(bool araw, int64_t m, int64_t kp, int32_t 
 // Packed-weight workspace: [split counters (unused: never split)][2R
 // activation planes, then the int32 row terms [R][packed_corr_ld(M)]; or
 // (up to 32 tokens) 8 blocks of channel-row fragments][row L1 norms].
-static PreparedLayout packed_layout(int64_t m, int64_t kp, int32_t channels) {
+static PreparedLayout packed_layout(int64_t m, int64_t kp, int32_t channels, int64_t xchg) {
   PreparedLayout l{};
   l.a_res = kTicketBytes;
   // per-channel planes, or (up to 8 tokens) two blocks of channel-row fragments
@@ -1406,7 +1424,7 @@ static PreparedLayout packed_layout(int64_t m, int64_t kp, int32_t channels) {
   const int64_t rows = m <= kRowsMaxBlocks * 4 ? int64_t{kRowsMaxBlocks} * 2 * kp * 16 : 0;
   l.row_l1 = l.a_res + round_up(std::max(planes, rows), 256);
   l.xchg = l.row_l1 + round_up(8 * (m + 1), 256);  // the norms, then their maximum
-  l.total = l.xchg;
+  l.total = l.xchg + xchg;
   return l;
 }
 
@@ -1476,7 +1494,8 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
   g.mods = *mods;
   GemmChoice c{};
   if (int32_t rc = packed ? packed_plan_from(plan, g, c) : plan_from(plan, g, araw, true, c)) return rc;
-  const PreparedLayout l = packed ? packed_layout(m, kp, R) : prepared_layout(araw, m, kp, R, xchg_bytes(c, g));
+  const PreparedLayout l = packed ? packed_layout(m, kp, R, xchg_bytes(c, g))
+                                  : prepared_layout(araw, m, kp, R, xchg_bytes(c, g));
   if (workspace_bytes < l.total) {
     set_error("workspace too small: %lld < %lld bytes", static_cast<long long>(workspace_bytes),
               static_cast<long long>(l.total));
@@ -1561,11 +1580,16 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
   return launch_gemm(g, araw, c, reinterpret_cast<uint32_t *>(ws), ws + l.xchg, st, packed);
 }
 
-int64_t rnsmx_packed_workspace_bytes(int64_t m, int64_t k, int64_t n, int32_t channels) {
+int64_t rnsmx_packed_workspace_bytes(int64_t m, int64_t k, int64_t n, int32_t channels,
+                                     const rnsmx_plan_t *plan) {
   if (m < 0 || k < 0 || n < 0 || channels < 1 || channels > kPackedMaxChannels || m > INT32_MAX ||
       n > INT32_MAX || k > INT32_MAX - 63)
     return -1;
-  return packed_layout(m, round_up(std::max<int64_t>(k, 1), RNSMX_K_ALIGN), channels).total;
+  const GemmArgs g = plan_args(std::max<int64_t>(m, 1), std::max<int64_t>(n, 1), std::max<int64_t>(k, 1), channels,
+                               false);
+  GemmChoice c{};
+  if (packed_plan_from(plan, g, c) != RNSMX_OK) return -1;
+  return packed_layout(m, g.kp, channels, xchg_bytes(c, g)).total;
 }
 
 int32_t rnsmx_matmul_prepared_fused(const void *a_dev, int32_t a_dtype, int32_t m, int32_t k, int32_t n,
@@ -1736,7 +1760,7 @@ int32_t rnsmx_packed_plan(int64_t m, int64_t n, int64_t k, int32_t channels, rns
     return fail(RNSMX_EINVAL, "gemm plan needs 1 <= M, N, K < 2^31");
   if (channels < 2 || channels > kPackedMaxChannels) return fail(RNSMX_EINVAL, "packed plan needs 2..6 channels");
   const GemmChoice c = packed_auto(plan_args(m, n, k, channels, false));
-  *out = rnsmx_plan_t{c.kind, c.mb, c.nb, c.ks, 1, 0};
+  *out = rnsmx_plan_t{c.kind, c.mb, c.nb, c.ks, c.splits, c.tail};
   return RNSMX_OK;
 }
 

@@ -146,7 +146,7 @@ _SIGNATURES = {
                ctypes.POINTER(Epilogue), _P, _P]),
     "rnsmx_gemm_plan": (_I32, [_I64, _I64, _I64, _I32, _I32, ctypes.POINTER(Plan)]),
     "rnsmx_prepare_weight_packed": (_I32, [_P, _I32, _I32, _I32, _P, _P, _P]),
-    "rnsmx_packed_workspace_bytes": (_I64, [_I64, _I64, _I64, _I32]),
+    "rnsmx_packed_workspace_bytes": (_I64, [_I64, _I64, _I64, _I32, ctypes.POINTER(Plan)]),
     "rnsmx_matmul_packed_fused": (
         _I32, [_P, _I32, _I32, _I32, _I32, _P, ctypes.POINTER(Moduli), _P, _I32,
                ctypes.POINTER(Adaptive), ctypes.POINTER(Epilogue), ctypes.POINTER(Plan),

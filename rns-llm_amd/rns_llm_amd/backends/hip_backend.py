@@ -507,12 +507,15 @@ class HipRNSBackend:
             self._ws_bytes[key] = nbytes
         return nbytes
 
-    def _packed_workspace_bytes(self, m: int, k: int, n: int, channels: int) -> int:
-        key = ("packed", m, k, n, channels)
+    def _packed_workspace_bytes(self, m: int, k: int, n: int, channels: int, plan) -> int:
+        key = ("packed", m, k, n, channels, None if plan is None else plan.as_tuple())
         nbytes = self._ws_bytes.get(key)
         if nbytes is None:
-            nbytes = int(self._lib.rnsmx_packed_workspace_bytes(m, k, n, channels))
+            nbytes = int(self._lib.rnsmx_packed_workspace_bytes(
+                m, k, n, channels, None if plan is None else ctypes.byref(plan)))
             if nbytes < 0:
+                if plan is not None:  # the call itself reports why the plan does not fit
+                    return self._packed_workspace_bytes(m, k, n, channels, None)
                 raise ValueError("bad workspace shape")
             self._ws_bytes[key] = nbytes
         return nbytes
@@ -750,7 +753,7 @@ class HipRNSBackend:
         plan = _native.make_plan(plan)
         packed_form = prepared.form == "packed"
         if packed_form:
-            scratch = self._scratch(workspace, self._packed_workspace_bytes(m, k, n, channels))
+            scratch = self._scratch(workspace, self._packed_workspace_bytes(m, k, n, channels, plan))
         else:
             scratch = self._scratch(workspace, self._prepared_workspace_bytes(m, k, n, channels, plan))
         epi = None

@@ -197,6 +197,34 @@ def test_lds_planes_kernel_float_epilogue(backend, out_dtype):
     run_case(backend, SETS[6], 300, 512, 130, dtype=torch.int16, seed=9, out_dtype=out_dtype, plan=(8, 0, 0, 0))
 
 
+@pytest.mark.parametrize("r", [4, 6])
+@pytest.mark.parametrize("m,k,n,splits", [(300, 1024, 100, 2), (129, 2048, 260, 4)])
+def test_split_k_lds_planes_kernel(backend, r, m, k, n, splits):
+    # every tile's K range over `splits` workgroups: residue bytes of up to 6
+    # channels exchanged in two words per element, twice on one workspace
+    run_case(backend, SETS[r], m, k, n, dtype=torch.int16, seed=m + splits + r, plan=(8, 0, 0, 0, splits),
+             repeat=2)
+
+
+@pytest.mark.parametrize("r", [4, 6])
+def test_tail_split_lds_planes_kernel(backend, r):
+    # 3 x 86 = 258 tiles: 256 run whole, the last 2 split K in two halves
+    gen = torch.Generator().manual_seed(258 + r)
+    m, k, n = 300, 512, 128 * 86 - 5
+    a = torch.randint(-2000, 2001, (m, k), generator=gen, dtype=torch.int32).to(torch.int16)
+    b = torch.randint(-127, 128, (k, n), generator=gen, dtype=torch.int32).to(torch.int8)
+    prepared = backend.prepare_weight(b.to(DEV), SETS[r])
+    ws = backend.create_workspace(device=torch.device(DEV), channels=r, m=m, n=n, k=k)
+    whole = backend.matmul_prepared_fused(a.to(DEV), prepared, workspace=ws, plan=(8, 0, 0, 0)).cpu()
+    for _ in range(2):
+        split = backend.matmul_prepared_fused(a.to(DEV), prepared, workspace=ws, plan=(8, 0, 0, 0, 2, 1)).cpu()
+        assert torch.equal(split, whole)
+    rows = [0, 127, 128, 299]
+    np.testing.assert_array_equal(whole[rows].numpy(), ro.exact_matmul(a[rows].numpy(), b.numpy()))
+    cols = slice(128 * 85 - 7, n)  # the split tiles' columns
+    np.testing.assert_array_equal(whole[:, cols].numpy(), ro.exact_matmul(a.numpy(), b[:, cols].numpy()))
+
+
 def test_lds_planes_kernel_rejects_unfit_shapes(backend):
     planes = (8, 0, 0, 0)
     prepared = backend.prepare_weight(torch.ones((256, 16), dtype=torch.int8, device=DEV), SETS[6])

@@ -101,6 +101,45 @@ def test_packed_every_plan_and_activation_type(backend, plan, moduli, a_dtype):
     assert torch.equal(out.cpu(), exact(a.to(torch.int32), w))
 
 
+# the residue-plane LDS kernel (kind 8) on packed weights: two staging units
+# per channel (a' x hi, a x lo), row terms added before the epilogue
+@pytest.mark.parametrize("m,k,n", [(300, 512, 200), (129, 256, 129), (128 * 2 + 37, 1024, 128 * 3 + 5)])
+@pytest.mark.parametrize("moduli", [DENSE4, DENSE5, DENSE6], ids=["r4", "r5", "r6"])
+@pytest.mark.parametrize("a_dtype", [torch.int8, torch.int16, torch.int32])
+def test_packed_lds_kernel(backend, m, k, n, moduli, a_dtype):
+    # the worst-case sums must fit the set: K * a_lim * 32768 < P / 2
+    a_lim = 16 if len(moduli) == 4 else 127 if a_dtype == torch.int8 else 2047 if len(moduli) == 5 else 32767
+    a = ints((m, k), -a_lim, a_lim, m + k + len(moduli), a_dtype)
+    w = ints((n, k), -32768, 32767, n + len(moduli))
+    a[0, :8] = -a_lim
+    w[0, :8] = -32768
+    prepared = backend.prepare_weight_packed_nk(w.to(DEV), moduli)
+    ws = backend.create_workspace(device=torch.device(DEV), channels=len(moduli), m=m, n=n)
+    for _ in range(2):
+        out = backend.matmul_prepared_fused(a.to(DEV), prepared, workspace=ws, plan=(8, 0, 0, 0))
+        assert torch.equal(out.cpu(), exact(a.to(torch.int32), w))
+
+
+@pytest.mark.parametrize("moduli", [DENSE4, DENSE6], ids=["r4", "r6"])
+def test_packed_lds_kernel_split(backend, moduli):
+    # 3 x 86 = 258 tiles: the tail split (the last 2 tiles in two halves of
+    # K) and a split of every tile, both equal to the whole-K product; the
+    # row terms are added by one half only
+    m, k, n = 300, 512, 128 * 86 - 5
+    a_lim = 16 if len(moduli) == 4 else 32767
+    a = ints((m, k), -a_lim, a_lim, 17 + len(moduli))
+    w = ints((n, k), -32768, 32767, 19 + len(moduli))
+    prepared = backend.prepare_weight_packed_nk(w.to(DEV), moduli)
+    ws = backend.create_workspace(device=torch.device(DEV), channels=len(moduli), m=m, n=n)
+    whole = backend.matmul_prepared_fused(a.to(DEV), prepared, workspace=ws, plan=(8, 0, 0, 0)).cpu()
+    for plan in ((8, 0, 0, 0, 2, 1), (8, 0, 0, 0, 2, 1), (8, 0, 0, 0, 2)):
+        assert torch.equal(backend.matmul_prepared_fused(a.to(DEV), prepared, workspace=ws, plan=plan).cpu(), whole)
+    rows = [0, 127, 128, 299]
+    assert torch.equal(whole[rows], exact(a[rows].to(torch.int32), w))
+    cols = slice(128 * 85 - 7, n)
+    assert torch.equal(whole[:, cols], exact(a.to(torch.int32), w[cols]))
+
+
 # decode: the channel-row kernel (kind 6) with 1, 2, 4 or 8 blocks of 16 / R
 # tokens, every wave count, ragged N and K, three activation types
 ROW_CASES = [(DENSE6, 1), (DENSE6, 2), (DENSE6, 3), (DENSE6, 4), (DENSE6, 7), (DENSE6, 16), (DENSE4, 1),

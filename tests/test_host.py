@@ -113,8 +113,8 @@ def test_gemm_plan_rules(shape, plan):
 def test_gemm_plan_residue_plane_activations():
     # int16 / int32 activations (encoded per channel) with 6 channels: the
     # 128 x 128 LDS kernel once its tiles fill a round of the CUs
-    assert gemm_plan(512, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 1, 0)
-    assert gemm_plan(2048, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 1, 0)
+    assert gemm_plan(512, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 2, 1)   # 384 tiles: the last 128 split
+    assert gemm_plan(2048, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 1, 0)  # six full rounds
     assert gemm_plan(256, 16384, 1024, 5, raw_a=0) == (8, 0, 0, 0, 1, 0)   # 5 channels: capacity 6
     assert gemm_plan(512, 12288, 4096, 6)[0] == 2                          # raw int8: MFMA kernel
     assert gemm_plan(512, 4096, 4096, 6, raw_a=0)[0] == 2                  # 128 tiles: MFMA kernel
@@ -229,7 +229,9 @@ def packed_plan(m, n, k, channels=6):
 # tokens (kind 6, mb = blocks, a power of two), then the stream kernel where the
 # residue-plane choice takes it (16- or 32-row tiles, K over as many waves
 # as chunks allow, at most 4), else the MFMA kernel with 32- or 64-row
-# tiles (fewest rows per CU, 64 on a tie); never split
+# tiles (fewest rows per CU, 64 on a tie), or from 129 rows and one round
+# of 128 x 128 tiles (K a multiple of 256) the residue-plane LDS kernel;
+# never split
 PACKED_PLANS = [
     ((1, 12288, 4096, 6), (6, 1, 1, 4, 1, 0)),   # decode: channel rows, chunks of 8 steps, 4 waves
     ((1, 768, 768, 6), (6, 1, 1, 2, 1, 0)),
@@ -244,7 +246,11 @@ PACKED_PLANS = [
     ((1, 768, 50_000, 6), (1, 1, 1, 4, 1, 0)),   # K past the channel-row sums' int32 range
     ((96, 2304, 768, 6), (1, 2, 1, 4, 1, 0)),    # 432 stream tiles of 32 x 16
     ((100, 2304, 768, 6), (2, 2, 1, 0, 1, 0)),   # MFMA: 144 tiles of 32 rows beat 72 of 64
-    ((1024, 4096, 1024, 6), (2, 4, 1, 0, 1, 0)),  # 256 rows per CU either way: 64
+    ((1024, 4096, 1100, 6), (2, 4, 1, 0, 1, 0)),  # 256 rows per CU either way: 64 (K not 256-aligned)
+    ((1024, 4096, 1024, 6), (8, 0, 0, 0, 1, 0)),  # residue-plane LDS kernel: 256 tiles of 128 x 128
+    ((512, 12288, 4096, 6), (8, 0, 0, 0, 2, 1)),  # 384 tiles: the last 128 split K in two
+    ((1024, 4096, 1000, 4), (8, 0, 0, 0, 1, 0)),  # K = 1000 padded to 1024
+    ((1024, 2048, 1024, 6), (2, 4, 1, 0, 1, 0)),  # 128 tiles: MFMA kernel
 ]
 
 
@@ -258,11 +264,11 @@ def test_packed_queries_and_rejects_without_gpu():
     tickets = 4 * _native.SPLIT_TICKETS
     # counters + the larger of (2R activation planes + int32 row terms [R][round_up(M, 64) + 64])
     # and (up to 32 tokens) eight blocks of channel-row fragments [2][kp/64][1 KB] + row norms
-    assert lib.rnsmx_packed_workspace_bytes(1, 768, 768, 6) == tickets + max(
+    assert lib.rnsmx_packed_workspace_bytes(1, 768, 768, 6, None) == tickets + max(
         2 * 6 * 768 + 4 * 6 * 128, 8 * 2 * 768 * 16) + 256
-    assert lib.rnsmx_packed_workspace_bytes(100, 100, 37, 5) == (
+    assert lib.rnsmx_packed_workspace_bytes(100, 100, 37, 5, None) == (
         tickets + (2 * 5 * 100 * 128 + 4 * 5 * 192 + 255) // 256 * 256 + (8 * 100 + 255) // 256 * 256)
-    assert lib.rnsmx_packed_workspace_bytes(1, 768, 768, 7) == -1
+    assert lib.rnsmx_packed_workspace_bytes(1, 768, 768, 7, None) == -1
     out = _native.Plan()
     assert lib.rnsmx_packed_plan(1, 768, 768, 7, ctypes.byref(out)) == _native.EINVAL
     x = ctypes.c_int64(0)
