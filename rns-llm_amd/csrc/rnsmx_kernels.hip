@@ -638,9 +638,14 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
     c.kind = wide ? kLdsWide : kLds;
     return c;
   }
-  // Residue-plane activations with 6 channels (int16 / int32 inputs): the
-  // 128 x 128 LDS-staged kernel once its tiles fill a round of the CUs.
-  if (g.m > 128 && rcap == 6 && lds_planes_fits(g, araw, rcap) && tiles(kPlBM, kPlBN) >= 256) {
+  // Residue-plane activations (int16 / int32 inputs) with 4 or 6 channels:
+  // the 128 x 128 LDS-staged kernel from 64 rows, given 4096 tile-steps of
+  // work (int16 x int8, K = 4096, 6 channels: M=64 N=12288 81 us with K in
+  // two halves against 111 with the MFMA kernel, M=128 94 against 205,
+  // M=256 123 against 304, M=512 N=4096 84 against 210; 4 channels M=2048
+  // N=12288 472 against 886; K = 768, N = 2304: M=4096 81 against 108, but
+  // M=256 (36 tiles, 12 steps) 28.5 against 19.6, so not there).
+  if (g.m >= 64 && lds_planes_fits(g, araw, rcap) && tiles(kPlBM, kPlBN) * nk >= 4096) {
     c.kind = kLdsPlanes;
     return c;
   }
@@ -794,6 +799,14 @@ static int choose_splits(const GemmChoice &c, const GemmArgs &g) {
   const bool stream = c.kind == kStream || c.kind == kStreamWide;
   int s = 1;
   if (c.kind == kLdsWide) return 1;  // chosen only where no tail split pays
+  if (c.kind == kLdsPlanes && tiles < 256) {
+    // fewer tiles than CUs: split K over as many workgroups as one round
+    // holds, keeping 16 K steps per split (M=512 N=4096 K=4096: 128 tiles,
+    // 84 us in two halves against 114 whole; 192 tiles split in two, 1.5
+    // rounds, lose: 156 against 123)
+    while (2 * s * tiles <= 256 && nk / (2 * s) >= 16 && s < 8) s *= 2;
+    return s;
+  }
   if (is_lds(c.kind) && tiles >= 256) {
     const int64_t last = tiles - (tiles - 1) / 256 * 256;  // tiles of the last round
     if (last <= 128 && nk >= 32) {
@@ -946,11 +959,11 @@ static GemmChoice packed_auto(const GemmArgs &g) {
   c.splits = 1;
   c.tail = 0;
   // the residue-plane LDS kernel with two units per channel (a' x hi, a x
-  // lo) where its tiles fill a round of the CUs, with the residue-plane
-  // kernel's tail split
-  if (g.m > 128 && lds_planes_fits(g, false, rcap) &&
-      static_cast<int64_t>((g.m + kPlBM - 1) / kPlBM) * ((g.n + kPlBN - 1) / kPlBN) >= 256) {
-    GemmChoice t{kLdsPlanes, 0, 0, 0, 1, 1};
+  // lo) under the rule and split of residue-plane weights
+  const int64_t pl_tiles = static_cast<int64_t>((g.m + kPlBM - 1) / kPlBM) * ((g.n + kPlBN - 1) / kPlBN);
+  if (g.m >= 64 && lds_planes_fits(g, false, rcap) && pl_tiles * (g.kp / 64) >= 4096) {
+    const int64_t tiles = pl_tiles;
+    GemmChoice t{kLdsPlanes, 0, 0, 0, 1, tiles >= 256};
     t.splits = choose_splits(t, g);
     if (t.splits > 1 && split_fits(t, g)) return t;
     return GemmChoice{kLdsPlanes, 0, 0, 0, 1, 0};

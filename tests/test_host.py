@@ -111,15 +111,23 @@ def test_gemm_plan_rules(shape, plan):
 
 
 def test_gemm_plan_residue_plane_activations():
-    # int16 / int32 activations (encoded per channel) with 6 channels: the
-    # 128 x 128 LDS kernel once its tiles fill a round of the CUs
+    # int16 / int32 activations (encoded per channel) with 4 or 6 channels:
+    # the 128 x 128 LDS kernel from 129 rows (K a multiple of 256)
     assert gemm_plan(512, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 2, 1)   # 384 tiles: the last 128 split
     assert gemm_plan(2048, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 1, 0)  # six full rounds
     assert gemm_plan(256, 16384, 1024, 5, raw_a=0) == (8, 0, 0, 0, 1, 0)   # 5 channels: capacity 6
+    assert gemm_plan(512, 12288, 4096, 4, raw_a=0) == (8, 0, 0, 0, 2, 1)   # 4 channels
+    assert gemm_plan(512, 4096, 4096, 6, raw_a=0) == (8, 0, 0, 0, 2, 0)    # 128 tiles: every tile in two
+    assert gemm_plan(256, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 1, 0)   # 192 tiles: no split
+    assert gemm_plan(256, 4096, 1024, 6, raw_a=0)[0] == 2                  # 64 tiles x 16 steps: MFMA kernel
+    assert gemm_plan(1024, 4096, 1024, 6, raw_a=0) == (8, 0, 0, 0, 1, 0)   # 256 tiles x 16 steps
     assert gemm_plan(512, 12288, 4096, 6)[0] == 2                          # raw int8: MFMA kernel
-    assert gemm_plan(512, 4096, 4096, 6, raw_a=0)[0] == 2                  # 128 tiles: MFMA kernel
-    assert gemm_plan(128, 12288, 4096, 6, raw_a=0)[0] == 2                 # 128 rows or fewer
-    assert gemm_plan(512, 12288, 4096, 4, raw_a=0)[0] == 2                 # 4 channels: MFMA kernel
+    assert gemm_plan(64, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 2, 0)    # 96 tiles: K in two halves
+    assert gemm_plan(128, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 2, 0)
+    assert gemm_plan(48, 12288, 4096, 6, raw_a=0)[0] == 2                  # under 64 rows
+    assert gemm_plan(256, 2304, 768, 4, raw_a=0)[0] != 8                   # 36 tiles x 12 steps: too little work
+    assert gemm_plan(4096, 2304, 768, 4, raw_a=0) == (8, 0, 0, 0, 1, 0)    # 576 tiles
+    assert gemm_plan(512, 12288, 4096, 3, raw_a=0)[0] == 2                 # 3-channel capacity
 
 
 def test_gemm_plan_rejects_bad_shapes():
@@ -229,9 +237,9 @@ def packed_plan(m, n, k, channels=6):
 # tokens (kind 6, mb = blocks, a power of two), then the stream kernel where the
 # residue-plane choice takes it (16- or 32-row tiles, K over as many waves
 # as chunks allow, at most 4), else the MFMA kernel with 32- or 64-row
-# tiles (fewest rows per CU, 64 on a tie), or from 129 rows and one round
-# of 128 x 128 tiles (K a multiple of 256) the residue-plane LDS kernel;
-# never split
+# tiles (fewest rows per CU, 64 on a tie), or from 129 rows the
+# residue-plane LDS kernel (K a multiple of 256), split over K as for
+# residue-plane weights; the others never split
 PACKED_PLANS = [
     ((1, 12288, 4096, 6), (6, 1, 1, 4, 1, 0)),   # decode: channel rows, chunks of 8 steps, 4 waves
     ((1, 768, 768, 6), (6, 1, 1, 2, 1, 0)),
@@ -250,7 +258,8 @@ PACKED_PLANS = [
     ((1024, 4096, 1024, 6), (8, 0, 0, 0, 1, 0)),  # residue-plane LDS kernel: 256 tiles of 128 x 128
     ((512, 12288, 4096, 6), (8, 0, 0, 0, 2, 1)),  # 384 tiles: the last 128 split K in two
     ((1024, 4096, 1000, 4), (8, 0, 0, 0, 1, 0)),  # K = 1000 padded to 1024
-    ((1024, 2048, 1024, 6), (2, 4, 1, 0, 1, 0)),  # 128 tiles: MFMA kernel
+    ((1024, 2048, 1024, 6), (2, 4, 1, 0, 1, 0)),  # 128 tiles x 16 K steps: too little work, MFMA kernel
+    ((512, 4096, 4096, 6), (8, 0, 0, 0, 2, 0)),   # 128 tiles, 64 K steps: every tile in two
 ]
 
 
