@@ -72,6 +72,31 @@ def test_noalloc_drops_a_split_that_does_not_fit(backend):
     assert torch.equal(want[rows].double(), exact)
 
 
+def test_noalloc_residue_planes_drop_the_split(backend):
+    # int16 activations, 6 channels, C5 M=512: the automatic plan is the
+    # residue-plane LDS kernel with its tail split, whose exchange (two words
+    # per element) does not fit the static scratch next to the 12 MiB of
+    # activation planes; the no-allocation entry point runs it unsplit
+    m, k, n = 512, 4096, 12288
+    mods = (255, 253, 251, 247, 241, 239)
+    auto = _native.Plan()
+    _native.check(backend._lib.rnsmx_gemm_plan(m, n, k, 6, 0, ctypes.byref(auto)))
+    assert auto.as_tuple() == (8, 0, 0, 0, 2, 1)
+    assert backend._lib.rnsmx_prepared_workspace_bytes(m, k, n, 6, None) > 16 << 20
+    gen = torch.Generator(device=DEV).manual_seed(512)
+    w = torch.randint(-127, 128, (n, k), generator=gen, device=DEV, dtype=torch.int8)
+    a = torch.randint(-3000, 3001, (m, k), generator=gen, device=DEV, dtype=torch.int32).to(torch.int16)
+    prepared = backend.prepare_weight_nk(w, mods)
+    want = backend.matmul_prepared_fused(a, prepared).clone()
+    for mm in (m, 200):  # the second call smaller
+        out = torch.full((mm, n), -1, dtype=torch.int64, device=DEV)
+        _native.check(noalloc_call(backend, a[:mm].contiguous(), prepared, out))
+        torch.cuda.synchronize()
+        assert torch.equal(out, want[:mm])
+    rows = torch.arange(0, m, 29, device=DEV)
+    assert torch.equal(want[rows].double(), a[rows].double() @ w.double().t())
+
+
 def test_noalloc_rejects_oversize_without_launch(backend):
     # int16 activations need R * M * kp bytes of residue planes: 4 * 8192 *
     # 1024 = 32 MiB > 16 MiB
