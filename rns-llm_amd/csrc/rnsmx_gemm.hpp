@@ -860,7 +860,10 @@ __device__ __forceinline__ int xcd_order(int b, int total) {
 // split tiles (the exchange slot).  Workgroups [0, split_from) take the
 // whole tiles [0, split_from): they are dispatched first and spread over
 // every XCD.  The rest take (tile, split) units of the tiles from
-// split_from on, split-major.
+// split_from on, split-minor: with each XCD's contiguous run of units, the
+// splits of one tile run on one XCD and exchange their residues through
+// its L2 (split-major put the halves of a tile on different XCDs, so the
+// exchange went through the MALL).
 struct WorkUnit {
   int mt, nt, split, split_tile;
 };
@@ -878,8 +881,8 @@ __device__ __forceinline__ WorkUnit work_of(G &g) {
   } else {
     const int parted = tiles - whole;
     const int u = xcd_order(b - whole, parted * g.splits);
-    w.split = u / parted;
-    t = whole + (u - w.split * parted);
+    w.split = u % g.splits;
+    t = whole + u / g.splits;
   }
   w.mt = t % g.tiles_m;
   w.nt = t / g.tiles_m;
