@@ -855,7 +855,8 @@ def main():
         f"{head['us_per_call_p50']:.2f} us, {head['eff_tops']:.1f} eff TOPS")
     rows = [head]
     if not args.no_extra:
-        extra = [("C2 fused QKV", m, 768, 768, 3, 17) for m in (1, 16, 128)]
+        extra = [("C1 single RNSLinear shape", 128, 768, 768, 1, 11)]  # the CPU baseline's shape
+        extra += [("C2 fused QKV", m, 768, 768, 3, 17) for m in (1, 16, 128)]
         extra += [(f"C3 decode {q} requests", q, 768, 768, 1, 33) for q in (1, 2, 4)]
         extra += [("C5 OPT-6.7B QKV", m, 4096, 4096, 3, 67) for m in (1, 512, 2048)]
         extra += [("C5 OPT-6.7B QKV adaptive", m, 4096, 4096, 3, 67) for m in (1, 2048)]
