@@ -580,7 +580,9 @@ static int stream_ks_cap(int rcap, int mb, int nb) {
 // 128 x 128 tiles once they give >= 1024 workgroups (their weight reuse then
 // pays for one wave per SIMD), else 32, 48 or 64 x 64 (or x 48) tiles,
 // the one that leaves the fewest rows on any CU.
-static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
+// packed: packed weights (packed_auto), which keep the raw-activation row
+// rule of the stream kernel (their stream kernel reads two weight planes).
+static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false) {
   const int rcap = rcap_for(g.mods.channels);
   const int nk = g.kp / 64;
   auto tiles = [&](int bm, int bn) {
@@ -595,15 +597,32 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
   // 9.6, N=4608 10.3 against 14.0, K=4096 N=12288 62 against 110; at
   // N=768, 192 tiles, 5.1 against 7.4; at M=96, N=2304, 432 tiles, 7.6
   // against 8.7).
+  // Residue-plane activations (int16 / int32 inputs) make every stream wave
+  // load each channel's A fragment as well (as many bytes as the weight
+  // residues at M <= 16, against one shared fragment for raw int8), and
+  // past 4 channels the stream kernel has no 8-step chunks; there it pays
+  // only up to 48 rows while the MFMA kernel's 32 x 64 tiles number under
+  // 128.  Residue planes, K=4096, 6 channels: N=12288 M=1/16 65/68 us with
+  // the MFMA kernel against 81/98, N=8192 M=16 60 against 70, N=4096 M=16
+  // 39 with the stream kernel against 54, M=64 60 with the MFMA kernel
+  // against 105; K=768, N=2304: M=16 12.6 stream against 17.2, M=48 12.5
+  // against 13.8 (4 channels), M=64 18.9 MFMA against 24.1, M=96 19.0
+  // against 30.8.  Raw int8, 6 channels, K=4096: N=12288 M=1/16 58/58
+  // MFMA against 67/72, N=4096 M=1/32 27/30 stream against 35/39.
   const bool long_k = nk > 16;
-  const bool stream = g.m <= 16 || (g.m <= 64 && !(long_k && tiles(16, 16) > 1024)) ||
-                      (g.m > 64 && g.m <= 128 && tiles(32, 16) <= 512);
+  const bool plane_rule = !packed && (!araw || rcap > 4);
+  const bool stream = plane_rule ? g.m <= 48 && tiles(32, 64) < 128
+                                 : g.m <= 16 || (g.m <= 64 && !(long_k && tiles(16, 16) > 1024)) ||
+                                       (g.m > 64 && g.m <= 128 && tiles(32, 16) <= 512);
   if (stream) {
     c.mb = g.m <= 64 ? 1 : 2;
     c.nb = 1;
-    // chunks of 8 K steps once K >= 4096 (16-row tiles, up to 4 channels):
-    // each wave then has half as many dependent round trips to memory
-    const bool wide = c.mb == 1 && rcap <= 4 && nk >= 64;
+    // chunks of 8 K steps once K >= 4096 (16-row tiles, up to 4 channels,
+    // raw int8 activations): each wave then has half as many dependent round
+    // trips to memory.  With residue planes the A fragments share the
+    // registers and the 7-step chunks measured slower (K=4096, N=4096, 4
+    // channels, M=1: 25.7 against 20.9 us with chunks of 4).
+    const bool wide = araw && c.mb == 1 && rcap <= 4 && nk >= 64;
     c.kind = wide ? kStreamWide : kStream;
     const int u = stream_u_of(rcap, araw, c.mb, c.nb, wide ? 8 : 4);
     c.ks = std::min(stream_ks_cap(rcap, c.mb, c.nb), std::max(1, (nk + u - 1) / u));
@@ -699,9 +718,10 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw) {
     }
   }
   // a ring of 4 K steps measured 1-3 % faster than 3 for 32- and 48-row
-  // tiles and for three-wave tiles (and slower for 64 x 64 ones)
+  // tiles and for three-wave tiles (and slower for 64 x 64 ones); past 6
+  // channels the registers hold a ring of 3 only (the tile's default)
   if (best_w == 3) c.kind = kMfma3;
-  if (c.mb < 4 || best_w == 3) c.ks = 4;
+  if ((c.mb < 4 || best_w == 3) && rcap <= 6) c.ks = 4;
   return c;
 }
 
@@ -955,7 +975,7 @@ static GemmChoice packed_auto(const GemmArgs &g) {
     const int u = rows_steps_of(nblk);
     return GemmChoice{kRows, nblk, 1, std::min(4, std::max(1, (g.kp / 64 + u - 1) / u)), 1, 0};
   }
-  GemmChoice c = choose_gemm(g, false);
+  GemmChoice c = choose_gemm(g, false, true);
   c.splits = 1;
   c.tail = 0;
   // the residue-plane LDS kernel with two units per channel (a' x hi, a x

@@ -72,7 +72,12 @@ PLANS = [
     ((1, 12288, 4096, 4), (4, 1, 1, 4, 1, 0)),     # C5 decode: stream with 8-step chunks
     ((16, 12288, 4096, 4), (4, 1, 1, 4, 1, 0)),    # long K, 16 rows: stream, 8-step chunks
     ((16, 2048, 2048, 4), (1, 1, 1, 4, 1, 0)),     # K = 2048: 4-step chunks
-    ((1, 12288, 4096, 6), (1, 1, 1, 4, 1, 0)),     # 8-step chunks only up to 4 channels
+    ((1, 12288, 4096, 6), (2, 2, 1, 4, 1, 0)),     # no 8-step chunks past 4 channels: 192 MFMA tiles
+    ((1, 4096, 4096, 6), (1, 1, 1, 4, 1, 0)),      # 64 MFMA tiles: stream, 4-step chunks
+    ((48, 2304, 768, 6), (1, 1, 1, 3, 1, 0)),
+    ((64, 4096, 4096, 6), (2, 2, 1, 4, 1, 0)),     # past 48 rows
+    ((96, 48, 64, 10), (2, 2, 1, 0, 1, 0)),        # 10 channels: the tile's default ring (3 steps)
+    ((256, 2304, 768, 10), (2, 4, 1, 0, 1, 0)),
     ((32, 12288, 4096, 4), (2, 2, 1, 4, 1, 0)),    # long K, wide N: MFMA, 32 rows
     ((48, 12288, 4096, 4), (2, 3, 1, 4, 1, 0)),
     ((64, 12288, 4096, 4), (2, 4, 1, 0, 1, 0)),
@@ -128,6 +133,23 @@ def test_gemm_plan_residue_plane_activations():
     assert gemm_plan(256, 2304, 768, 4, raw_a=0)[0] != 8                   # 36 tiles x 12 steps: too little work
     assert gemm_plan(4096, 2304, 768, 4, raw_a=0) == (8, 0, 0, 0, 1, 0)    # 576 tiles
     assert gemm_plan(512, 12288, 4096, 3, raw_a=0)[0] == 2                 # 3-channel capacity
+
+
+def test_gemm_plan_residue_plane_few_rows():
+    # residue-plane activations at decode sizes: the stream kernel (chunks of
+    # at most 4 K steps) only while the MFMA kernel's 32 x 64 tiles number
+    # under 128 and the rows are at most 32, else 32-row MFMA tiles
+    assert gemm_plan(1, 12288, 4096, 6, raw_a=0) == (2, 2, 1, 4, 1, 0)    # 192 MFMA tiles
+    assert gemm_plan(16, 12288, 4096, 6, raw_a=0) == (2, 2, 1, 4, 1, 0)
+    assert gemm_plan(16, 4096, 4096, 6, raw_a=0) == (1, 1, 1, 4, 1, 0)    # 64 MFMA tiles: stream
+    assert gemm_plan(32, 4096, 4096, 4, raw_a=0) == (1, 1, 1, 4, 1, 0)
+    assert gemm_plan(1, 4096, 4096, 4, raw_a=0) == (1, 1, 1, 4, 1, 0)     # never 8-step chunks
+    assert gemm_plan(64, 4096, 4096, 6, raw_a=0) == (2, 2, 1, 4, 1, 0)    # past 32 rows
+    assert gemm_plan(64, 2304, 768, 6, raw_a=0) == (2, 2, 1, 4, 1, 0)
+    assert gemm_plan(16, 2304, 768, 6, raw_a=0)[0] == 1                   # 36 MFMA tiles
+    # raw int8 keeps its rule: 8-step chunks at K = 4096, the stream kernel to 64 rows
+    assert gemm_plan(1, 4096, 4096, 4) == (4, 1, 1, 4, 1, 0)
+    assert gemm_plan(64, 2304, 768, 4)[0] == 1
 
 
 def test_gemm_plan_rejects_bad_shapes():
