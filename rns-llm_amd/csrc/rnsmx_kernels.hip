@@ -615,7 +615,11 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
                                  : g.m <= 16 || (g.m <= 64 && !(long_k && tiles(16, 16) > 1024)) ||
                                        (g.m > 64 && g.m <= 128 && tiles(32, 16) <= 512);
   if (stream) {
-    c.mb = g.m <= 64 ? 1 : 2;
+    // 16-row tiles up to 64 rows, and beyond while they number at most 768
+    // (raw int8, K=768: N=768 M=96 5.95 us against 6.73 with 32-row tiles,
+    // M=128 6.35 against 6.87; N=2304 M=80 7.77 against 8.27; at M=96,
+    // 864 tiles, 8.88 against 8.75)
+    c.mb = g.m <= 64 || (!packed && tiles(16, 16) <= 768) ? 1 : 2;
     c.nb = 1;
     // chunks of 8 K steps once K >= 4096 (16-row tiles, up to 4 channels,
     // raw int8 activations): each wave then has half as many dependent round
@@ -626,6 +630,13 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
     c.kind = wide ? kStreamWide : kStream;
     const int u = stream_u_of(rcap, araw, c.mb, c.nb, wide ? 8 : 4);
     c.ks = std::min(stream_ks_cap(rcap, c.mb, c.nb), std::max(1, (nk + u - 1) / u));
+    // From 16 rows the 16 x 16 tile's LDS epilogue (256 elements) runs one
+    // element per thread with 4 waves, and that pays for a 4th wave even
+    // where the K chunks keep only 3 busy (K=768: M=16 5.18 us against
+    // 5.64 with 3 waves, M=80 5.14 against 5.76; K=512 M=16 5.05 against
+    // 5.58); fewer rows go the one-element path, where the 3rd wave is
+    // enough (M=1-8 0.1-0.2 us faster with 3).
+    if (g.m >= 16 && c.mb == 1) c.ks = stream_ks_cap(rcap, c.mb, c.nb);
     c.splits = 1;
     return c;
   }

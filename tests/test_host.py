@@ -54,9 +54,11 @@ def gemm_plan(m, n, k, channels=4, raw_a=1):
 # splits: workgroups sharing each output tile's K range
 PLANS = [
     ((1, 2304, 768, 4), (1, 1, 1, 3, 1, 0)),       # decode: stream, 3 waves split 12 K steps
-    ((64, 2304, 768, 4), (1, 1, 1, 3, 1, 0)),      # stream up to 64 rows at short K
+    ((64, 2304, 768, 4), (1, 1, 1, 4, 1, 0)),      # stream up to 64 rows at short K, 4 waves from 16 rows
+    ((8, 2304, 768, 4), (1, 1, 1, 3, 1, 0)),       # under 16 rows: 3 waves (12 K steps in chunks of 4)
     ((96, 2304, 768, 4), (1, 2, 1, 3, 1, 0)),      # stream: 432 tiles of 32 x 16
-    ((128, 768, 768, 4), (1, 2, 1, 3, 1, 0)),      # stream: 192 tiles
+    ((128, 768, 768, 4), (1, 1, 1, 4, 1, 0)),      # stream: 384 tiles of 16 x 16 (at most 768)
+    ((80, 2304, 768, 4), (1, 1, 1, 4, 1, 0)),      # 720 tiles of 16 x 16
     ((128, 2304, 768, 4), (5, 2, 1, 4, 1, 0)),     # 576 stream tiles: MFMA, 32 x 48 (192 tiles)
     ((256, 1536, 768, 4), (5, 2, 1, 4, 1, 0)),     # 32 x 48 fills 256 CUs (32 x 64: 192)
     ((256, 3072, 768, 4), (5, 4, 1, 4, 1, 0)),     # 64 x 48, 256 tiles, ties 64 x 64 on rows
@@ -74,7 +76,7 @@ PLANS = [
     ((16, 2048, 2048, 4), (1, 1, 1, 4, 1, 0)),     # K = 2048: 4-step chunks
     ((1, 12288, 4096, 6), (2, 2, 1, 4, 1, 0)),     # no 8-step chunks past 4 channels: 192 MFMA tiles
     ((1, 4096, 4096, 6), (1, 1, 1, 4, 1, 0)),      # 64 MFMA tiles: stream, 4-step chunks
-    ((48, 2304, 768, 6), (1, 1, 1, 3, 1, 0)),
+    ((48, 2304, 768, 6), (1, 1, 1, 4, 1, 0)),
     ((64, 4096, 4096, 6), (2, 2, 1, 4, 1, 0)),     # past 48 rows
     ((96, 48, 64, 10), (2, 2, 1, 0, 1, 0)),        # 10 channels: the tile's default ring (3 steps)
     ((256, 2304, 768, 10), (2, 4, 1, 0, 1, 0)),
