@@ -590,9 +590,9 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   };
   GemmChoice c{};
   // Stream kernel up to 16 rows; up to 64 unless K > 1024 and its 16 x 16
-  // tiles number over 1024 (K=4096, N=12288: M=64 45 us with the MFMA
-  // kernel against 79, M=32 39 against 54; at K=768, N=2304, M=64 the
-  // stream kernel's 6.9 against 8.7); up to 128 while its 32 x 16 tiles
+  // tiles number 1024 or more (K=4096, N=12288: M=64 45 us with the MFMA
+  // kernel against 79, M=32 39 against 54; N=4096 M=64 28 against 33; at
+  // K=768, N=2304, M=64 the stream kernel's 6.9 against 8.7); up to 128 while its 32 x 16 tiles
   // number at most 512 (M=128: N=2304 8.8 us with the MFMA kernel against
   // 9.6, N=4608 10.3 against 14.0, K=4096 N=12288 62 against 110; at
   // N=768, 192 tiles, 5.1 against 7.4; at M=96, N=2304, 432 tiles, 7.6
@@ -612,7 +612,7 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   const bool long_k = nk > 16;
   const bool plane_rule = !packed && (!araw || rcap > 4);
   const bool stream = plane_rule ? g.m <= 48 && tiles(32, 64) < 128
-                                 : g.m <= 16 || (g.m <= 64 && !(long_k && tiles(16, 16) > 1024)) ||
+                                 : g.m <= 16 || (g.m <= 64 && !(long_k && tiles(16, 16) >= 1024)) ||
                                        (g.m > 64 && g.m <= 128 && tiles(32, 16) <= 512);
   if (stream) {
     // 16-row tiles up to 64 rows, and beyond while they number at most 768
@@ -664,7 +664,15 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   const int64_t rounds = (lds_tiles + 255) / 256;
   const bool full_rounds = 8 * lds_tiles >= 7 * 256 * rounds;
   c.splits = 1;
-  if (g.m > 128 && lds_kernel_fits(g, araw, rcap) && lds_tiles >= 256 && (g.kp >= 2048 || full_rounds)) {
+  // At K = 4096 the 256 x 64 tiles win from 128 rows once they number 192
+  // (three quarters of a round), their long K loop reusing each weight
+  // column over 256 rows however many are padding (N=12288: M=128 48.8 us
+  // against 62.5 with 64 x 64 MFMA tiles, M=192 53.2 against 80.7, M=256
+  // 54.8 against 78.5; N=4096, 64 tiles, 46.3 against 31.9; K=2048 N=8192
+  // M=128, 128 tiles, 26.1 against 21.5).
+  const bool lds_long = g.m >= 128 && lds_tiles >= 192 && nk >= 64 && nk < 128;
+  if (lds_kernel_fits(g, araw, rcap) &&
+      ((g.m > 128 && lds_tiles >= 256 && (g.kp >= 2048 || full_rounds)) || lds_long)) {
     c.kind = wide ? kLdsWide : kLds;
     return c;
   }
