@@ -713,14 +713,21 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   // (C2 M=128 32 x 48, 192 tiles, 8.3 us against 8.8 with 32 x 64; N=1536
   // M=256 8.5 against 9.0; K=1024 N=3072 M=256 64 x 48, 12.9 against 13.5),
   // then the taller, then the wider tile.  48 x 48 and 64 x 48 never beat
-  // 48 x 64 on the headline (10.9 against 9.9 us).
+  // 48 x 64 on the headline (10.9 against 9.9 us).  At K = 2048-4096 the
+  // same tie-break gains 2-10 % (K=4096: N=12288 M=48 40.2 us against 41.0,
+  // M=64 43.2 against 46.4; N=4096 M=64 25.6 against 28.1; N=6144 M=64
+  // 28.4 against 30.3; K=2048 N=4096 M=64 13.6 against 15.1).
   c.mb = 4;
   int best_w = 4;
   int64_t best_rows = -1, best_fill = 0;
   for (int w = 4; w >= 3; --w) {
-    if (w == 3 && !(araw && rcap <= 4 && nk <= 16)) continue;
+    if (w == 3 && !(araw && rcap <= 4)) continue;
     for (int mb = 4; mb >= 2; --mb) {
       if (mb == 3 && rcap > 4) continue;
+      // past K = 1024 a three-wave tile only where the four-wave one of its
+      // height already gives 128 workgroups and K is under 8192 (so neither
+      // would split K over workgroups)
+      if (w == 3 && nk > 16 && !(nk < 128 && tiles(16 * mb, 64) >= 128)) continue;
       const int64_t t = tiles(16 * mb, 16 * w);
       if (t > 512) continue;
       const int64_t rows = (t + 255) / 256 * (16 * mb);

@@ -80,14 +80,15 @@ PLANS = [
     ((64, 4096, 4096, 6), (2, 2, 1, 4, 1, 0)),     # past 48 rows
     ((96, 48, 64, 10), (2, 2, 1, 0, 1, 0)),        # 10 channels: the tile's default ring (3 steps)
     ((256, 2304, 768, 10), (2, 4, 1, 0, 1, 0)),
-    ((32, 12288, 4096, 4), (2, 2, 1, 4, 1, 0)),    # long K, wide N: MFMA, 32 rows
-    ((48, 12288, 4096, 4), (2, 3, 1, 4, 1, 0)),
-    ((64, 12288, 4096, 4), (2, 4, 1, 0, 1, 0)),
+    ((32, 12288, 4096, 4), (5, 2, 1, 4, 1, 0)),    # long K, wide N: MFMA, 32 rows, three waves (256 tiles)
+    ((48, 12288, 4096, 4), (5, 3, 1, 4, 1, 0)),
+    ((64, 12288, 4096, 4), (5, 4, 1, 4, 1, 0)),
     ((128, 12288, 4096, 4), (3, 0, 0, 0, 1, 0)),   # K = 4096, 192 LDS tiles: three quarters of a round
     ((256, 12288, 4096, 4), (3, 0, 0, 0, 1, 0)),
     ((128, 12288, 8192, 4), (2, 4, 1, 0, 2, 0)),   # K = 8192: MFMA tiles (K in two halves)
     ((256, 4096, 4096, 4), (2, 4, 1, 0, 1, 0)),    # 64 LDS tiles: MFMA
-    ((64, 4096, 4096, 4), (2, 2, 1, 4, 1, 0)),     # 1024 stream tiles at long K: MFMA
+    ((64, 4096, 4096, 4), (5, 2, 1, 4, 1, 0)),     # 1024 stream tiles at long K: MFMA
+    ((64, 4096, 8192, 4), (2, 2, 1, 4, 2, 0)),     # K = 8192: four waves, K in two halves
     ((512, 12288, 4096, 4), (7, 0, 0, 0, 1, 0)),   # LDS-staged, 256 x 96 tiles: 256, one round
     ((2048, 12288, 4096, 4), (7, 0, 0, 0, 1, 0)),  # 4 rounds of 96 columns against 6 of 64
     ((1024, 12288, 4096, 4), (7, 0, 0, 0, 1, 0)),
