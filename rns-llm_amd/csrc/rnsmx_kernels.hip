@@ -683,7 +683,9 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   // M=256 123 against 304, M=512 N=4096 84 against 210; 4 channels M=2048
   // N=12288 472 against 886; K = 768, N = 2304: M=4096 81 against 108, but
   // M=256 (36 tiles, 12 steps) 28.5 against 19.6, so not there).
-  if (g.m >= 64 && lds_planes_fits(g, araw, rcap) && tiles(kPlBM, kPlBN) * nk >= 4096) {
+  // From 48 rows too: K=4096 N=12288 M=48, 6 channels, 90.8 us with K in
+  // two halves against 103 on 32-row MFMA tiles.
+  if (g.m >= 48 && lds_planes_fits(g, araw, rcap) && tiles(kPlBM, kPlBN) * nk >= 4096) {
     c.kind = kLdsPlanes;
     return c;
   }
@@ -693,6 +695,16 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   if (g.m > 128 && rcap <= 4 && tiles(128, 128) >= 1024) {
     c.mb = 8;
     c.nb = 2;
+    return c;
+  }
+  // Residue-plane activations stage R A planes per K step (raw int8 one),
+  // so their bytes grow with the tile height: 32-row tiles up to three
+  // rounds of them, whatever the rows per CU (6 channels, K=768 N=2304:
+  // M=256 27.2 us against 32.6 with 64-row tiles, M=512 39.1 against 56.6;
+  // 4 channels K=4096 N=4096 M=64 43.6 against 58.6).
+  if (!araw && tiles(32, 64) <= 768) {
+    c.mb = 2;
+    if (rcap <= 6) c.ks = 4;
     return c;
   }
   // 32, 48 or 64 rows x 64 (or 48) columns: among the tiles that give at
@@ -1026,8 +1038,11 @@ static GemmChoice packed_auto(const GemmArgs &g) {
     const int64_t t = static_cast<int64_t>((g.m + 16 * mb - 1) / (16 * mb)) * ((g.n + 63) / 64);
     return (t + 255) / 256 * 16 * mb;
   };
+  // 32-row tiles on a tie in rows per CU up to three rounds of them (6
+  // channels, K=768 N=2304 M=256: 36.0 us against 50.3 with 64-row tiles)
+  const bool few = static_cast<int64_t>((g.m + 31) / 32) * ((g.n + 63) / 64) <= 768;
   c.kind = kMfma;
-  c.mb = rows_per_cu(2) < rows_per_cu(4) ? 2 : 4;
+  c.mb = rows_per_cu(2) < rows_per_cu(4) || (few && rows_per_cu(2) == rows_per_cu(4)) ? 2 : 4;
   c.ks = 0;
   return c;
 }

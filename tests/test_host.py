@@ -136,7 +136,11 @@ def test_gemm_plan_residue_plane_activations():
     assert gemm_plan(512, 12288, 4096, 6)[0] == 2                          # raw int8: MFMA kernel
     assert gemm_plan(64, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 2, 0)    # 96 tiles: K in two halves
     assert gemm_plan(128, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 2, 0)
-    assert gemm_plan(48, 12288, 4096, 6, raw_a=0)[0] == 2                  # under 64 rows
+    assert gemm_plan(48, 12288, 4096, 6, raw_a=0) == (8, 0, 0, 0, 2, 0)    # from 48 rows: 96 tiles, K in two halves
+    assert gemm_plan(32, 12288, 4096, 6, raw_a=0)[0] == 2                  # under 48 rows
+    assert gemm_plan(256, 2304, 768, 6, raw_a=0) == (2, 2, 1, 4, 1, 0)     # residue planes: 32-row MFMA tiles
+    assert gemm_plan(512, 2304, 768, 6, raw_a=0) == (2, 2, 1, 4, 1, 0)     # 576 of them
+    assert gemm_plan(256, 2304, 768, 6) == (2, 4, 1, 0, 1, 0)              # raw int8: the rows-per-CU rule
     assert gemm_plan(256, 2304, 768, 4, raw_a=0)[0] != 8                   # 36 tiles x 12 steps: too little work
     assert gemm_plan(4096, 2304, 768, 4, raw_a=0) == (8, 0, 0, 0, 1, 0)    # 576 tiles
     assert gemm_plan(512, 12288, 4096, 3, raw_a=0)[0] == 2                 # 3-channel capacity
@@ -283,6 +287,7 @@ PACKED_PLANS = [
     ((1, 768, 50_000, 6), (1, 1, 1, 4, 1, 0)),   # K past the channel-row sums' int32 range
     ((96, 2304, 768, 6), (1, 2, 1, 4, 1, 0)),    # 432 stream tiles of 32 x 16
     ((100, 2304, 768, 6), (2, 2, 1, 0, 1, 0)),   # MFMA: 144 tiles of 32 rows beat 72 of 64
+    ((256, 2304, 768, 6), (2, 2, 1, 0, 1, 0)),   # a tie in rows per CU (288 tiles of 32 rows, 144 of 64): 32
     ((1024, 4096, 1100, 6), (2, 4, 1, 0, 1, 0)),  # 256 rows per CU either way: 64 (K not 256-aligned)
     ((1024, 4096, 1024, 6), (8, 0, 0, 0, 1, 0)),  # residue-plane LDS kernel: 256 tiles of 128 x 128
     ((512, 12288, 4096, 6), (8, 0, 0, 0, 2, 1)),  # 384 tiles: the last 128 split K in two
