@@ -92,7 +92,7 @@ struct GemmArgsOf {
   int8_t *xchg;       // partial residues, [tile * waves + wave][split][MI * NJ][4 words][64 lanes] x 4 bytes
   // adaptive prefix
   int32_t min_channels;  // 0: all channels
-  int32_t l1_rows;       // row norms at row_l1 to fold (1: their maximum, folded by the encoder)
+  int32_t l1_rows;       // words at row_l1 to fold: row norms, or row_l1_max_kernel's maxima of them
   const int64_t *row_l1;
   const int32_t *w_absmax;
   int64_t *meta;
@@ -289,8 +289,8 @@ __device__ __forceinline__ int64_t prefix_at(const Mods &mods, int idx) {
 
 // Number of moduli channels to use.  Without the adaptive prefix this is the
 // full set.  With it, every workgroup derives the same answer from the row
-// L1 norms (their maximum, one word written by the encoder; or l1_rows
-// norms to fold; or, when row_l1 is null, summed here
+// L1 norms (l1_rows words to fold: the norms, or at most 256 maxima of
+// them written by row_l1_max_kernel; or, when row_l1 is null, summed here
 // from the raw int8 activations: the launcher does so for a few rows only,
 // since every workgroup reads them) and max|B| written at weight preparation:
 // bound = max_i sum_k |a_ik| * max|B| (adaptive.py:44-52); the answer is the
@@ -302,10 +302,24 @@ template <int RCAP>
 __device__ __forceinline__ int active_channels(KArgs<RCAP> &g, int64_t *red, int *bcast, int nthreads) {
   const int full = g.mods.channels;
   if (g.min_channels <= 0) return full;
-  if (g.row_l1 != nullptr && g.l1_rows == 1) {
-    // one word (the maximum the encoder folded): every wave reads it and
-    // max|B| with scalar loads and decides alone, with no barrier
-    const int64_t best = *g.row_l1, wmax = *g.w_absmax;
+  if (g.row_l1 != nullptr && g.l1_rows <= 256) {
+    // at most 256 words (row norms, or row_l1_max_kernel's maxima of them):
+    // every wave folds them itself, reads max|B| with a scalar load and
+    // decides alone, with no barrier
+    const int lane = threadIdx.x & 63;
+    int64_t mx = 0;
+    static_for<4>([&](auto J) {
+      const int r = lane + 64 * decltype(J)::value;
+      if (r < g.l1_rows) {
+        const int64_t v = g.row_l1[r];
+        mx = v > mx ? v : mx;
+      }
+    });
+    mx = wave_max_i64(mx);  // every lane holds the maximum
+    const int64_t best = static_cast<int64_t>(
+        (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(mx) >> 32))) << 32) |
+        __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(mx)));
+    const int64_t wmax = *g.w_absmax;
     int64_t bound;
     if (__builtin_mul_overflow(best, wmax, &bound)) bound = LLONG_MAX;
     int c = full, overflow = 1;

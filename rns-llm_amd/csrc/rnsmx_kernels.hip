@@ -30,8 +30,6 @@ struct EncodeArgs {
   int64_t rows, cols, out_ld, plane;
   int8_t *out;
   int64_t *row_l1;
-  int64_t *row_l1_max;  // row_l1_max_kernel: max_i row_l1[i], one word
-  uint32_t *l1_ticket;  // row_l1_max_kernel: arrival counter (zero between calls)
   int32_t *absmax;
   rnsmx_moduli_t mods;
 };
@@ -164,63 +162,61 @@ __global__ __launch_bounds__(256) void encode_rows_kernel(const EncodeArgs e) {
 }
 
 // The adaptive bound's max_i sum_k |a_ik| of raw int8 rows (cols a multiple
-// of 16), folded into one word so that every GEMM workgroup reads that word
+// of 16), reduced to at most 256 words so that every GEMM wave folds those
 // instead of all M norms (C5 M=2048: 2048 norms re-read by each of 1024
 // workgroups before their first load).  Each wave sums whole rows (a lane
-// 16 bytes per 1 KB of the row), a workgroup keeps the largest of its rows
-// in row_l1[blockIdx.x], and the last workgroup to finish folds those into
-// row_l1_max.  At most 256 workgroups: the arrivals on the one counter are
-// serialised at the memory side (one workgroup per row, 2048 arrivals,
-// measured some 20 us).  The handoff is split_exchange's: agent-scope stores
-// and loads, the store complete before the ticket is taken, a
-// self-resetting counter.
+// 16 bytes per 1 KB of the row) and workgroup b writes the largest of its
+// rows to row_l1[b]; the GEMM that follows reads them (the launch boundary
+// orders the stores before its loads).  Folding them here into one word
+// through an arrival counter cost more: the arrivals on the one counter are
+// serialised at the memory side (256 of them ~2-3 us, 2048 some 20 us).
 __global__ __launch_bounds__(256) void row_l1_max_kernel(const EncodeArgs e) {
   __shared__ int64_t sh[4];
-  __shared__ int last;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int8_t *src = static_cast<const int8_t *>(e.values);
   int64_t best = 0;
-  for (int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + wv; r < e.rows; r += static_cast<int64_t>(gridDim.x) * 4) {
-    int32_t sum = 0;  // |a| <= 128 and K < 2^24: no overflow
-    for (int64_t k0 = lane * 16; k0 < e.cols; k0 += 64 * 16) {
-      const i32x4 w = *reinterpret_cast<const i32x4 *>(src + r * e.cols + k0);
-      static_for<16>([&](auto Q) {
-        constexpr int q = decltype(Q)::value;
-        const int32_t b = static_cast<int8_t>((static_cast<uint32_t>(w[q >> 2]) >> (8 * (q & 3))) & 0xFFu);
-        sum += b < 0 ? -b : b;
+  // Each wave takes two rows at a time and each lane issues its 16-byte
+  // loads of both, up to 4 KB of row per pass, before it sums any: one
+  // memory round trip per pass instead of one per 1 KB of row.
+  constexpr int kChunks = 4;  // 1 KB row chunks per pass
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 4;
+  const i32x4 zero = {0, 0, 0, 0};
+  for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * 4 + wv; r0 < e.rows; r0 += 2 * stride) {
+    const int64_t r1 = r0 + stride;
+    const bool two = r1 < e.rows;
+    int32_t sum0 = 0, sum1 = 0;  // |a| <= 128 and K < 2^24: no overflow
+    for (int64_t k0 = lane * 16; k0 < e.cols; k0 += 64 * 16 * kChunks) {
+      i32x4 w0[kChunks], w1[kChunks];
+      static_for<kChunks>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        const int64_t k = k0 + j * 1024;
+        w0[j] = zero;
+        w1[j] = zero;
+        if (k < e.cols) {
+          w0[j] = *reinterpret_cast<const i32x4 *>(src + r0 * e.cols + k);
+          if (two) w1[j] = *reinterpret_cast<const i32x4 *>(src + r1 * e.cols + k);
+        }
+      });
+      static_for<kChunks>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        static_for<16>([&](auto Q) {
+          constexpr int q = decltype(Q)::value;
+          const int32_t b0 = static_cast<int8_t>((static_cast<uint32_t>(w0[j][q >> 2]) >> (8 * (q & 3))) & 0xFFu);
+          const int32_t b1 = static_cast<int8_t>((static_cast<uint32_t>(w1[j][q >> 2]) >> (8 * (q & 3))) & 0xFFu);
+          sum0 += b0 < 0 ? -b0 : b0;
+          sum1 += b1 < 0 ? -b1 : b1;
+        });
       });
     }
-    const int64_t row = wave_sum_i64(sum);
-    best = row > best ? row : best;
+    const int64_t row0 = wave_sum_i64(sum0), row1 = wave_sum_i64(sum1);
+    best = row0 > best ? row0 : best;
+    best = row1 > best ? row1 : best;
   }
   if (lane == 0) sh[wv] = best;
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w = 1; w < 4; ++w) best = sh[w] > best ? sh[w] : best;
-    __hip_atomic_store(reinterpret_cast<uint64_t *>(e.row_l1 + blockIdx.x), static_cast<uint64_t>(best),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    wait_vm_all();
-    const uint32_t old = __hip_atomic_fetch_add(e.l1_ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = old == gridDim.x - 1;
-  }
-  __syncthreads();
-  if (!last) return;
-  asm volatile("" ::: "memory");
-  int64_t mx = 0;
-  for (unsigned b = threadIdx.x; b < gridDim.x; b += blockDim.x) {
-    const int64_t v = static_cast<int64_t>(
-        __hip_atomic_load(reinterpret_cast<uint64_t *>(e.row_l1 + b), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    mx = v > mx ? v : mx;
-  }
-  mx = wave_max_i64(mx);
-  __syncthreads();
-  if (lane == 0) sh[wv] = mx;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < 4; ++w) mx = sh[w] > mx ? sh[w] : mx;
-    __hip_atomic_store(reinterpret_cast<uint64_t *>(e.row_l1_max), static_cast<uint64_t>(mx), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(e.l1_ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    e.row_l1[blockIdx.x] = best;
   }
 }
 
@@ -558,9 +554,10 @@ static constexpr int kStreamLdsMax = 65536;
 // Up to this many raw int8 rows, the adaptive prefix's row norms are summed
 // inside the GEMM (every workgroup reads all the rows) instead of by a
 // separate encoder launch.  Beyond it the encoder sums them; up to
-// kAdaptiveFoldInGemm rows every GEMM workgroup folds the norms (a few KB),
-// beyond that the encoder folds their maximum into one word (C5 M=2048:
-// 2048 norms re-read by each of 1024 workgroups before their first load).
+// kAdaptiveFoldInGemm rows every GEMM wave folds the norms (at most 2 KB),
+// beyond that row_l1_max_kernel reduces them to that many words first (C5
+// M=2048: 2048 norms re-read by each of 1024 workgroups before their first
+// load).
 static constexpr int kAdaptiveRowsInGemm = 4;
 static constexpr int kAdaptiveFoldInGemm = 256;
 
@@ -768,9 +765,6 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
 // ---------------------------------------------------------------------------
 // Bytes of the arrival counters at the start of every workspace.
 static constexpr int64_t kTicketBytes = int64_t{RNSMX_SPLIT_TICKETS} * 4;
-// The last counter serves the adaptive row-norm fold (encode_rows_kernel);
-// the splits use the ones before it.
-static constexpr int kL1Ticket = RNSMX_SPLIT_TICKETS - 1;
 
 // Steps per split for `splits` workgroups over nk K steps (the LDS kernel
 // runs whole trips of its stages), and the split count that leaves no
@@ -808,7 +802,7 @@ static bool split_fits(const GemmChoice &c, const GemmArgs &g) {
     built = rcap <= 4;
   else
     built = mfma_splits(rcap, c.mb, c.nb);
-  return built && (gr.tiles - whole_tiles(c, gr.tiles)) * gr.waves <= kL1Ticket;
+  return built && (gr.tiles - whole_tiles(c, gr.tiles)) * gr.waves <= RNSMX_SPLIT_TICKETS;
 }
 
 // Exchange-area bytes of a choice (0 without a split).
@@ -1583,6 +1577,8 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
   // encoder launch: C5 adaptive M=1 44 -> 39 us.
   const bool l1_in_gemm = araw && min_ch != 0 && m <= kAdaptiveRowsInGemm;
   const bool l1_fold = araw && min_ch != 0 && !l1_in_gemm && m > kAdaptiveFoldInGemm;
+  // row_l1_max_kernel's workgroups: their maxima are the words the GEMM folds
+  const int l1_groups = static_cast<int>(std::min<int64_t>((m + 3) / 4, kAdaptiveFoldInGemm));
   EncodeArgs e{};
   e.values = a_dev;
   e.rows = m;
@@ -1591,8 +1587,6 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
   e.plane = static_cast<int64_t>(m) * kp;
   e.out = araw ? nullptr : a_res;
   e.row_l1 = min_ch != 0 ? row_l1 : nullptr;
-  e.row_l1_max = row_l1 + m;
-  e.l1_ticket = reinterpret_cast<uint32_t *>(ws) + kL1Ticket;
   e.absmax = nullptr;
   e.mods = *mods;
   const bool rows = packed && c.kind == kRows;
@@ -1622,8 +1616,7 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
   } else if (packed) {
     if (int32_t rc = launch_encode_rows(a_dtype, e, st, true)) return rc;
   } else if (l1_fold) {
-    const unsigned groups = static_cast<unsigned>(std::min<int64_t>((m + 3) / 4, 256));
-    hipLaunchKernelGGL(row_l1_max_kernel, dim3(groups), dim3(256), 0, st, e);
+    hipLaunchKernelGGL(row_l1_max_kernel, dim3(static_cast<unsigned>(l1_groups)), dim3(256), 0, st, e);
     if (int32_t rc = check_launch("row_l1_max")) return rc;
   } else if (!araw || (min_ch != 0 && !l1_in_gemm)) {
     if (int32_t rc = launch_encode_rows(a_dtype, e, st)) return rc;
@@ -1641,8 +1634,8 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
   g.b_cs = kp * 16 * ((n + 15) / 16);  // per channel, or per byte plane of packed weights
   g.min_channels = min_ch;
   // the norms, or the maximum the encoder folded
-  g.row_l1 = l1_in_gemm ? nullptr : l1_fold ? row_l1 + m : row_l1;
-  g.l1_rows = l1_fold ? 1 : m;
+  g.row_l1 = l1_in_gemm ? nullptr : row_l1;
+  g.l1_rows = l1_fold ? l1_groups : m;
   g.w_absmax = min_ch != 0 ? adaptive->w_absmax_dev : nullptr;
   g.meta = min_ch != 0 ? adaptive->meta_dev : nullptr;
   g.out = out_dev;
