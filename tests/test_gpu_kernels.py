@@ -251,7 +251,7 @@ def test_kernel_adaptive_prefix(backend, kind, mb, nb, ks, k):
 @pytest.mark.parametrize("plan", [(1, 1, 1, 4), (1, 2, 1, 1), (1, 1, 1, 1, 4), (4, 1, 1, 4), (2, 4, 1, 0),
                                   (2, 2, 1, 0, 2), (3, 0, 0, 0), (3, 0, 0, 0, 2), (7, 0, 0, 0), (7, 0, 0, 0, 2)])
 @pytest.mark.parametrize("dtype", [torch.int8, torch.int16])
-@pytest.mark.parametrize("m", [3, 70, 600])  # row norms summed in the GEMM / folded there / folded to one word
+@pytest.mark.parametrize("m", [3, 70, 600])  # row norms summed in the GEMM / folded there / reduced by the norm kernel first
 def test_kernel_adaptive_three_of_four_channels(backend, plan, dtype, m):
     # the device picks 3 of the 4 channels: the stream and LDS kernels then
     # run a body without the fourth channel's loads and MFMAs; exact against
