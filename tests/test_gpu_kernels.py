@@ -274,6 +274,29 @@ def test_kernel_adaptive_three_of_four_channels(backend, plan, dtype, m):
     np.testing.assert_array_equal(full.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("m,k,big", [(1030, 1088, 1029), (2100, 4160, 2099), (2100, 4160, 5), (300, 4096, 299)])
+def test_adaptive_norm_kernel_partial_maxima(backend, m, k, big):
+    # past 256 raw rows the norm kernel leaves one maximum per workgroup
+    # (each wave two rows a pass, K in passes of 4 KB, the last one partial)
+    # and every GEMM wave folds them: one large row anywhere, also the second
+    # row of a pass, raises the bound past the 3-channel range
+    gen = torch.Generator().manual_seed(m + k + big)
+    n = 16
+    a = torch.randint(-8, 9, (m, k), generator=gen).to(torch.int8)
+    b = torch.randint(-127, 128, (k, n), generator=gen).to(torch.int8)
+    b[0, 0] = 127  # max|B| = 127: small rows need 3 channels, a row of 127s 4
+    prepared = backend.prepare_weight_adaptive(b.to(DEV), DENSE4, min_channels=3)
+    ws = {4: backend.create_workspace(device=torch.device(DEV), channels=4, m=m, n=n, k=k)}
+    for planted, channels in ((False, 3), (True, 4)):
+        if planted:
+            a[big] = 127
+        want = ro.exact_matmul(a.numpy(), b.numpy())
+        out, meta = backend.matmul_prepared_adaptive_fused(a.to(DEV), prepared, workspace_by_channels=ws,
+                                                          return_metadata=True)
+        assert meta["channels"] == channels
+        np.testing.assert_array_equal(out.cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("kind,mb,nb,ks", [(1, 1, 2, 2), (1, 4, 1, 4), (1, 2, 1, 1), (2, 8, 2, 0), (2, 2, 1, 0),
                                            (3, 0, 0, 0), (7, 0, 0, 0)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
