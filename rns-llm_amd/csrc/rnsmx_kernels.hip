@@ -586,14 +586,18 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
     return static_cast<int64_t>((g.m + bm - 1) / bm) * ((g.n + bn - 1) / bn);
   };
   GemmChoice c{};
-  // Stream kernel up to 16 rows; up to 64 unless K > 1024 and its 16 x 16
-  // tiles number 1024 or more (K=4096, N=12288: M=64 45 us with the MFMA
-  // kernel against 79, M=32 39 against 54; N=4096 M=64 28 against 33; at
-  // K=768, N=2304, M=64 the stream kernel's 6.9 against 8.7); up to 128 while its 32 x 16 tiles
+  // Stream kernel up to 16 rows; up to 64 while its 16 x 16 tiles number
+  // under 1024 (K=4096, N=12288: M=64 45 us with the MFMA kernel against 79,
+  // M=32 39 against 54; N=4096 M=64 28 against 33; K=768 N=8192 M=32 9.3
+  // against 11.0; at K=768, N=2304, M=64 the stream kernel's 6.9 against
+  // 8.7); up to 128 while its 32 x 16 tiles
   // number at most 512 (M=128: N=2304 8.8 us with the MFMA kernel against
   // 9.6, N=4608 10.3 against 14.0, K=4096 N=12288 62 against 110; at
   // N=768, 192 tiles, 5.1 against 7.4; at M=96, N=2304, 432 tiles, 7.6
-  // against 8.7).
+  // against 8.7); up to 192 at K <= 2048 while its 16 x 16 tiles number at
+  // most 768 (N=768: K=768 M=160 6.4 against 7.5, M=192 7.1 against 7.6;
+  // K=2048 M=192 11.0 against 12.1; at K=4096 the MFMA kernel's K split
+  // wins, 15.6 against 17.1).
   // Residue-plane activations (int16 / int32 inputs) make every stream wave
   // load each channel's A fragment as well (as many bytes as the weight
   // residues at M <= 16, against one shared fragment for raw int8), and
@@ -606,11 +610,11 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   // against 13.8 (4 channels), M=64 18.9 MFMA against 24.1, M=96 19.0
   // against 30.8.  Raw int8, 6 channels, K=4096: N=12288 M=1/16 58/58
   // MFMA against 67/72, N=4096 M=1/32 27/30 stream against 35/39.
-  const bool long_k = nk > 16;
   const bool plane_rule = !packed && (!araw || rcap > 4);
   const bool stream = plane_rule ? g.m <= 48 && tiles(32, 64) < 128
-                                 : g.m <= 16 || (g.m <= 64 && !(long_k && tiles(16, 16) >= 1024)) ||
-                                       (g.m > 64 && g.m <= 128 && tiles(32, 16) <= 512);
+                                 : g.m <= 16 || (g.m <= 64 && tiles(16, 16) < 1024) ||
+                                       (g.m > 64 && g.m <= 128 && tiles(32, 16) <= 512) ||
+                                       (g.m > 128 && g.m <= 192 && nk <= 32 && tiles(16, 16) <= 768);
   if (stream) {
     // 16-row tiles up to 64 rows, and beyond while they number at most 768
     // (raw int8, K=768: N=768 M=96 5.95 us against 6.73 with 32-row tiles,
@@ -623,7 +627,11 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
     // trips to memory.  With residue planes the A fragments share the
     // registers and the 7-step chunks measured slower (K=4096, N=4096, 4
     // channels, M=1: 25.7 against 20.9 us with chunks of 4).
-    const bool wide = araw && c.mb == 1 && rcap <= 4 && nk >= 64;
+    // From K = 2048 too, up to 32 rows and 384 tiles (N=768 M=1/8/32
+    // 6.25/6.67/7.28 us against 7.18/7.53/7.80 with chunks of 4; N=3072 M=1
+    // 8.00 against 9.09; N=8192, 512 tiles, 23.2 against 16.5).
+    const bool wide = araw && c.mb == 1 && rcap <= 4 &&
+                      (nk >= 64 || (nk >= 32 && g.m <= 32 && tiles(16, 16) <= 384));
     c.kind = wide ? kStreamWide : kStream;
     const int u = stream_u_of(rcap, araw, c.mb, c.nb, wide ? 8 : 4);
     c.ks = std::min(stream_ks_cap(rcap, c.mb, c.nb), std::max(1, (nk + u - 1) / u));
@@ -656,20 +664,30 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
     const int64_t last_cost = last == 0 ? 0 : (tail_split && last <= 128 && nk >= 32) ? 70 : 100;
     return (t / 256 * 100 + last_cost) * per_round;
   };
-  const bool wide = t96 >= 256 && lds_cost(t96, 138, false) < lds_cost(t64, 100, true);
+  const bool wide = lds_cost(t96, 138, false) < lds_cost(t64, 100, true);
   const int64_t lds_tiles = wide ? t96 : t64;
   const int64_t rounds = (lds_tiles + 255) / 256;
   const bool full_rounds = 8 * lds_tiles >= 7 * 256 * rounds;
   c.splits = 1;
-  // At K = 4096 the 256 x 64 tiles win from 128 rows once they number 192
-  // (three quarters of a round), their long K loop reusing each weight
-  // column over 256 rows however many are padding (N=12288: M=128 48.8 us
-  // against 62.5 with 64 x 64 MFMA tiles, M=192 53.2 against 80.7, M=256
-  // 54.8 against 78.5; N=4096, 64 tiles, 46.3 against 31.9; K=2048 N=8192
-  // M=128, 128 tiles, 26.1 against 21.5).
-  const bool lds_long = g.m >= 128 && lds_tiles >= 192 && nk >= 64 && nk < 128;
+  // One round of LDS tiles runs in about the same time however many of the
+  // 256 CUs it fills (256 x 64: 18.5 us at K=768, 28.5 at K=2048, 45 at
+  // K=4096), and from 144 tiles (over half a round) that beats the MFMA
+  // tiles at every K measured, from 192 rows (128 at K >= 4096, where each
+  // weight column's reuse over 256 rows pays however many are padding):
+  // K=768 N=4608 M=512 (144 tiles) 19.1 against 21.5, N=3072 M=1024 19.0
+  // against 20.8; K=2048 N=3072 M=768 28.8 against 35.4, N=768 M=3072
+  // 28.8 against 35.1; K=4096 N=12288 M=128 48.8 against 62.5, M=192 53.2
+  // against 80.7; with 96 tiles or fewer the MFMA tiles win (K=4096
+  // N=3072 M=384 34.0 against 44.6; N=4096 M=256, 64 tiles, 31.9 against
+  // 46.3; at K=4096 128 tiles win too: N=8192 M=192 48.2 against 55.6).
+  // The 256 x 96 tile takes one round where the 256 x 64 one needs a
+  // second (K=768 M=1536 N=3072: 192 wide tiles 25.3 us against 29.9 on
+  // MFMA tiles; K=2048 43.1 against 59.2 with 288 narrow tiles, the tail
+  // split; K=4096 70.7 against 87.6).
+  const bool one_round = lds_tiles >= (nk >= 64 ? 128 : 144) && lds_tiles <= 256 && nk < 128 &&
+                         (g.m >= 192 || (g.m >= 128 && nk >= 64));
   if (lds_kernel_fits(g, araw, rcap) &&
-      ((g.m > 128 && lds_tiles >= 256 && (g.kp >= 2048 || full_rounds)) || lds_long)) {
+      ((g.m > 128 && t64 >= 256 && (g.kp >= 2048 || full_rounds)) || one_round)) {
     c.kind = wide ? kLdsWide : kLds;
     return c;
   }
@@ -721,7 +739,9 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   // choice that fits one round of 256 workgroups with the most of them wins
   // (C2 M=128 32 x 48, 192 tiles, 8.3 us against 8.8 with 32 x 64; N=1536
   // M=256 8.5 against 9.0; K=1024 N=3072 M=256 64 x 48, 12.9 against 13.5),
-  // then the taller, then the wider tile.  48 x 48 and 64 x 48 never beat
+  // past one round the one whose last round is fuller (K=768 N=3072 M=384:
+  // 48 x 48, 512 tiles, 12.4 against 14.0 with 384 of 48 x 64; N=768
+  // M=1536 12.1 against 13.2), then the taller, then the wider tile.  48 x 48 and 64 x 48 never beat
   // 48 x 64 on the headline (10.9 against 9.9 us).  At K = 2048-4096 the
   // same tie-break gains 2-10 % (K=4096: N=12288 M=48 40.2 us against 41.0,
   // M=64 43.2 against 46.4; N=4096 M=64 25.6 against 28.1; N=6144 M=64
@@ -740,7 +760,8 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
       const int64_t t = tiles(16 * mb, 16 * w);
       if (t > 512) continue;
       const int64_t rows = (t + 255) / 256 * (16 * mb);
-      const int64_t fill = t <= 256 ? t : 0;  // workgroups of a single round
+      // a single round first (by its workgroups), then the fuller last round
+      const int64_t fill = t <= 256 ? 256 + t : t - (t - 1) / 256 * 256;
       const bool better = best_rows < 0 || rows < best_rows ||
                           (rows == best_rows && fill > best_fill) ||
                           (rows == best_rows && fill == best_fill && mb > c.mb);
@@ -749,6 +770,32 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
         best_fill = fill;
         c.mb = mb;
         best_w = w;
+      }
+    }
+  }
+  // From K = 2048, where that choice needs more than one round of 256, the
+  // rows per CU mislead (the small MFMA workgroups run several to a CU):
+  // there a grid of at most 320 tiles wins, else the one closest to 512
+  // (K=4096 N=3072 M=384: 64 x 64, 288 tiles, 34.0 us against 44.5 with
+  // 384 tiles of 48 x 64 and 39.7 with 512 of 48 x 48; N=768 M=1536 33.6
+  // against 42.6; K=2048 N=3072 M=512: 64 x 48, 512 tiles, 27.0 against
+  // 29.2 with 384 of 64 x 64).
+  if (nk >= 32 && best_rows >= 0 && tiles(16 * c.mb, 16 * best_w) > 256) {
+    int64_t pick = -1;
+    for (int w = 4; w >= 3; --w) {
+      if (w == 3 && !(araw && rcap <= 4)) continue;
+      for (int mb = 4; mb >= 2; --mb) {
+        if (mb == 3 && rcap > 4) continue;
+        if (w == 3 && !(nk < 128 && tiles(16 * mb, 64) >= 128)) continue;
+        const int64_t t = tiles(16 * mb, 16 * w);
+        if (t > 512) continue;
+        // class 0 (at most 320 tiles) before class 1, then the most tiles
+        const int64_t score = (t <= 320 ? 1024 : 0) + t;
+        if (score > pick) {
+          pick = score;
+          c.mb = mb;
+          best_w = w;
+        }
       }
     }
   }

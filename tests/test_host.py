@@ -73,7 +73,8 @@ PLANS = [
     ((4096, 2304, 768, 4), (2, 4, 1, 0, 1, 0)),    # C4 QKV: over 512 tiles at every height
     ((1, 12288, 4096, 4), (4, 1, 1, 4, 1, 0)),     # C5 decode: stream with 8-step chunks
     ((16, 12288, 4096, 4), (4, 1, 1, 4, 1, 0)),    # long K, 16 rows: stream, 8-step chunks
-    ((16, 2048, 2048, 4), (1, 1, 1, 4, 1, 0)),     # K = 2048: 4-step chunks
+    ((16, 2048, 2048, 4), (4, 1, 1, 4, 1, 0)),     # K = 2048, up to 32 rows: 8-step chunks
+    ((48, 2048, 2048, 4), (1, 1, 1, 4, 1, 0)),     # past 32 rows: 4-step chunks
     ((1, 12288, 4096, 6), (2, 2, 1, 4, 1, 0)),     # no 8-step chunks past 4 channels: 192 MFMA tiles
     ((1, 4096, 4096, 6), (1, 1, 1, 4, 1, 0)),      # 64 MFMA tiles: stream, 4-step chunks
     ((48, 2304, 768, 6), (1, 1, 1, 4, 1, 0)),
@@ -97,7 +98,7 @@ PLANS = [
     # K split over workgroups: few tiles and long K
     ((1, 768, 16384, 4), (4, 1, 1, 1, 8, 0)),    # decode: 8 one-wave workgroups per 16 x 16 tile
     ((1, 768, 4096, 4), (4, 1, 1, 1, 4, 0)),     # 16 K steps per split: 4 splits
-    ((1, 768, 2048, 4), (1, 1, 1, 4, 1, 0)),     # 2 one-wave splits lose to 4 waves in one workgroup
+    ((1, 768, 2048, 4), (4, 1, 1, 4, 1, 0)),     # 4 waves of 8-step chunks (2 one-wave splits lose)
     ((1, 2304, 16384, 4), (4, 1, 1, 4, 1, 0)),   # 144 stream tiles: no split
     ((256, 256, 8192, 4), (2, 2, 1, 4, 8, 0)),   # 32 tiles: 8 splits (256 workgroups)
     ((256, 768, 4096, 4), (2, 2, 1, 4, 4, 0)),   # 96 tiles: at most 512 workgroups -> 4
@@ -109,7 +110,18 @@ PLANS = [
     ((512, 12288, 1024, 4), (7, 0, 0, 0, 1, 0)),    # short K: LDS only for full rounds (256 x 96: one)
     ((384, 12288, 1024, 4), (7, 0, 0, 0, 1, 0)),    # 2 x 128 tiles of 256 x 96 (the second row half padding)
     ((384, 12288, 768, 4), (7, 0, 0, 0, 1, 0)),
-    ((256, 12288, 1024, 4), (2, 4, 1, 0, 1, 0)),    # 128 tiles of 256 x 96: MFMA
+    ((256, 12288, 1024, 4), (3, 0, 0, 0, 1, 0)),    # 192 tiles of 256 x 64: one round from 144
+    ((256, 8192, 1024, 4), (2, 4, 1, 0, 1, 0)),     # 128 of them: MFMA
+    ((1536, 3072, 768, 4), (7, 0, 0, 0, 1, 0)),     # 192 wide tiles, one round (288 narrow: two)
+    ((512, 4608, 768, 4), (3, 0, 0, 0, 1, 0)),      # 144 tiles at K = 768
+    ((384, 3072, 4096, 4), (2, 4, 1, 0, 1, 0)),     # 288 MFMA tiles beat 384 of 48 rows at long K
+    ((512, 3072, 2048, 4), (5, 4, 1, 4, 1, 0)),     # none under 320: the most up to 512
+    ((192, 768, 768, 4), (1, 1, 1, 4, 1, 0)),       # stream up to 192 rows at short K, 576 tiles
+    ((192, 768, 4096, 4), (2, 2, 1, 4, 4, 0)),      # at K = 4096 the MFMA kernel's K split
+    ((384, 3072, 768, 4), (5, 3, 1, 4, 1, 0)),      # rows tie (96 per CU): the fuller last round, 512 tiles
+    ((32, 8192, 768, 4), (5, 2, 1, 4, 1, 0)),       # 1024 stream tiles at short K too: MFMA
+    ((1, 8192, 2048, 4), (1, 1, 1, 4, 1, 0)),       # K = 2048, 512 tiles: 4-step chunks
+    ((192, 8192, 4096, 4), (3, 0, 0, 0, 1, 0)),     # K = 4096: one LDS round from 128 tiles
 ]
 
 
