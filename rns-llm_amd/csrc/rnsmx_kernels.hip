@@ -609,8 +609,10 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   // against 105; K=768, N=2304: M=16 12.6 stream against 17.2, M=48 12.5
   // against 13.8 (4 channels), M=64 18.9 MFMA against 24.1, M=96 19.0
   // against 30.8.  Raw int8, 6 channels, K=4096: N=12288 M=1/16 58/58
-  // MFMA against 67/72, N=4096 M=1/32 27/30 stream against 35/39.
-  const bool plane_rule = !packed && (!araw || rcap > 4);
+  // MFMA against 67/72, N=4096 M=1/32 27/30 stream against 35/39.  Packed
+  // weights (their stream kernel loads 2R activation planes per step) take
+  // the same rule: K=768 N=2304 M=96 29.6 us on MFMA tiles against 40.7.
+  const bool plane_rule = packed || !araw || rcap > 4;
   const bool stream = plane_rule ? g.m <= 48 && tiles(32, 64) < 128
                                  : g.m <= 16 || (g.m <= 64 && tiles(16, 16) < 1024) ||
                                        (g.m > 64 && g.m <= 128 && tiles(32, 16) <= 512) ||
@@ -699,8 +701,11 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   // N=12288 472 against 886; K = 768, N = 2304: M=4096 81 against 108, but
   // M=256 (36 tiles, 12 steps) 28.5 against 19.6, so not there).
   // From 48 rows too: K=4096 N=12288 M=48, 6 channels, 90.8 us with K in
-  // two halves against 103 on 32-row MFMA tiles.
-  if (g.m >= 48 && lds_planes_fits(g, araw, rcap) && tiles(kPlBM, kPlBN) * nk >= 4096) {
+  // two halves against 103 on 32-row MFMA tiles; and from 128 tiles at any
+  // K (K=768 N=2304 M=1024, 144 tiles: 44.7 against 86.1 with 6 channels,
+  // 32.9 against 42.5 with 4).
+  if (g.m >= 48 && lds_planes_fits(g, araw, rcap) &&
+      (tiles(kPlBM, kPlBN) * nk >= 4096 || tiles(kPlBM, kPlBN) >= 128)) {
     c.kind = kLdsPlanes;
     return c;
   }
@@ -714,10 +719,11 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   }
   // Residue-plane activations stage R A planes per K step (raw int8 one),
   // so their bytes grow with the tile height: 32-row tiles up to three
-  // rounds of them, whatever the rows per CU (6 channels, K=768 N=2304:
-  // M=256 27.2 us against 32.6 with 64-row tiles, M=512 39.1 against 56.6;
-  // 4 channels K=4096 N=4096 M=64 43.6 against 58.6).
-  if (!araw && tiles(32, 64) <= 768) {
+  // rounds of them with 6 channels, one with 4, whatever the rows per CU (6
+  // channels, K=768 N=2304: M=256 27.2 us against 32.6 with 64-row tiles,
+  // M=512 39.1 against 56.6; 4 channels K=4096 N=4096 M=64 43.6 against
+  // 58.6, but K=768 N=2304 M=256, 288 tiles, 23.2 against 21.7).
+  if (!araw && tiles(32, 64) <= (rcap >= 6 ? 768 : 256)) {
     c.mb = 2;
     if (rcap <= 6) c.ks = 4;
     return c;
@@ -1060,7 +1066,7 @@ static GemmChoice packed_auto(const GemmArgs &g) {
   // the residue-plane LDS kernel with two units per channel (a' x hi, a x
   // lo) under the rule and split of residue-plane weights
   const int64_t pl_tiles = static_cast<int64_t>((g.m + kPlBM - 1) / kPlBM) * ((g.n + kPlBN - 1) / kPlBN);
-  if (g.m >= 64 && lds_planes_fits(g, false, rcap) && pl_tiles * (g.kp / 64) >= 4096) {
+  if (g.m >= 64 && lds_planes_fits(g, false, rcap) && (pl_tiles * (g.kp / 64) >= 4096 || pl_tiles >= 128)) {
     const int64_t tiles = pl_tiles;
     GemmChoice t{kLdsPlanes, 0, 0, 0, 1, tiles >= 256};
     t.splits = choose_splits(t, g);
@@ -1070,7 +1076,9 @@ static GemmChoice packed_auto(const GemmArgs &g) {
   c.nb = 1;
   if (c.kind == kStream || c.kind == kStreamWide) {
     c.kind = kStream;
-    c.mb = std::min(c.mb, 2);
+    // past 16 rows 32-row tiles: the 2R activation planes of a step serve
+    // twice the rows (K=4096 N=4096 M=32, 6 channels: 64.0 us against 83.8)
+    c.mb = g.m > 16 ? 2 : 1;
     const int u = stream_u_of(rcap, false, c.mb, 1, 4, true);
     c.ks = std::min(stream_ks_cap(rcap, c.mb, 1), std::max(1, (g.kp / 64 + u - 1) / u));
     return c;

@@ -294,17 +294,18 @@ PACKED_PLANS = [
     ((5, 768, 768, 6), (6, 4, 1, 3, 1, 0)),      # four blocks, chunks of 4 steps
     ((9, 768, 768, 4), (6, 4, 1, 3, 1, 0)),
     ((16, 12288, 4096, 6), (6, 8, 1, 4, 1, 0)),  # eight blocks, chunks of 2 steps
-    ((17, 768, 768, 6), (1, 1, 1, 4, 1, 0)),     # past eight blocks: stream, chunks of 3 steps
-    ((33, 768, 768, 4), (1, 1, 1, 3, 1, 0)),     # 4 channels: chunks of 4 steps, 3 waves
+    ((17, 768, 768, 6), (1, 2, 1, 4, 1, 0)),     # past eight blocks: stream, 32-row tiles
+    ((33, 768, 768, 4), (1, 2, 1, 4, 1, 0)),     # 4 channels, 12 MFMA tiles: stream
     ((1, 768, 50_000, 6), (1, 1, 1, 4, 1, 0)),   # K past the channel-row sums' int32 range
-    ((96, 2304, 768, 6), (1, 2, 1, 4, 1, 0)),    # 432 stream tiles of 32 x 16
+    ((96, 2304, 768, 6), (2, 2, 1, 0, 1, 0)),    # past 48 rows: MFMA tiles
     ((100, 2304, 768, 6), (2, 2, 1, 0, 1, 0)),   # MFMA: 144 tiles of 32 rows beat 72 of 64
     ((256, 2304, 768, 6), (2, 2, 1, 0, 1, 0)),   # a tie in rows per CU (288 tiles of 32 rows, 144 of 64): 32
     ((1024, 4096, 1100, 6), (2, 4, 1, 0, 1, 0)),  # 256 rows per CU either way: 64 (K not 256-aligned)
     ((1024, 4096, 1024, 6), (8, 0, 0, 0, 1, 0)),  # residue-plane LDS kernel: 256 tiles of 128 x 128
     ((512, 12288, 4096, 6), (8, 0, 0, 0, 2, 1)),  # 384 tiles: the last 128 split K in two
     ((1024, 4096, 1000, 4), (8, 0, 0, 0, 1, 0)),  # K = 1000 padded to 1024
-    ((1024, 2048, 1024, 6), (2, 4, 1, 0, 1, 0)),  # 128 tiles x 16 K steps: too little work, MFMA kernel
+    ((1024, 2048, 1024, 6), (8, 0, 0, 0, 1, 0)),  # 128 tiles of 128 x 128: the residue-plane LDS kernel
+    ((512, 2048, 1024, 6), (2, 2, 1, 0, 1, 0)),   # 64 of them, 16 K steps: MFMA kernel
     ((512, 4096, 4096, 6), (8, 0, 0, 0, 2, 0)),   # 128 tiles, 64 K steps: every tile in two
 ]
 
