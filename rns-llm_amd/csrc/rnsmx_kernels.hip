@@ -600,24 +600,29 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   // wins, 15.6 against 17.1).
   // Residue-plane activations (int16 / int32 inputs) make every stream wave
   // load each channel's A fragment as well (as many bytes as the weight
-  // residues at M <= 16, against one shared fragment for raw int8), and
-  // past 4 channels the stream kernel has no 8-step chunks; there it pays
-  // only up to 48 rows while the MFMA kernel's 32 x 64 tiles number under
-  // 128.  Residue planes, K=4096, 6 channels: N=12288 M=1/16 65/68 us with
+  // residues at M <= 16, against one shared fragment for raw int8); there
+  // the stream kernel pays only up to 48 rows while the MFMA kernel's 32 x
+  // 64 tiles number under 128.  Residue planes, K=4096, 6 channels: N=12288 M=1/16 65/68 us with
   // the MFMA kernel against 81/98, N=8192 M=16 60 against 70, N=4096 M=16
   // 39 with the stream kernel against 54, M=64 60 with the MFMA kernel
   // against 105; K=768, N=2304: M=16 12.6 stream against 17.2, M=48 12.5
   // against 13.8 (4 channels), M=64 18.9 MFMA against 24.1, M=96 19.0
-  // against 30.8.  Raw int8, 6 channels, K=4096: N=12288 M=1/16 58/58
-  // MFMA against 67/72, N=4096 M=1/32 27/30 stream against 35/39.  Packed
+  // against 30.8.  Packed
   // weights (their stream kernel loads 2R activation planes per step) take
   // the same rule: K=768 N=2304 M=96 29.6 us on MFMA tiles against 40.7.
-  const bool plane_rule = packed || !araw || rcap > 4;
+  const bool plane_rule = packed || !araw;
   const bool stream = plane_rule ? g.m <= 48 && tiles(32, 64) < 128
                                  : g.m <= 16 || (g.m <= 64 && tiles(16, 16) < 1024) ||
                                        (g.m > 64 && g.m <= 128 && tiles(32, 16) <= 512) ||
                                        (g.m > 128 && g.m <= 192 && nk <= 32 && tiles(16, 16) <= 768);
-  if (stream) {
+  // Raw int8 past 4 channels has no 8-step chunks: where they would be used
+  // (K >= 4096) the MFMA kernel's 32 x 64 tiles win from 128 of them (6
+  // channels, K=4096: N=12288 M=1/16 58 us against 67/72, N=8192 M=1 43.6
+  // against 46.8), elsewhere the raw rule holds (N=768 M=96 7.3 against 11.3
+  // at K=768, 17.2 against 33.4 at K=4096; K=768 N=8192 M=1 10.6 against
+  // 12.3).
+  const bool no_chunks = araw && rcap > 4 && nk >= 64 && tiles(32, 64) >= 128;
+  if (stream && !no_chunks) {
     // 16-row tiles up to 64 rows, and beyond while they number at most 768
     // (raw int8, K=768: N=768 M=96 5.95 us against 6.73 with 32-row tiles,
     // M=128 6.35 against 6.87; N=2304 M=80 7.77 against 8.27; at M=96,

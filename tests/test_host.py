@@ -79,7 +79,10 @@ PLANS = [
     ((1, 4096, 4096, 6), (1, 1, 1, 4, 1, 0)),      # 64 MFMA tiles: stream, 4-step chunks
     ((48, 2304, 768, 6), (1, 1, 1, 4, 1, 0)),
     ((64, 4096, 4096, 6), (2, 2, 1, 4, 1, 0)),     # past 48 rows
-    ((96, 48, 64, 10), (2, 2, 1, 0, 1, 0)),        # 10 channels: the tile's default ring (3 steps)
+    ((224, 2304, 768, 10), (2, 2, 1, 0, 1, 0)),    # 10 channels: the tile's default ring (3 steps)
+    ((96, 48, 64, 10), (1, 1, 1, 4, 1, 0)),        # raw int8 past 4 channels: the raw stream rule
+    ((96, 768, 768, 6), (1, 1, 1, 4, 1, 0)),
+    ((32, 12288, 4096, 6), (2, 2, 1, 4, 1, 0)),    # no 8-step chunks past 4 channels: MFMA from 128 tiles
     ((256, 2304, 768, 10), (2, 4, 1, 0, 1, 0)),
     ((32, 12288, 4096, 4), (5, 2, 1, 4, 1, 0)),    # long K, wide N: MFMA, 32 rows, three waves (256 tiles)
     ((48, 12288, 4096, 4), (5, 3, 1, 4, 1, 0)),
