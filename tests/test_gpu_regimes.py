@@ -7,7 +7,9 @@ product:
   * config C5 at its full shape (M = 1 and 2048, K = 4096, N = 12288), every
     row, fixed and adaptive;
   * the device-side prefix choosing 5 and 6 channels (int16 sources, the
-    6-channel dense set, min_channels = 3)."""
+    6-channel dense set, min_channels = 3);
+  * the automatic plan at shapes where the kernel-choice rules switch
+    family, against another kernel and sampled exact rows."""
 import numpy as np
 import pytest
 import torch
@@ -141,3 +143,44 @@ def test_device_prefix_picks_five_and_six_channels(backend, expect, b_max, m):
     assert c == expect
     assert dict(meta) == {"channels": c, "bound": bound, "capacity": cap}
     np.testing.assert_array_equal(out.cpu().numpy(), ro.exact_matmul(a.numpy(), b.numpy()))
+
+
+# (M, K, N, channels, int16 activations?, kernel kind the automatic plan picks)
+AUTO_SHAPES = [
+    (1536, 768, 3072, 4, False, 7),   # one round of 256 x 96 tiles where 256 x 64 needs two
+    (512, 768, 4608, 4, False, 3),    # one round of 144 LDS tiles at K = 768
+    (192, 768, 768, 4, False, 1),     # the stream kernel up to 192 rows
+    (8, 2048, 768, 4, False, 4),      # 8-step chunks from K = 2048
+    (384, 4096, 3072, 4, False, 2),   # 288 MFMA tiles past one round at long K
+    (384, 768, 3072, 4, False, 5),    # the fuller last round on a rows tie
+    (96, 768, 768, 6, False, 1),      # raw int8 past 4 channels: the raw stream rule
+    (1024, 768, 2304, 6, True, 8),    # residue planes: the LDS kernel from 128 tiles
+]
+
+
+@pytest.mark.parametrize("m,k,n,channels,wide,kind", AUTO_SHAPES,
+                         ids=lambda v: str(v) if not isinstance(v, bool) else ("int16" if v else "int8"))
+def test_automatic_plan_at_rule_boundaries(backend, m, k, n, channels, wide, kind):
+    """The automatic plan at shapes where the kernel-choice rules switch
+    family: the kind the host query reports runs, its output equals the
+    32 x 64 MFMA kernel's bit for bit, and sampled rows equal the exact
+    product."""
+    import ctypes
+
+    from rns_llm_amd import _native
+
+    mods = DENSE4 if channels == 4 else DENSE6
+    plan = _native.Plan()
+    _native.check(_native.lib().rnsmx_gemm_plan(m, n, k, channels, 0 if wide else 1, ctypes.byref(plan)))
+    assert plan.kind == kind
+    gen = torch.Generator().manual_seed(m + k + n + channels)
+    lo, hi, dt = (-32767, 32768, torch.int16) if wide else (-127, 128, torch.int8)
+    a = torch.randint(lo, hi, (m, k), generator=gen, dtype=torch.int32).to(dt)
+    b = torch.randint(lo, hi, (k, n), generator=gen, dtype=torch.int32).to(dt)
+    prepared = backend.prepare_weight(b.to(DEV), mods)
+    out = backend.matmul_prepared_fused(a.to(DEV), prepared)
+    other = backend.matmul_prepared_fused(a.to(DEV), prepared, plan=(2, 2, 1, 0))
+    assert torch.equal(out, other)
+    rows = torch.randperm(m, generator=gen)[:24]
+    want = ro.exact_matmul(a[rows].numpy(), b.numpy())
+    np.testing.assert_array_equal(out.cpu()[rows].numpy(), want)
