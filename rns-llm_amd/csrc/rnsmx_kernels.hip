@@ -590,11 +590,10 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   // under 1024 (K=4096, N=12288: M=64 45 us with the MFMA kernel against 79,
   // M=32 39 against 54; N=4096 M=64 28 against 33; K=768 N=8192 M=32 9.3
   // against 11.0; at K=768, N=2304, M=64 the stream kernel's 6.9 against
-  // 8.7); up to 128 while its 32 x 16 tiles
-  // number at most 512 (M=128: N=2304 8.8 us with the MFMA kernel against
-  // 9.6, N=4608 10.3 against 14.0, K=4096 N=12288 62 against 110; at
-  // N=768, 192 tiles, 5.1 against 7.4; at M=96, N=2304, 432 tiles, 7.6
-  // against 8.7); up to 192 at K <= 2048 while its 16 x 16 tiles number at
+  // 8.7); up to 128 while its 32 x 16 tiles number at most 512 (M=128:
+  // N=2304 8.8 us with the MFMA kernel against 9.6, N=4608 10.3 against
+  // 14.0, K=4096 N=12288 62 against 110; at N=768, 192 tiles, 5.1 against
+  // 7.4; at M=96, N=2304, 432 tiles, 7.6 against 8.7); up to 192 at K <= 2048 while its 16 x 16 tiles number at
   // most 768 (N=768: K=768 M=160 6.4 against 7.5, M=192 7.1 against 7.6;
   // K=2048 M=192 11.0 against 12.1; at K=4096 the MFMA kernel's K split
   // wins, 15.6 against 17.1).
@@ -602,14 +601,14 @@ static GemmChoice choose_gemm(const GemmArgs &g, bool araw, bool packed = false)
   // load each channel's A fragment as well (as many bytes as the weight
   // residues at M <= 16, against one shared fragment for raw int8); there
   // the stream kernel pays only up to 48 rows while the MFMA kernel's 32 x
-  // 64 tiles number under 128.  Residue planes, K=4096, 6 channels: N=12288 M=1/16 65/68 us with
-  // the MFMA kernel against 81/98, N=8192 M=16 60 against 70, N=4096 M=16
-  // 39 with the stream kernel against 54, M=64 60 with the MFMA kernel
+  // 64 tiles number under 128 (K=4096, 6 channels: N=12288 M=1/16 65/68 us
+  // with the MFMA kernel against 81/98, N=8192 M=16 60 against 70, N=4096
+  // M=16 39 with the stream kernel against 54, M=64 60 with the MFMA kernel
   // against 105; K=768, N=2304: M=16 12.6 stream against 17.2, M=48 12.5
-  // against 13.8 (4 channels), M=64 18.9 MFMA against 24.1, M=96 19.0
-  // against 30.8.  Packed
-  // weights (their stream kernel loads 2R activation planes per step) take
-  // the same rule: K=768 N=2304 M=96 29.6 us on MFMA tiles against 40.7.
+  // against 13.8 with 4 channels, M=64 18.9 MFMA against 24.1, M=96 19.0
+  // against 30.8).  Packed weights, whose stream kernel loads 2R activation
+  // planes per step, take the same rule (K=768 N=2304 M=96 29.6 us on MFMA
+  // tiles against 40.7).
   const bool plane_rule = packed || !araw;
   const bool stream = plane_rule ? g.m <= 48 && tiles(32, 64) < 128
                                  : g.m <= 16 || (g.m <= 64 && tiles(16, 16) < 1024) ||
