@@ -9,7 +9,9 @@ product:
   * the device-side prefix choosing 5 and 6 channels (int16 sources, the
     6-channel dense set, min_channels = 3);
   * the automatic plan at shapes where the kernel-choice rules switch
-    family, against another kernel and sampled exact rows."""
+    family, against another kernel and sampled exact rows;
+  * the residue-plane MFMA kernel on both sides of its single-row-tile
+    instantiation (streaming weight loads), every row exact."""
 import numpy as np
 import pytest
 import torch
@@ -184,3 +186,24 @@ def test_automatic_plan_at_rule_boundaries(backend, m, k, n, channels, wide, kin
     rows = torch.randperm(m, generator=gen)[:24]
     want = ro.exact_matmul(a[rows].numpy(), b.numpy())
     np.testing.assert_array_equal(out.cpu()[rows].numpy(), want)
+
+
+
+@pytest.mark.parametrize("m,mb", [(1, 2), (32, 2), (33, 2), (1, 4), (17, 4), (64, 4), (65, 4)])
+@pytest.mark.parametrize("channels", [4, 6])
+def test_residue_plane_mfma_single_and_several_row_tiles(backend, m, mb, channels):
+    """The residue-plane MFMA kernel loads its weights with the streaming
+    hint when one row tile covers M (a separate instantiation) and with
+    plain loads otherwise: both sides of that switch, at a ragged K and N
+    (padding steps and a partial last column tile), equal the exact product
+    on every row (int16 operands; within +-255 for 4 channels, whose range
+    holds K * 255^2)."""
+    mods = DENSE4 if channels == 4 else DENSE6
+    lim = 256 if channels == 4 else 32768
+    k, n = 1000, 1000
+    gen = torch.Generator().manual_seed(m * 7 + mb + channels)
+    a = torch.randint(1 - lim, lim, (m, k), generator=gen, dtype=torch.int32).to(torch.int16)
+    b = torch.randint(1 - lim, lim, (k, n), generator=gen, dtype=torch.int32).to(torch.int16)
+    prepared = backend.prepare_weight(b.to(DEV), mods)
+    out = backend.matmul_prepared_fused(a.to(DEV), prepared, plan=(2, mb, 1, 0))
+    np.testing.assert_array_equal(out.cpu().numpy(), ro.exact_matmul(a.numpy(), b.numpy()))
