@@ -282,8 +282,13 @@ __global__ __launch_bounds__(256) void encode_frag_kernel(const EncodeArgs e) {
 // [block][a' | a][kp/64][1 KB] MFMA A fragments in which row t * rpt + c of
 // block b holds token b * (16 / rpt) + t, channel c (a' = centered residue
 // of d_c a, d_c = 256 mod m_c); rows past the tokens or the channels and K
-// past cols are zero.  One wave per fragment: lane l writes row l & 15, K
-// bytes 64 ks + 16 (l >> 4) .. +16.
+// past cols are zero.  Lane l of a fragment holds row l & 15, K bytes
+// 64 ks + 16 (l >> 4) .. +16.  One thread per 4-byte word (word w of a
+// fragment: lane w >> 2, bytes 4 (w & 3) of that lane's 16), so each
+// thread forms 4 residues (8 with a'): the encode is one short dependent
+// launch before the GEMM, whose latency is what counts; 16 values per lane
+// (one wave per fragment) made the packed decode step ~1 us slower (M=1,
+// K=4096, N=12288: 23.5 against 22.6 us).
 struct TokenRowsArgs {
   const void *values;
   int64_t m, cols, nk, blocks;  // blocks: the GEMM's (blocks past the tokens are zero)
@@ -293,41 +298,56 @@ struct TokenRowsArgs {
 };
 
 template <typename T>
+__device__ __forceinline__ void load4(const T *p, int32_t (&v)[4]) {
+  if constexpr (sizeof(T) == 1) {
+    const uint32_t w = *reinterpret_cast<const uint32_t *>(p);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = static_cast<int8_t>((w >> (8 * q)) & 0xFFu);
+  } else if constexpr (sizeof(T) == 2) {
+    const uint2 w = *reinterpret_cast<const uint2 *>(p);
+    v[0] = static_cast<int16_t>(w.x & 0xFFFFu);
+    v[1] = static_cast<int16_t>(w.x >> 16);
+    v[2] = static_cast<int16_t>(w.y & 0xFFFFu);
+    v[3] = static_cast<int16_t>(w.y >> 16);
+  } else {
+    const i32x4 w = *reinterpret_cast<const i32x4 *>(p);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = w[q];
+  }
+}
+
+template <typename T>
 __global__ __launch_bounds__(256) void encode_token_rows_kernel(const TokenRowsArgs e) {
-  const int lane = threadIdx.x & 63;
-  const int tpb = 16 / e.rpt;
-  const int64_t f = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t word = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t f = word >> 8;  // 1 KB fragment: 256 words
   if (f >= e.blocks * 2 * e.nk) return;
+  const int w = static_cast<int>(word & 255), lane = w >> 2;
+  const int tpb = 16 / e.rpt;
   const int64_t ks = f % e.nk, b = f / (2 * e.nk);
   const bool scaled = (f / e.nk) % 2 == 0;  // a' fragments first
   const int r = lane & 15, t = r / e.rpt, c = r % e.rpt;
-  const int64_t token = b * tpb + t, k0 = ks * 64 + (lane >> 4) * 16;
-  i32x4 w = {0, 0, 0, 0};
+  const int64_t token = b * tpb + t, k0 = ks * 64 + (lane >> 4) * 16 + 4 * (w & 3);
+  uint32_t packed = 0;
   if (t < tpb && token < e.m && c < e.mods.channels) {
     const T *src = static_cast<const T *>(e.values) + token * e.cols;
-    int32_t v[16];
-    if (e.cols % 16 == 0 && k0 + 16 <= e.cols) {
-      load16<T>(src + k0, v);
+    int32_t v[4];
+    if (e.cols % 16 == 0 && k0 + 4 <= e.cols) {
+      load4<T>(src + k0, v);
     } else {
 #pragma unroll
-      for (int q = 0; q < 16; ++q) v[q] = (k0 + q < e.cols) ? static_cast<int32_t>(src[k0 + q]) : 0;
+      for (int q = 0; q < 4; ++q) v[q] = (k0 + q < e.cols) ? static_cast<int32_t>(src[k0 + q]) : 0;
     }
     const uint32_t m = static_cast<uint32_t>(e.mods.moduli[c]);
     const uint32_t magic = e.mods.magic[c], c31 = e.mods.c31[c];
     const int32_t d = static_cast<int32_t>(256u % m);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      uint32_t packed = 0;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        int32_t x = centered_i32(v[4 * g + q], m, magic, c31);
-        if (scaled) x = centered_i32(d * x, m, magic, c31);
-        packed |= (static_cast<uint32_t>(x) & 0xFFu) << (8 * q);
-      }
-      w[g] = static_cast<int32_t>(packed);
+    for (int q = 0; q < 4; ++q) {
+      int32_t x = centered_i32(v[q], m, magic, c31);
+      if (scaled) x = centered_i32(d * x, m, magic, c31);
+      packed |= (static_cast<uint32_t>(x) & 0xFFu) << (8 * q);
     }
   }
-  *reinterpret_cast<i32x4 *>(e.out + f * 1024 + lane * 16) = w;
+  reinterpret_cast<uint32_t *>(e.out)[word] = packed;
 }
 
 // Packed weight preparation: int8/int16 [N][K] -> two byte planes in the
@@ -1659,8 +1679,8 @@ static int32_t run_prepared(const void *a_dev, int32_t a_dtype, int32_t m, int32
     t.blocks = c.mb;
     t.out = a_res;
     t.mods = *mods;
-    const int64_t frags = t.blocks * 2 * t.nk;
-    const dim3 grid(static_cast<unsigned>((frags + 3) / 4)), block(256);
+    const int64_t frags = t.blocks * 2 * t.nk;  // one workgroup per 1 KB fragment
+    const dim3 grid(static_cast<unsigned>(frags)), block(256);
     switch (a_dtype) {
       case RNSMX_INT8: hipLaunchKernelGGL(encode_token_rows_kernel<int8_t>, grid, block, 0, st, t); break;
       case RNSMX_INT16: hipLaunchKernelGGL(encode_token_rows_kernel<int16_t>, grid, block, 0, st, t); break;
