@@ -278,25 +278,6 @@ __global__ __launch_bounds__(256) void encode_frag_kernel(const EncodeArgs e) {
   }
 }
 
-// Activations for rows_packed_kernel (packed weights at decode):
-// [block][a' | a][kp/64][1 KB] MFMA A fragments in which row t * rpt + c of
-// block b holds token b * (16 / rpt) + t, channel c (a' = centered residue
-// of d_c a, d_c = 256 mod m_c); rows past the tokens or the channels and K
-// past cols are zero.  Lane l of a fragment holds row l & 15, K bytes
-// 64 ks + 16 (l >> 4) .. +16.  One thread per 4-byte word (word w of a
-// fragment: lane w >> 2, bytes 4 (w & 3) of that lane's 16), so each
-// thread forms 4 residues (8 with a'): the encode is one short dependent
-// launch before the GEMM, whose latency is what counts; 16 values per lane
-// (one wave per fragment) made the packed decode step ~1 us slower (M=1,
-// K=4096, N=12288: 23.5 against 22.6 us).
-struct TokenRowsArgs {
-  const void *values;
-  int64_t m, cols, nk, blocks;  // blocks: the GEMM's (blocks past the tokens are zero)
-  int32_t rpt;                  // rows per token: the kernel's channel capacity
-  int8_t *out;
-  rnsmx_moduli_t mods;
-};
-
 template <typename T>
 __device__ __forceinline__ void load4(const T *p, int32_t (&v)[4]) {
   if constexpr (sizeof(T) == 1) {
@@ -315,6 +296,52 @@ __device__ __forceinline__ void load4(const T *p, int32_t (&v)[4]) {
     for (int q = 0; q < 4; ++q) v[q] = w[q];
   }
 }
+
+// Residue planes of a few rows (no row norm, no max |v|, no packed planes):
+// one thread per 4 K values, grid (row, channel, K / 1024), so a short
+// batch's encode is spread over many workgroups (its latency, not its
+// bytes, is what the step pays).  Int16, 6 channels, K=4096, N=12288: M=16
+// 60.1-60.9 against 61.3-61.5 us per step; M=1 and 4 within noise.
+template <typename T>
+__global__ __launch_bounds__(256) void encode_rows_split_kernel(const EncodeArgs e) {
+  const int64_t row = blockIdx.x;
+  const int c = static_cast<int>(blockIdx.y);
+  const int64_t k0 = (static_cast<int64_t>(blockIdx.z) * 256 + threadIdx.x) * 4;
+  if (k0 >= e.out_ld) return;
+  const T *src = static_cast<const T *>(e.values) + row * e.cols;
+  int32_t v[4];
+  if (e.cols % 16 == 0 && k0 + 4 <= e.cols) {
+    load4<T>(src + k0, v);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = (k0 + q < e.cols) ? static_cast<int32_t>(src[k0 + q]) : 0;
+  }
+  const uint32_t m = static_cast<uint32_t>(e.mods.moduli[c]);
+  const uint32_t magic = e.mods.magic[c], c31 = e.mods.c31[c];
+  uint32_t packed = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) packed |= (static_cast<uint32_t>(centered_i32(v[q], m, magic, c31)) & 0xFFu) << (8 * q);
+  *reinterpret_cast<uint32_t *>(e.out + c * e.plane + row * e.out_ld + k0) = packed;
+}
+
+// Activations for rows_packed_kernel (packed weights at decode):
+// [block][a' | a][kp/64][1 KB] MFMA A fragments in which row t * rpt + c of
+// block b holds token b * (16 / rpt) + t, channel c (a' = centered residue
+// of d_c a, d_c = 256 mod m_c); rows past the tokens or the channels and K
+// past cols are zero.  Lane l of a fragment holds row l & 15, K bytes
+// 64 ks + 16 (l >> 4) .. +16.  One thread per 4-byte word (word w of a
+// fragment: lane w >> 2, bytes 4 (w & 3) of that lane's 16), so each
+// thread forms 4 residues (8 with a'): the encode is one short dependent
+// launch before the GEMM, whose latency is what counts; 16 values per lane
+// (one wave per fragment) made the packed decode step ~1 us slower (M=1,
+// K=4096, N=12288: 23.5 against 22.6 us).
+struct TokenRowsArgs {
+  const void *values;
+  int64_t m, cols, nk, blocks;  // blocks: the GEMM's (blocks past the tokens are zero)
+  int32_t rpt;                  // rows per token: the kernel's channel capacity
+  int8_t *out;
+  rnsmx_moduli_t mods;
+};
 
 template <typename T>
 __global__ __launch_bounds__(256) void encode_token_rows_kernel(const TokenRowsArgs e) {
@@ -1040,8 +1067,22 @@ static int32_t launch_gemm(GemmArgs g, bool araw, const GemmChoice &c, uint32_t 
 // Activation encoder launch: one workgroup per (row, channel), or per row
 // for the row L1 alone (e.out null), with a thread per 16 K values up to
 // 256 threads (one pass up to K = 4096).
+// Up to this many rows the plain residue-plane encode runs split over K.
+static constexpr int64_t kEncodeSplitRows = 16;
+
 static int32_t launch_encode_rows(int32_t dtype, const EncodeArgs &e, hipStream_t st, bool packed = false) {
   if (e.rows == 0) return RNSMX_OK;
+  if (!packed && e.out != nullptr && e.row_l1 == nullptr && e.absmax == nullptr && e.rows <= kEncodeSplitRows) {
+    const dim3 grid(static_cast<unsigned>(e.rows), static_cast<unsigned>(e.mods.channels),
+                    static_cast<unsigned>((e.out_ld + 1023) / 1024));
+    switch (dtype) {
+      case RNSMX_INT8: hipLaunchKernelGGL(encode_rows_split_kernel<int8_t>, grid, dim3(256), 0, st, e); break;
+      case RNSMX_INT16: hipLaunchKernelGGL(encode_rows_split_kernel<int16_t>, grid, dim3(256), 0, st, e); break;
+      case RNSMX_INT32: hipLaunchKernelGGL(encode_rows_split_kernel<int32_t>, grid, dim3(256), 0, st, e); break;
+      default: return fail(RNSMX_EINVAL, "encoder supports int8, int16 and int32");
+    }
+    return check_launch("encode_rows_split");
+  }
   const int64_t chunks = (e.out_ld + 15) / 16;
   const unsigned threads = static_cast<unsigned>(std::min<int64_t>(256, (chunks + 63) / 64 * 64));
   const dim3 grid(static_cast<unsigned>(e.rows), e.out != nullptr ? static_cast<unsigned>(e.mods.channels) : 1u);
