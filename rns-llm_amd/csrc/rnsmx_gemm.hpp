@@ -1420,7 +1420,12 @@ __global__ __launch_bounds__(256) void rows_packed_kernel(const GemmArgsK<RCAP> 
   prefetch_kernel_args<kGemmHotArgBytes>();
   static_assert(RCAP == 4 || RCAP == 6, "4 or 6 channel rows per token");
   constexpr int TPB = 16 / RCAP;                                   // tokens per 16-row block
-  constexpr int U = NBLK == 1 ? 8 : NBLK == 2 ? 6 : NBLK == 4 ? 4 : 2;  // K steps per chunk
+  // K steps per chunk: the most that keep 3 waves per SIMD (all 768
+  // workgroups of N=12288 in one round) up to 4 blocks (2 blocks with 6
+  // steps: 204 VGPRs, M=4 37.1 against 35.4 us; 4 blocks with 4: 272, M=8
+  // 46.1 against 42.8); 8 blocks keep 2 steps at one wave per SIMD (one step
+  // at two waves measured slower, M=16 74.4 against 69.3 us)
+  constexpr int U = NBLK == 1 ? 8 : NBLK == 2 ? 4 : 2;
   __shared__ __attribute__((aligned(16))) int32_t sums[NBLK][16][16];
   __shared__ int64_t red[4];
   __shared__ int bcast;

@@ -1114,7 +1114,7 @@ static int32_t launch_encode_rows(int32_t dtype, const EncodeArgs &e, hipStream_
 static constexpr int kRowsMaxKp = 44032;
 static constexpr int kRowsMaxBlocks = 8;
 
-static int rows_steps_of(int nblk) { return nblk == 1 ? 8 : nblk == 2 ? 6 : nblk == 4 ? 4 : 2; }
+static int rows_steps_of(int nblk) { return nblk == 1 ? 8 : nblk == 2 ? 4 : 2; }
 
 static GemmChoice packed_auto(const GemmArgs &g) {
   const int rcap = g.mods.channels <= 4 ? 4 : 6;

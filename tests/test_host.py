@@ -292,10 +292,10 @@ PACKED_PLANS = [
     ((1, 12288, 4096, 6), (6, 1, 1, 4, 1, 0)),   # decode: channel rows, chunks of 8 steps, 4 waves
     ((1, 768, 768, 6), (6, 1, 1, 2, 1, 0)),
     ((2, 768, 768, 6), (6, 1, 1, 2, 1, 0)),      # 2 tokens x 6 channel rows in one block
-    ((3, 768, 768, 6), (6, 2, 1, 2, 1, 0)),      # two blocks, chunks of 6 steps
-    ((8, 768, 768, 4), (6, 2, 1, 2, 1, 0)),      # 4 tokens x 4 channel rows per block
-    ((5, 768, 768, 6), (6, 4, 1, 3, 1, 0)),      # four blocks, chunks of 4 steps
-    ((9, 768, 768, 4), (6, 4, 1, 3, 1, 0)),
+    ((3, 768, 768, 6), (6, 2, 1, 3, 1, 0)),      # two blocks, chunks of 4 steps
+    ((8, 768, 768, 4), (6, 2, 1, 3, 1, 0)),      # 4 tokens x 4 channel rows per block
+    ((5, 768, 768, 6), (6, 4, 1, 4, 1, 0)),      # four blocks, chunks of 2 steps
+    ((9, 768, 768, 4), (6, 4, 1, 4, 1, 0)),
     ((16, 12288, 4096, 6), (6, 8, 1, 4, 1, 0)),  # eight blocks, chunks of 2 steps
     ((17, 768, 768, 6), (1, 2, 1, 4, 1, 0)),     # past eight blocks: stream, 32-row tiles
     ((33, 768, 768, 4), (1, 2, 1, 4, 1, 0)),     # 4 channels, 12 MFMA tiles: stream
