@@ -184,7 +184,7 @@ __global__ __launch_bounds__(256) void row_l1_max_kernel(const EncodeArgs e) {
   for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * 4 + wv; r0 < e.rows; r0 += 2 * stride) {
     const int64_t r1 = r0 + stride;
     const bool two = r1 < e.rows;
-    int32_t sum0 = 0, sum1 = 0;  // |a| <= 128 and K < 2^24: no overflow
+    uint32_t sum0 = 0, sum1 = 0;  // |a| <= 128 and K < 2^24: no overflow
     for (int64_t k0 = lane * 16; k0 < e.cols; k0 += 64 * 16 * kChunks) {
       i32x4 w0[kChunks], w1[kChunks];
       static_for<kChunks>([&](auto J) {
@@ -199,16 +199,11 @@ __global__ __launch_bounds__(256) void row_l1_max_kernel(const EncodeArgs e) {
       });
       static_for<kChunks>([&](auto J) {
         constexpr int j = decltype(J)::value;
-        static_for<16>([&](auto Q) {
-          constexpr int q = decltype(Q)::value;
-          const int32_t b0 = static_cast<int8_t>((static_cast<uint32_t>(w0[j][q >> 2]) >> (8 * (q & 3))) & 0xFFu);
-          const int32_t b1 = static_cast<int8_t>((static_cast<uint32_t>(w1[j][q >> 2]) >> (8 * (q & 3))) & 0xFFu);
-          sum0 += b0 < 0 ? -b0 : b0;
-          sum1 += b1 < 0 ? -b1 : b1;
-        });
+        sum0 = abs_sum_i8x16(w0[j], sum0);
+        sum1 = abs_sum_i8x16(w1[j], sum1);
       });
     }
-    const int64_t row0 = wave_sum_i64(sum0), row1 = wave_sum_i64(sum1);
+    const int64_t row0 = wave_sum_i64(static_cast<int64_t>(sum0)), row1 = wave_sum_i64(static_cast<int64_t>(sum1));
     best = row0 > best ? row0 : best;
     best = row1 > best ? row1 : best;
   }
