@@ -168,6 +168,22 @@ def test_packed_channel_rows_exact(backend, moduli, m, ks, a_dtype):
         assert torch.equal(out.cpu(), exact(a.to(torch.int32), w))
 
 
+@pytest.mark.parametrize("moduli,m", [(DENSE6, 1), (DENSE6, 3), (DENSE6, 16), (DENSE4, 5)],
+                         ids=lambda v: str(len(v)) if isinstance(v, tuple) else str(v))
+@pytest.mark.parametrize("a_dtype", [torch.int8, torch.int16, torch.int32])
+def test_packed_channel_rows_whole_vectors(backend, moduli, m, a_dtype):
+    """K a multiple of 16: the activation encode takes its vector loads (4
+    values per thread, int8 / int16 / int32), and every row equals the exact
+    product."""
+    k, n = 1024, 130
+    a_lim = 127 if len(moduli) == 4 or a_dtype == torch.int8 else 32767
+    a = ints((m, k), -a_lim, a_lim, m * 5 + k, a_dtype)
+    w = ints((n, k), -32768, 32767, 13 * len(moduli) + m)
+    prepared = backend.prepare_weight_packed_nk(w.to(DEV), moduli)
+    out = backend.matmul_prepared_fused(a.to(DEV), prepared)
+    assert torch.equal(out.cpu(), exact(a.to(torch.int32), w))
+
+
 @pytest.mark.parametrize("m", [1, 4])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_packed_channel_rows_float_epilogue(backend, m, out_dtype):

@@ -207,3 +207,18 @@ def test_residue_plane_mfma_single_and_several_row_tiles(backend, m, mb, channel
     prepared = backend.prepare_weight(b.to(DEV), mods)
     out = backend.matmul_prepared_fused(a.to(DEV), prepared, plan=(2, mb, 1, 0))
     np.testing.assert_array_equal(out.cpu().numpy(), ro.exact_matmul(a.numpy(), b.numpy()))
+
+
+@pytest.mark.parametrize("k", [1000, 1024])
+@pytest.mark.parametrize("a_dtype", [torch.int16, torch.int32])
+@pytest.mark.parametrize("m", [1, 16, 17])
+def test_few_row_residue_plane_encode(backend, k, a_dtype, m):
+    """Up to 16 rows the residue-plane encode runs split over K (one thread
+    per 4 values; 17 rows take the per-row encoder): vector and ragged K,
+    int16 and int32 activations, every row exact."""
+    gen = torch.Generator().manual_seed(k + m)
+    a = torch.randint(-32767, 32768, (m, k), generator=gen, dtype=torch.int32).to(a_dtype)
+    b = torch.randint(-32767, 32768, (k, 200), generator=gen, dtype=torch.int32).to(torch.int16)
+    prepared = backend.prepare_weight(b.to(DEV), DENSE6)
+    out = backend.matmul_prepared_fused(a.to(DEV), prepared)
+    np.testing.assert_array_equal(out.cpu().numpy(), ro.exact_matmul(a.to(torch.int32).numpy(), b.numpy()))
