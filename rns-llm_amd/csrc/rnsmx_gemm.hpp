@@ -1461,50 +1461,70 @@ __global__ __launch_bounds__(256) void rows_packed_kernel(const GemmArgsK<RCAP> 
     rowv[b] = (lane & 15) < min(TPB, max(0, g.m - b * TPB)) * RCAP;
   });
   i32x4 fh[U], fl[U], fa2[U][NBLK], fa[U][NBLK];
-  auto load_chunk = [&](int q) {
+  // loads and MFMAs of the chunk's steps [P0, P1)
+  auto load_part = [&](int q, auto P0, auto P1) {
     static_for<U>([&](auto UU) {
       constexpr int u = decltype(UU)::value;
-      const int ks = min(q + u, nk - 1);
-      const bool live = q + u < nk;  // steps past K: zero activations
-      fh[u] = load16_nt(bp + ks * 1024);
-      fl[u] = load16_nt(bp + g.b_cs + ks * 1024);
-      static_for<NBLK>([&](auto B) {
-        constexpr int b = decltype(B)::value;
-        if constexpr (NBLK == 2) {
-          fa2[u][b] = select16(live, load16(ap + b * g.a_cs + ks * 1024));
-          fa[u][b] = select16(live, load16(ap + b * g.a_cs + mstride + ks * 1024));
-        } else {
-          i32x4 x2 = {0, 0, 0, 0}, x = {0, 0, 0, 0};
-          if (live && rowv[b]) {
-            x2 = load16(ap + b * g.a_cs + ks * 1024);
-            x = load16(ap + b * g.a_cs + mstride + ks * 1024);
+      if constexpr (u >= decltype(P0)::value && u < decltype(P1)::value) {
+        const int ks = min(q + u, nk - 1);
+        const bool live = q + u < nk;  // steps past K: zero activations
+        fh[u] = load16_nt(bp + ks * 1024);
+        fl[u] = load16_nt(bp + g.b_cs + ks * 1024);
+        static_for<NBLK>([&](auto B) {
+          constexpr int b = decltype(B)::value;
+          if constexpr (NBLK == 2) {
+            fa2[u][b] = select16(live, load16(ap + b * g.a_cs + ks * 1024));
+            fa[u][b] = select16(live, load16(ap + b * g.a_cs + mstride + ks * 1024));
+          } else {
+            i32x4 x2 = {0, 0, 0, 0}, x = {0, 0, 0, 0};
+            if (live && rowv[b]) {
+              x2 = load16(ap + b * g.a_cs + ks * 1024);
+              x = load16(ap + b * g.a_cs + mstride + ks * 1024);
+            }
+            fa2[u][b] = x2;
+            fa[u][b] = x;
           }
-          fa2[u][b] = x2;
-          fa[u][b] = x;
-        }
-      });
+        });
+      }
     });
   };
-  auto mfma_chunk = [&]() {
+  auto mfma_part = [&](auto P0, auto P1) {
     static_for<U>([&](auto UU) {
       constexpr int u = decltype(UU)::value;
-      static_for<NBLK>([&](auto B) {
-        constexpr int b = decltype(B)::value;
-        acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa2[u][b], fh[u], acc[b], 0, 0, 0);
-        acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][b], fl[u], acc[b], 0, 0, 0);
-        rsum[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][b], ones, rsum[b], 0, 0, 0);
-      });
+      if constexpr (u >= decltype(P0)::value && u < decltype(P1)::value) {
+        static_for<NBLK>([&](auto B) {
+          constexpr int b = decltype(B)::value;
+          acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa2[u][b], fh[u], acc[b], 0, 0, 0);
+          acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][b], fl[u], acc[b], 0, 0, 0);
+          rsum[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][b], ones, rsum[b], 0, 0, 0);
+        });
+      }
     });
   };
-  load_chunk(wave * U);
+  // Two halves of the register chunk in turn: the next chunk's first half
+  // is loaded while the second half's MFMAs wait, so each wave keeps loads
+  // in flight across its chunks (loads complete in order: the MFMAs of a
+  // half wait only for that half).
+  constexpr std::integral_constant<int, 0> h0{};
+  constexpr std::integral_constant<int, U / 2> h1{};
+  constexpr std::integral_constant<int, U> h2{};
+  int q = wave * U;
+  load_part(q, h0, h1);
+  load_part(q, h1, h2);
   Epi<RCAP> e;
   load_epi<RCAP>(g, e, c_act);
   pin_epi<RCAP>(e);
   for (int i = threadIdx.x; i < NBLK * 256; i += nthreads) (&sums[0][0][0])[i] = 0;
-  if (wave * U < nk) mfma_chunk();
-  for (int q = wave * U + ks_n * U; q < nk; q += ks_n * U) {
-    load_chunk(q);
-    mfma_chunk();
+  if (q < nk) {
+    for (;;) {
+      const int qn = q + ks_n * U;
+      mfma_part(h0, h1);
+      if (qn < nk) load_part(qn, h0, h1);
+      mfma_part(h1, h2);
+      if (qn >= nk) break;
+      load_part(qn, h1, h2);
+      q = qn;
+    }
   }
   __syncthreads();
   // channel sums of every element: a' hi + a lo + 128 sum_k a
