@@ -1194,59 +1194,66 @@ __device__ __forceinline__ void stream_main(KArgs<RCAP> &g, const int c_act) {
   });
 
   i32x4 fa[U][AP][MB], fb[U][BP][NB];
-  auto load_chunk = [&](int q) {
+  // loads and MFMAs of the chunk's steps [P0, P1)
+  auto load_part = [&](int q, auto P0, auto P1) {
     static_for<U>([&](auto UU) {
       constexpr int u = decltype(UU)::value;
-      const int ks = min(q + u, nk - 1);
-      const int ka = ks * 64 + kofs;
-      const bool av = (q + u < nk) && (ka < a_k);
-      const int kac = min(ka, a_k - 16);
-      static_for<APE>([&](auto PP) {
-        constexpr int p = decltype(PP)::value;
-        static_for<MB>([&](auto I) {
-          constexpr int i = decltype(I)::value;
-          fa[u][p][i] = select16(av, load16(ap[i] + aoff[p] + kac));
-        });
-      });
-      static_for<BPE>([&](auto C) {
-        constexpr int c = decltype(C)::value;
-        static_for<NB>([&](auto J) {
-          constexpr int j = decltype(J)::value;
-          // the 8-step chunks serve decode over a long K (a few 16-row
-          // tiles): weights loaded with the streaming hint (C5 M=1: 34.3
-          // against 38.1 us; neutral at 2-4 row tiles)
-          fb[u][c][j] = UCAP == 8 ? load16_nt(bp[j] + boff[c] + ks * 1024) : load16(bp[j] + boff[c] + ks * 1024);
-        });
-      });
-    });
-  };
-  auto mfma_chunk = [&]() {
-    static_for<U>([&](auto UU) {
-      constexpr int u = decltype(UU)::value;
-      // every computed channel, with no branch (with CA = RCAP, channels
-      // past the prefix read channel 0's plane; their sums are dropped by
-      // the epilogue)
-      static_for<CA>([&](auto C) {
-        constexpr int c = decltype(C)::value;
-        static_for<MB>([&](auto I) {
-          constexpr int i = decltype(I)::value;
-          static_for<NB>([&](auto J) {
-            constexpr int j = decltype(J)::value;
-            if constexpr (PK) {
-              // a' x hi + a x lo: the channel's residue of the weight, formed by the MFMAs
-              acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][RCAP + c][i], fb[u][0][j],
-                                                                   acc[c][i][j], 0, 0, 0);
-              acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][c][i], fb[u][1][j],
-                                                                   acc[c][i][j], 0, 0, 0);
-            } else {
-              acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][ARAW ? 0 : c][i], fb[u][c][j],
-                                                                   acc[c][i][j], 0, 0, 0);
-            }
+      if constexpr (u >= decltype(P0)::value && u < decltype(P1)::value) {
+        const int ks = min(q + u, nk - 1);
+        const int ka = ks * 64 + kofs;
+        const bool av = (q + u < nk) && (ka < a_k);
+        const int kac = min(ka, a_k - 16);
+        static_for<APE>([&](auto PP) {
+          constexpr int p = decltype(PP)::value;
+          static_for<MB>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            fa[u][p][i] = select16(av, load16(ap[i] + aoff[p] + kac));
           });
         });
-      });
+        static_for<BPE>([&](auto C) {
+          constexpr int c = decltype(C)::value;
+          static_for<NB>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            // the 8-step chunks serve decode over a long K (a few 16-row
+            // tiles): weights loaded with the streaming hint (C5 M=1: 34.3
+            // against 38.1 us; neutral at 2-4 row tiles)
+            fb[u][c][j] = UCAP == 8 ? load16_nt(bp[j] + boff[c] + ks * 1024) : load16(bp[j] + boff[c] + ks * 1024);
+          });
+        });
+      }
     });
   };
+  auto load_chunk = [&](int q) { load_part(q, std::integral_constant<int, 0>{}, std::integral_constant<int, U>{}); };
+  auto mfma_part = [&](auto P0, auto P1) {
+    static_for<U>([&](auto UU) {
+      constexpr int u = decltype(UU)::value;
+      if constexpr (u >= decltype(P0)::value && u < decltype(P1)::value) {
+        // every computed channel, with no branch (with CA = RCAP, channels
+        // past the prefix read channel 0's plane; their sums are dropped by
+        // the epilogue)
+        static_for<CA>([&](auto C) {
+          constexpr int c = decltype(C)::value;
+          static_for<MB>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            static_for<NB>([&](auto J) {
+              constexpr int j = decltype(J)::value;
+              if constexpr (PK) {
+                // a' x hi + a x lo: the channel's residue of the weight, formed by the MFMAs
+                acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][RCAP + c][i], fb[u][0][j],
+                                                                     acc[c][i][j], 0, 0, 0);
+                acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][c][i], fb[u][1][j],
+                                                                     acc[c][i][j], 0, 0, 0);
+              } else {
+                acc[c][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[u][ARAW ? 0 : c][i], fb[u][c][j],
+                                                                     acc[c][i][j], 0, 0, 0);
+              }
+            });
+          });
+        });
+      }
+    });
+  };
+  auto mfma_chunk = [&]() { mfma_part(std::integral_constant<int, 0>{}, std::integral_constant<int, U>{}); };
 
   // first chunk in flight before the epilogue constants are waited for
   load_chunk(wave * U);
@@ -1269,10 +1276,30 @@ __device__ __forceinline__ void stream_main(KArgs<RCAP> &g, const int c_act) {
   });
   // the column of a thread that finishes one element (few rows, below)
   const ColScale cs1 = col_scale<RCAP>(e, n0 + threadIdx.x % BN, n_lim);
-  if (wave * U < nk) mfma_chunk();
-  for (int q = wave * U + ks_n * U; q < nk; q += ks_n * U) {
-    load_chunk(q);
-    mfma_chunk();
+  if constexpr (U == 8) {
+    // long K: the two halves of the chunk in turn, the next chunk's first
+    // half loaded while the second half's MFMAs wait for their loads
+    constexpr std::integral_constant<int, 0> h0{};
+    constexpr std::integral_constant<int, U / 2> h1{};
+    constexpr std::integral_constant<int, U> h2{};
+    int q = wave * U;
+    if (q < nk) {
+      for (;;) {
+        const int qn = q + ks_n * U;
+        mfma_part(h0, h1);
+        if (qn < nk) load_part(qn, h0, h1);
+        mfma_part(h1, h2);
+        if (qn >= nk) break;
+        load_part(qn, h1, h2);
+        q = qn;
+      }
+    }
+  } else {
+    if (wave * U < nk) mfma_chunk();
+    for (int q = wave * U + ks_n * U; q < nk; q += ks_n * U) {
+      load_chunk(q);
+      mfma_chunk();
+    }
   }
   // packed weights: the per-row term, once per tile (wave 0 of the whole K
   // or of its first split)
