@@ -11,7 +11,9 @@ product:
   * the automatic plan at shapes where the kernel-choice rules switch
     family, against another kernel and sampled exact rows;
   * the residue-plane MFMA kernel on both sides of its single-row-tile
-    instantiation (streaming weight loads), every row exact."""
+    instantiation (streaming weight loads), every row exact;
+  * the few-row residue-plane encode and the decode kernels' chunk halves
+    with partial last chunks."""
 import numpy as np
 import pytest
 import torch
@@ -222,3 +224,26 @@ def test_few_row_residue_plane_encode(backend, k, a_dtype, m):
     prepared = backend.prepare_weight(b.to(DEV), DENSE6)
     out = backend.matmul_prepared_fused(a.to(DEV), prepared)
     np.testing.assert_array_equal(out.cpu().numpy(), ro.exact_matmul(a.to(torch.int32).numpy(), b.numpy()))
+
+
+@pytest.mark.parametrize("k", [4288, 2131])
+@pytest.mark.parametrize("ks", [1, 2, 3, 4])
+@pytest.mark.parametrize("m", [1, 5])
+def test_long_k_chunk_halves_partial_chunks(backend, k, ks, m):
+    """The 8-step stream chunks and the channel-row kernel walk the halves of
+    each chunk in turn; with K = 67 (or a ragged 34) steps of 64 the last
+    chunk of a wave is partly or wholly past K.  Raw int8 through the stream
+    plan and int16 through packed weights, every row exact."""
+    gen = torch.Generator().manual_seed(k * 10 + ks + m)
+    a = torch.randint(-127, 128, (m, k), generator=gen, dtype=torch.int32).to(torch.int8)
+    b = torch.randint(-127, 128, (k, 300), generator=gen, dtype=torch.int32).to(torch.int8)
+    prepared = backend.prepare_weight(b.to(DEV), DENSE4)
+    out = backend.matmul_prepared_fused(a.to(DEV), prepared, plan=(4, 1, 1, ks))
+    np.testing.assert_array_equal(out.cpu().numpy(), ro.exact_matmul(a.to(torch.int32).numpy(), b.numpy()))
+    a16 = torch.randint(-32767, 32768, (m, k), generator=gen, dtype=torch.int32).to(torch.int16)
+    w16 = torch.randint(-32767, 32768, (300, k), generator=gen, dtype=torch.int32).to(torch.int16)
+    packed = backend.prepare_weight_packed_nk(w16.to(DEV), DENSE6)
+    blocks = 1 if m <= 2 else 4
+    out16 = backend.matmul_prepared_fused(a16.to(DEV), packed, plan=(6, blocks, 1, ks))
+    np.testing.assert_array_equal(out16.cpu().numpy(),
+                                  ro.exact_matmul(a16.to(torch.int32).numpy(), w16.to(torch.int32).numpy().T))
